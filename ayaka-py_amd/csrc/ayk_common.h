@@ -1,0 +1,172 @@
+// Shared device helpers of libayaka_fp8: number codecs, typed loads/stores,
+// wavefront reductions and the error/launch plumbing of the C ABI.
+//
+// Everything here targets gfx950 (CDNA4): 64-lane wavefronts, OCP fp8 formats.
+#pragma once
+
+#include <hip/hip_runtime.h>
+#include <hip/hip_fp16.h>
+#include <stdint.h>
+#include <string.h>
+
+#include "ayaka_fp8.h"
+
+namespace ayk {
+
+constexpr float kE4M3Max = 448.0f;
+constexpr int kWave = 64;
+
+// ------------------------------------------------------------------ bit casts
+__host__ __device__ inline uint32_t f2u(float f) {
+#if defined(__HIP_DEVICE_COMPILE__)
+  return __float_as_uint(f);
+#else
+  uint32_t u;
+  memcpy(&u, &f, 4);
+  return u;
+#endif
+}
+__host__ __device__ inline float u2f(uint32_t u) {
+#if defined(__HIP_DEVICE_COMPILE__)
+  return __uint_as_float(u);
+#else
+  float f;
+  memcpy(&f, &u, 4);
+  return f;
+#endif
+}
+
+// --------------------------------------------------------------- e4m3fn codec
+// OCP e4m3fn: 1 sign, 4 exponent (bias 7), 3 mantissa bits; no infinities; the
+// all-ones magnitude 0x7F is NaN; largest finite value 448 = 1.75 * 2^8; the
+// subnormal grid is 2^-9. Encoding rounds to nearest, ties to even, and maps NaN
+// and every magnitude that rounds above 448 (>= 464 after the tie rule) to NaN,
+// i.e. the IEEE-style result in a format whose only "overflow" value is NaN.
+__host__ __device__ inline uint8_t e4m3_encode(float v) {
+  const uint32_t bits = f2u(v);
+  const uint8_t sign = (uint8_t)((bits >> 24) & 0x80u);
+  const uint32_t mag = bits & 0x7FFFFFFFu;
+  if (mag >= 0x43F00000u) return sign | 0x7F;  // NaN, inf, >= 480
+  if (mag < 0x3C800000u) {                     // below 2^-6: subnormal range
+    // mag * 2^9 is exact; rounding it to an integer in [0, 8] is the subnormal
+    // code (8 == 2^-6, the smallest normal, whose code is also 8).
+    const float scaled = u2f(mag) * 512.0f;
+    return sign | (uint8_t)rintf(scaled);
+  }
+  // Normal range: keep 3 of the 23 mantissa bits with round-half-even; a carry out
+  // of the mantissa bumps the exponent, which is the correct rounding.
+  const uint32_t lsb = (mag >> 20) & 1u;
+  const uint32_t rounded = (mag + 0x7FFFFu + lsb) >> 20;
+  return sign | (uint8_t)(rounded - ((127u - 7u) << 3));
+}
+
+// Exact decode of one e4m3fn byte (host and device; the device hot loops use the
+// gfx950 hardware converter instead, see e4m3x4_to_f32).
+__host__ __device__ inline float e4m3_decode(uint8_t c) {
+  const uint32_t sign = (uint32_t)(c & 0x80) << 24;
+  const uint32_t e = (c >> 3) & 0xF;
+  const uint32_t m = c & 0x7;
+  if (e == 0xF && m == 0x7) return u2f(sign | 0x7FC00000u);
+  if (e == 0) return u2f(sign | f2u((float)m * (1.0f / 512.0f)));
+  return u2f(sign | ((e + 120u) << 23) | (m << 20));
+}
+
+// UE8M0 exponent code: value 2^(c-127) built as the fp32 bit pattern c << 23, so
+// code 0 is +0.0 and 0xFF is NaN.
+__host__ __device__ inline float e8m0_decode(uint32_t c) {
+  return c == 0xFFu ? u2f(0x7FC00000u) : u2f(c << 23);
+}
+
+// ------------------------------------------------------------------ 16-bit floats
+// fp32 -> bf16, round to nearest even; every NaN becomes the canonical 0x7FC0.
+__host__ __device__ inline uint16_t f32_to_bf16_bits(float f) {
+  const uint32_t u = f2u(f);
+  if ((u & 0x7FFFFFFFu) > 0x7F800000u) return 0x7FC0;
+  return (uint16_t)((u + 0x7FFFu + ((u >> 16) & 1u)) >> 16);
+}
+__host__ __device__ inline float bf16_bits_to_f32(uint32_t b) { return u2f(b << 16); }
+
+__device__ inline float f16_bits_to_f32(uint16_t h) {
+  return __half2float(__ushort_as_half(h));
+}
+__device__ inline uint16_t f32_to_f16_bits(float f) {
+  return __half_as_ushort(__float2half_rn(f));
+}
+
+// Element-type tags used to template kernels on the activation / output type.
+struct F32T { using storage = float; static constexpr int id = AYK_F32; };
+struct F16T { using storage = uint16_t; static constexpr int id = AYK_F16; };
+struct BF16T { using storage = uint16_t; static constexpr int id = AYK_BF16; };
+
+template <typename T>
+__device__ inline float to_f32(typename T::storage v);
+template <>
+__device__ inline float to_f32<F32T>(float v) { return v; }
+template <>
+__device__ inline float to_f32<F16T>(uint16_t v) { return f16_bits_to_f32(v); }
+template <>
+__device__ inline float to_f32<BF16T>(uint16_t v) { return bf16_bits_to_f32(v); }
+
+// Runtime-typed scalar load / store (epilogues, scales, biases).
+__device__ inline float load_f32(const void* p, int dtype, int64_t i) {
+  switch (dtype) {
+    case AYK_F32: return reinterpret_cast<const float*>(p)[i];
+    case AYK_F16: return f16_bits_to_f32(reinterpret_cast<const uint16_t*>(p)[i]);
+    case AYK_BF16: return bf16_bits_to_f32(reinterpret_cast<const uint16_t*>(p)[i]);
+    case AYK_U8: return e8m0_decode(reinterpret_cast<const uint8_t*>(p)[i]);
+    default: return 0.0f;
+  }
+}
+__device__ inline void store_f32(void* p, int dtype, int64_t i, float v) {
+  switch (dtype) {
+    case AYK_F32: reinterpret_cast<float*>(p)[i] = v; break;
+    case AYK_F16: reinterpret_cast<uint16_t*>(p)[i] = f32_to_f16_bits(v); break;
+    case AYK_BF16: reinterpret_cast<uint16_t*>(p)[i] = f32_to_bf16_bits(v); break;
+    default: break;
+  }
+}
+
+// Four e4m3 bytes packed in one dword -> four floats (hardware OCP converter).
+__device__ inline void e4m3x4_to_f32(uint32_t w, float* out) {
+  typedef float v2f __attribute__((ext_vector_type(2)));
+  const v2f lo = __builtin_amdgcn_cvt_pk_f32_fp8((int)w, false);
+  const v2f hi = __builtin_amdgcn_cvt_pk_f32_fp8((int)w, true);
+  out[0] = lo.x;
+  out[1] = lo.y;
+  out[2] = hi.x;
+  out[3] = hi.y;
+}
+
+// NaN-propagating max of magnitudes, the semantics of torch's amax.
+__device__ inline float nanmax(float a, float b) { return (a > b || a != a) ? a : b; }
+
+// Clamp to the finite e4m3 range, keeping NaN (torch.clamp semantics).
+__host__ __device__ inline float clamp_e4m3(float v) {
+  return v > kE4M3Max ? kE4M3Max : (v < -kE4M3Max ? -kE4M3Max : v);
+}
+
+// -------------------------------------------------------------- wave reductions
+template <int WIDTH>
+__device__ inline float wave_max(float v) {
+#pragma unroll
+  for (int off = WIDTH / 2; off > 0; off >>= 1) v = nanmax(v, __shfl_xor(v, off, WIDTH));
+  return v;
+}
+template <int WIDTH>
+__device__ inline float wave_sum(float v) {
+#pragma unroll
+  for (int off = WIDTH / 2; off > 0; off >>= 1) v += __shfl_xor(v, off, WIDTH);
+  return v;
+}
+
+// ---------------------------------------------------------------- misc helpers
+__host__ __device__ constexpr int64_t cdiv(int64_t a, int64_t b) { return (a + b - 1) / b; }
+
+inline bool aligned16(const void* p) { return (reinterpret_cast<uintptr_t>(p) & 15u) == 0; }
+
+// Error state of the C ABI (defined in capi.hip).
+int fail(int status, const char* fmt, ...);
+int check_launch(const char* what);
+int check_device();
+
+}  // namespace ayk

@@ -1,0 +1,374 @@
+// Decode GEMV (M == 1) over an [N, K] e4m3 weight, for gfx950.
+//
+//   out[n] = sum_k w[n, k] * x[k] * wscale(n, k) * ascale(k)  (+ bias[n])
+//
+// Serves three reference operators (python/ayaka/kernel/triton/gemm/fp8_gemv.py):
+//   * fp8_weight_only_gemv (:323): x fp16/bf16, weight scale
+//     scale[(n / by) * stride + k / bx] in UE8M0 / fp32 / bf16, no activation scale;
+//   * fp8_blockwise_gemv (:433): x e4m3 with a per-128 activation scale and a
+//     [N/128, K/128] weight scale, plus bias;
+//   * the M == 1 MXFP8 product (fp8_mxfp8_gemm.py:163 at M == 1): x e4m3 and w e4m3,
+//     each with one UE8M0 code per 32-wide K group.
+//
+// The kernel is HBM-bound: its cost is N * K weight bytes. Each wavefront owns R
+// weight rows and walks K in 1024-byte strides (64 lanes x one 16-byte vector), so
+// every weight load is a fully coalesced 128-bit load and a wave keeps U * R of them
+// in flight per lane. The activation chunk a lane needs is the same for all R rows,
+// so it is loaded once (L1/L2 resident) and reused R times. A K split (grid.y) is
+// used only when N alone cannot fill the 256 CUs; its fp32 partials are summed by a
+// second kernel in a fixed order, so results are deterministic.
+#include "ayk_common.h"
+
+namespace ayk {
+namespace {
+
+constexpr int kGemvThreads = 256;
+constexpr int kGemvWaves = kGemvThreads / kWave;
+constexpr int kChunk = 16;                      // K elements per lane vector
+constexpr int64_t kWaveK = (int64_t)kWave * kChunk;  // K elements per wave sweep
+
+enum ActKind { ACT_BF16 = 0, ACT_F16 = 1, ACT_E4M3 = 2 };
+enum WScaleKind { WS_ROW = 0, WS_CHUNK = 1 };
+enum AScaleKind { AS_NONE = 0, AS_BLOCK128 = 1, AS_MX32 = 2 };
+
+struct GemvArgs {
+  const void* x;
+  const uint8_t* w;
+  int64_t ldw;
+  int64_t N, K;
+  const void* wscale;
+  int wscale_dtype;
+  int64_t srs;  // weight-scale row stride
+  int64_t by, bx;
+  const void* ascale;  // per-128 float scale or per-32 UE8M0 codes of x
+  int ascale_dtype;
+  const void* bias;
+  int bias_dtype;
+  void* out;
+  int out_dtype;
+  float* part;       // [split, N] partials when split > 1
+  int64_t k_per_split;  // multiple of kWaveK
+};
+
+// Load the 16 activation values of chunk `c` (elements 16c .. 16c+15) as floats.
+template <int ACT>
+__device__ inline void load_x_chunk(const void* x, int64_t c, float* f) {
+  if constexpr (ACT == ACT_E4M3) {
+    const uint4 v = reinterpret_cast<const uint4*>(x)[c];
+    e4m3x4_to_f32(v.x, f);
+    e4m3x4_to_f32(v.y, f + 4);
+    e4m3x4_to_f32(v.z, f + 8);
+    e4m3x4_to_f32(v.w, f + 12);
+  } else {
+    const uint4* p = reinterpret_cast<const uint4*>(x) + 2 * c;
+    const uint4 a = p[0], b = p[1];
+    const uint32_t w[8] = {a.x, a.y, a.z, a.w, b.x, b.y, b.z, b.w};
+#pragma unroll
+    for (int i = 0; i < 8; ++i) {
+      if constexpr (ACT == ACT_BF16) {
+        f[2 * i] = u2f(w[i] << 16);
+        f[2 * i + 1] = u2f(w[i] & 0xFFFF0000u);
+      } else {
+        f[2 * i] = f16_bits_to_f32((uint16_t)(w[i] & 0xFFFFu));
+        f[2 * i + 1] = f16_bits_to_f32((uint16_t)(w[i] >> 16));
+      }
+    }
+  }
+}
+
+__device__ inline float dot16(const uint4& wv, const float* xf) {
+  float wf[16];
+  e4m3x4_to_f32(wv.x, wf);
+  e4m3x4_to_f32(wv.y, wf + 4);
+  e4m3x4_to_f32(wv.z, wf + 8);
+  e4m3x4_to_f32(wv.w, wf + 12);
+  float s = 0.0f;
+#pragma unroll
+  for (int i = 0; i < 16; ++i) s = fmaf(wf[i], xf[i], s);
+  return s;
+}
+
+template <int AS>
+__device__ inline float act_scale(const GemvArgs& a, int64_t k0) {
+  if constexpr (AS == AS_BLOCK128) return load_f32(a.ascale, a.ascale_dtype, k0 / 128);
+  else if constexpr (AS == AS_MX32) return e8m0_decode(reinterpret_cast<const uint8_t*>(a.ascale)[k0 / 32]);
+  else return 1.0f;
+}
+
+template <int ACT, int WS, int AS, int R>
+__global__ __launch_bounds__(kGemvThreads) void gemv_kernel(GemvArgs a) {
+  const int lane = threadIdx.x % kWave;
+  const int wave = threadIdx.x / kWave;
+  const int64_t row0 = ((int64_t)blockIdx.x * kGemvWaves + wave) * R;
+  const int64_t kbeg = (int64_t)blockIdx.y * a.k_per_split;
+  const int64_t kend = min(a.K, kbeg + a.k_per_split);
+  int64_t rows[R];
+#pragma unroll
+  for (int r = 0; r < R; ++r) rows[r] = min(row0 + r, a.N - 1);  // clamp: loads stay in bounds
+  float acc[R];
+#pragma unroll
+  for (int r = 0; r < R; ++r) acc[r] = 0.0f;
+
+  // Scale row offsets are computed once; per-chunk column indices use 32-bit math.
+  int64_t sbase[R];
+#pragma unroll
+  for (int r = 0; r < R; ++r) sbase[r] = (rows[r] / a.by) * a.srs;
+  float row_scale[R];
+  if constexpr (WS == WS_ROW) {
+#pragma unroll
+    for (int r = 0; r < R; ++r) row_scale[r] = load_f32(a.wscale, a.wscale_dtype, sbase[r]);
+  }
+  const uint32_t bx = (uint32_t)a.bx;
+
+  for (int64_t k0 = kbeg + (int64_t)lane * kChunk; k0 < kend; k0 += kWaveK) {
+    float xf[16];
+    load_x_chunk<ACT>(a.x, k0 / kChunk, xf);
+    uint4 wv[R];
+#pragma unroll
+    for (int r = 0; r < R; ++r) wv[r] = *reinterpret_cast<const uint4*>(a.w + rows[r] * a.ldw + k0);
+    const float sa = act_scale<AS>(a, k0);
+    const uint32_t kcol = WS == WS_CHUNK ? (uint32_t)k0 / bx : 0u;
+#pragma unroll
+    for (int r = 0; r < R; ++r) {
+      const float d = dot16(wv[r], xf);
+      if constexpr (WS == WS_ROW && AS == AS_NONE) {
+        acc[r] += d;
+      } else if constexpr (WS == WS_ROW) {
+        acc[r] = fmaf(d, sa, acc[r]);
+      } else {
+        const float sw = load_f32(a.wscale, a.wscale_dtype, sbase[r] + kcol);
+        acc[r] = fmaf(d, sw * sa, acc[r]);
+      }
+    }
+  }
+
+#pragma unroll
+  for (int r = 0; r < R; ++r) {
+    float v = wave_sum<kWave>(acc[r]);
+    if constexpr (WS == WS_ROW) v *= row_scale[r];
+    const int64_t n = row0 + r;
+    if (lane == 0 && n < a.N) {
+      if (gridDim.y == 1) {
+        if (a.bias) v += load_f32(a.bias, a.bias_dtype, n);
+        store_f32(a.out, a.out_dtype, n, v);
+      } else {
+        a.part[(int64_t)blockIdx.y * a.N + n] = v;
+      }
+    }
+  }
+}
+
+// Fixed-order sum over the split axis, bias, one rounding to the output dtype.
+__global__ __launch_bounds__(256) void splitk_reduce_kernel(const float* __restrict__ part,
+                                                            int64_t N, int split,
+                                                            const void* bias, int bias_dtype,
+                                                            void* out, int out_dtype) {
+  const int64_t n = (int64_t)blockIdx.x * 256 + threadIdx.x;
+  if (n >= N) return;
+  float v = 0.0f;
+  for (int s = 0; s < split; ++s) v += part[(int64_t)s * N + n];
+  if (bias) v += load_f32(bias, bias_dtype, n);
+  store_f32(out, out_dtype, n, v);
+}
+
+// Generic fallback (any K, stride, alignment or scale block): one wave per output
+// row, element-wise byte loads, per-element scale. Correct everywhere, not fast.
+template <int ACT, int AS>
+__global__ __launch_bounds__(kGemvThreads) void gemv_generic_kernel(GemvArgs a) {
+  const int lane = threadIdx.x % kWave;
+  const int64_t n = (int64_t)blockIdx.x * kGemvWaves + threadIdx.x / kWave;
+  if (n >= a.N) return;
+  const uint8_t* wr = a.w + n * a.ldw;
+  float acc = 0.0f;
+  for (int64_t k = lane; k < a.K; k += kWave) {
+    float xv;
+    if constexpr (ACT == ACT_E4M3) xv = e4m3_decode(reinterpret_cast<const uint8_t*>(a.x)[k]);
+    else if constexpr (ACT == ACT_BF16) xv = bf16_bits_to_f32(reinterpret_cast<const uint16_t*>(a.x)[k]);
+    else xv = f16_bits_to_f32(reinterpret_cast<const uint16_t*>(a.x)[k]);
+    const float sw = load_f32(a.wscale, a.wscale_dtype, (n / a.by) * a.srs + k / a.bx);
+    acc = fmaf(e4m3_decode(wr[k]) * xv, sw * act_scale<AS>(a, k), acc);
+  }
+  acc = wave_sum<kWave>(acc);
+  if (lane == 0) {
+    if (a.bias) acc += load_f32(a.bias, a.bias_dtype, n);
+    store_f32(a.out, a.out_dtype, n, acc);
+  }
+}
+
+constexpr int kRows = 4;  // weight rows per wavefront
+
+// Split plan from shapes only (graph-capture safe): the smallest power-of-two K
+// split that gives >= 2048 row-waves (8 per CU), never splitting below one sweep.
+struct SplitPlan {
+  int split;
+  int64_t k_per_split;
+};
+SplitPlan gemv_split_plan(int64_t N, int64_t K) {
+  const int64_t waves = cdiv(N, kRows);
+  const int64_t sweeps = cdiv(K, kWaveK);
+  int split = 1;
+  while (waves * split < 2048 && split * 2 <= sweeps && split < 64) split *= 2;
+  const int64_t kps = cdiv(sweeps, split) * kWaveK;
+  split = (int)cdiv(K, kps);
+  return {split, kps};
+}
+
+template <int ACT, int WS, int AS>
+void launch_gemv_fast(GemvArgs& a, int split, hipStream_t st) {
+  const dim3 grid((unsigned)cdiv(a.N, (int64_t)kGemvWaves * kRows), (unsigned)split);
+  hipLaunchKernelGGL((gemv_kernel<ACT, WS, AS, kRows>), grid, dim3(kGemvThreads), 0, st, a);
+}
+
+template <int ACT, int AS>
+int run_gemv(GemvArgs a, bool row_scale, size_t ws_bytes, const char* op, hipStream_t st) {
+  const bool fast = aligned16(a.w) && aligned16(a.x) && a.ldw % 16 == 0 && a.K % kChunk == 0 &&
+                    (row_scale || a.bx % kChunk == 0);
+  if (!fast) {
+    const dim3 grid((unsigned)cdiv(a.N, kGemvWaves));
+    hipLaunchKernelGGL((gemv_generic_kernel<ACT, AS>), grid, dim3(kGemvThreads), 0, st, a);
+    return check_launch(op);
+  }
+  const SplitPlan plan = gemv_split_plan(a.N, a.K);
+  a.k_per_split = plan.k_per_split;
+  if (plan.split > 1) {
+    const size_t need = (size_t)plan.split * (size_t)a.N * sizeof(float);
+    if (a.part == nullptr || ws_bytes < need) {
+      return fail(AYK_EWORKSPACE, "%s: workspace of %zu bytes required, %zu given", op, need, ws_bytes);
+    }
+  }
+  if (row_scale) launch_gemv_fast<ACT, WS_ROW, AS>(a, plan.split, st);
+  else launch_gemv_fast<ACT, WS_CHUNK, AS>(a, plan.split, st);
+  if (int rc = check_launch(op)) return rc;
+  if (plan.split > 1) {
+    hipLaunchKernelGGL(splitk_reduce_kernel, dim3((unsigned)cdiv(a.N, 256)), dim3(256), 0, st,
+                       a.part, a.N, plan.split, a.bias, a.bias_dtype, a.out, a.out_dtype);
+    return check_launch(op);
+  }
+  return AYK_OK;
+}
+
+size_t gemv_workspace(int64_t N, int64_t K) {
+  if (N <= 0 || K <= 0) return 0;
+  const SplitPlan plan = gemv_split_plan(N, K);
+  return plan.split > 1 ? (size_t)plan.split * (size_t)N * sizeof(float) : 0;
+}
+
+bool is_float_dtype(int dt) { return dt == AYK_F32 || dt == AYK_F16 || dt == AYK_BF16; }
+
+}  // namespace
+
+// Used by the MXFP8 GEMM entry point for M == 1.
+int mx_gemv(const void* a, const uint8_t* a_scale, const void* w, int64_t ldw,
+            const uint8_t* w_scale, int64_t ld_ws, int64_t N, int64_t K, const void* bias,
+            int bias_dtype, void* out, int out_dtype, hipStream_t st) {
+  GemvArgs g{};
+  g.x = a;
+  g.w = static_cast<const uint8_t*>(w);
+  g.ldw = ldw;
+  g.N = N;
+  g.K = K;
+  g.wscale = w_scale;
+  g.wscale_dtype = AYK_U8;
+  g.srs = ld_ws;
+  g.by = 1;
+  g.bx = 32;
+  g.ascale = a_scale;
+  g.ascale_dtype = AYK_U8;
+  g.bias = bias;
+  g.bias_dtype = bias_dtype;
+  g.out = out;
+  g.out_dtype = out_dtype;
+  g.part = nullptr;
+  // No workspace is available here: force a single K split.
+  const bool fast = aligned16(g.w) && aligned16(g.x) && ldw % 16 == 0 && K % kChunk == 0;
+  if (!fast) {
+    hipLaunchKernelGGL((gemv_generic_kernel<ACT_E4M3, AS_MX32>), dim3((unsigned)cdiv(N, kGemvWaves)),
+                       dim3(kGemvThreads), 0, st, g);
+    return check_launch("mxfp8_scaled_mm(M=1)");
+  }
+  g.k_per_split = cdiv(K, kWaveK) * kWaveK;
+  launch_gemv_fast<ACT_E4M3, WS_CHUNK, AS_MX32>(g, 1, st);
+  return check_launch("mxfp8_scaled_mm(M=1)");
+}
+
+}  // namespace ayk
+
+using namespace ayk;
+
+extern "C" {
+
+size_t ayk_fp8_weight_only_gemv_workspace_bytes(int64_t N, int64_t K) { return gemv_workspace(N, K); }
+size_t ayk_fp8_blockwise_gemv_workspace_bytes(int64_t N, int64_t K) { return gemv_workspace(N, K); }
+
+int ayk_fp8_weight_only_gemv(const void* x, int x_dtype, const void* w, int64_t ldw, int64_t N,
+                             int64_t K, const void* scale, int scale_dtype,
+                             int64_t scale_row_stride, int64_t block_size_y,
+                             int64_t block_size_x, void* out, void* workspace,
+                             size_t workspace_bytes, ayk_stream_t stream) {
+  const char* op = "fp8_weight_only_gemv";
+  if (x_dtype != AYK_BF16 && x_dtype != AYK_F16) return fail(AYK_EINVAL, "%s: input must be float16 or bfloat16", op);
+  if (scale_dtype != AYK_U8 && scale_dtype != AYK_F32 && scale_dtype != AYK_BF16) {
+    return fail(AYK_EINVAL, "%s: scale dtype must be e8m0 (uint8), float32 or bfloat16", op);
+  }
+  if (N < 0 || K < 1 || ldw < K) return fail(AYK_EINVAL, "%s: bad shape N=%lld K=%lld ldw=%lld", op, (long long)N, (long long)K, (long long)ldw);
+  if (block_size_y < 1 || block_size_x < 1) return fail(AYK_EINVAL, "%s: block sizes must be positive", op);
+  if (scale_row_stride < 1) return fail(AYK_EINVAL, "%s: scale_row_stride must be positive", op);
+  if (N == 0) return AYK_OK;
+  if (int rc = check_device()) return rc;
+  GemvArgs g{};
+  g.x = x;
+  g.w = static_cast<const uint8_t*>(w);
+  g.ldw = ldw;
+  g.N = N;
+  g.K = K;
+  g.wscale = scale;
+  g.wscale_dtype = scale_dtype;
+  g.srs = scale_row_stride;
+  g.by = block_size_y;
+  g.bx = block_size_x;
+  g.ascale = nullptr;
+  g.ascale_dtype = AYK_F32;
+  g.bias = nullptr;
+  g.bias_dtype = AYK_F32;
+  g.out = out;
+  g.out_dtype = x_dtype;
+  g.part = static_cast<float*>(workspace);
+  const bool row_scale = block_size_x >= K;
+  hipStream_t st = static_cast<hipStream_t>(stream);
+  if (x_dtype == AYK_BF16) return run_gemv<ACT_BF16, AS_NONE>(g, row_scale, workspace_bytes, op, st);
+  return run_gemv<ACT_F16, AS_NONE>(g, row_scale, workspace_bytes, op, st);
+}
+
+int ayk_fp8_blockwise_gemv(const void* a, const void* b, int64_t ldb, int64_t N, int64_t K,
+                           const void* scale_a, int sa_dtype, const void* scale_b, int sb_dtype,
+                           const void* bias, int bias_dtype, void* out, int out_dtype,
+                           void* workspace, size_t workspace_bytes, ayk_stream_t stream) {
+  const char* op = "fp8_blockwise_gemv";
+  if (!is_float_dtype(sa_dtype) || !is_float_dtype(sb_dtype)) return fail(AYK_EINVAL, "%s: scales must be float32, float16 or bfloat16", op);
+  if (!is_float_dtype(out_dtype)) return fail(AYK_EINVAL, "%s: out must be float16, bfloat16, or float32", op);
+  if (bias && !is_float_dtype(bias_dtype)) return fail(AYK_EINVAL, "%s: bad bias dtype", op);
+  if (N < 0 || K < 1 || ldb < K) return fail(AYK_EINVAL, "%s: bad shape N=%lld K=%lld", op, (long long)N, (long long)K);
+  if (N == 0) return AYK_OK;
+  if (int rc = check_device()) return rc;
+  GemvArgs g{};
+  g.x = a;
+  g.w = static_cast<const uint8_t*>(b);
+  g.ldw = ldb;
+  g.N = N;
+  g.K = K;
+  g.wscale = scale_b;
+  g.wscale_dtype = sb_dtype;
+  g.srs = cdiv(K, 128);
+  g.by = 128;
+  g.bx = 128;
+  g.ascale = scale_a;
+  g.ascale_dtype = sa_dtype;
+  g.bias = bias;
+  g.bias_dtype = bias_dtype;
+  g.out = out;
+  g.out_dtype = out_dtype;
+  g.part = static_cast<float*>(workspace);
+  return run_gemv<ACT_E4M3, AS_BLOCK128>(g, false, workspace_bytes, op, static_cast<hipStream_t>(stream));
+}
+
+}  // extern "C"

@@ -1,0 +1,480 @@
+// Dynamic and static activation quantizers to OCP e4m3fn (gfx950).
+//
+// Semantics follow the reference's plain-torch quantizers
+// (python/ayaka/kernel/triton/reference/quant.py:19-79): fp32 amax, IEEE fp32
+// division x / s, clamp to +-448 (NaN kept), round-to-nearest-even e4m3 encode.
+// These kernels are HBM-bound (3 bytes/element for bf16 in, e4m3 out), so the
+// layout work is about coalescing: every lane moves 16-byte vectors and the
+// per-row / per-group reductions are wavefront shuffles, with the row kept in
+// registers so x is read from HBM exactly once.
+#include "ayk_common.h"
+
+namespace ayk {
+namespace {
+
+constexpr int kQuantThreads = 256;
+
+// 16-byte vector of activation elements.
+template <typename T>
+struct Vec16 {
+  static constexpr int N = 16 / sizeof(typename T::storage);
+};
+
+template <typename T>
+__device__ inline void unpack16(const uint4& v, float* f);
+template <>
+__device__ inline void unpack16<BF16T>(const uint4& v, float* f) {
+  const uint32_t w[4] = {v.x, v.y, v.z, v.w};
+#pragma unroll
+  for (int i = 0; i < 4; ++i) {
+    f[2 * i] = u2f(w[i] << 16);
+    f[2 * i + 1] = u2f(w[i] & 0xFFFF0000u);
+  }
+}
+template <>
+__device__ inline void unpack16<F16T>(const uint4& v, float* f) {
+  const uint32_t w[4] = {v.x, v.y, v.z, v.w};
+#pragma unroll
+  for (int i = 0; i < 4; ++i) {
+    f[2 * i] = f16_bits_to_f32((uint16_t)(w[i] & 0xFFFFu));
+    f[2 * i + 1] = f16_bits_to_f32((uint16_t)(w[i] >> 16));
+  }
+}
+template <>
+__device__ inline void unpack16<F32T>(const uint4& v, float* f) {
+  f[0] = u2f(v.x);
+  f[1] = u2f(v.y);
+  f[2] = u2f(v.z);
+  f[3] = u2f(v.w);
+}
+
+template <int N>
+__device__ inline float absmax_n(const float* f, float m) {
+#pragma unroll
+  for (int i = 0; i < N; ++i) m = nanmax(m, fabsf(f[i]));
+  return m;
+}
+
+// Quantize N floats with scale s (q = e4m3(clamp(f / s))) and store N bytes.
+template <int N>
+__device__ inline void store_quant(uint8_t* dst, const float* f, float s) {
+  uint32_t w[(N + 3) / 4] = {};
+#pragma unroll
+  for (int i = 0; i < N; ++i) {
+    w[i / 4] |= (uint32_t)e4m3_encode(clamp_e4m3(f[i] / s)) << (8 * (i % 4));
+  }
+  if constexpr (N == 8) {
+    *reinterpret_cast<uint2*>(dst) = make_uint2(w[0], w[1]);
+  } else {
+    static_assert(N == 4, "16-byte vectors hold 4 or 8 elements");
+    *reinterpret_cast<uint32_t*>(dst) = w[0];
+  }
+}
+
+// Block-wide NaN-propagating max over 256 threads; every thread gets the result.
+__device__ inline float block_max256(float v, float* red) {
+  v = wave_max<kWave>(v);
+  const int wave = threadIdx.x / kWave;
+  if ((threadIdx.x % kWave) == 0) red[wave] = v;
+  __syncthreads();
+  float r = red[0];
+#pragma unroll
+  for (int i = 1; i < kQuantThreads / kWave; ++i) r = nanmax(r, red[i]);
+  return r;
+}
+
+__device__ inline float floor_amax(float amax) {
+  // clamp_min(1e-10) with NaN kept (reference quant.py:26, :63)
+  return amax < 1e-10f ? 1e-10f : amax;
+}
+
+// ------------------------------------------------------------ rowwise (a1)
+// One 256-thread block per row. VPT > 0 keeps VPT 16-byte vectors per thread in
+// registers (one HBM read of x); VPT == 0 walks the row twice (very long rows).
+template <typename T, int VPT>
+__global__ __launch_bounds__(kQuantThreads) void per_token_quant_vec_kernel(
+    const typename T::storage* __restrict__ x, int64_t k, int64_t ldx,
+    uint8_t* __restrict__ q, int64_t ldq, float* __restrict__ scale) {
+  constexpr int V = Vec16<T>::N;
+  __shared__ float red[kQuantThreads / kWave];
+  const int64_t row = blockIdx.x;
+  const int64_t nvec = k / V;
+  const uint4* xr = reinterpret_cast<const uint4*>(x + row * ldx);
+  uint8_t* qr = q + row * ldq;
+  float amax = 0.0f;
+  float f[V];
+  if constexpr (VPT > 0) {
+    uint4 cache[VPT];
+#pragma unroll
+    for (int i = 0; i < VPT; ++i) {
+      const int64_t v = threadIdx.x + (int64_t)i * kQuantThreads;
+      if (v < nvec) {
+        cache[i] = xr[v];
+        unpack16<T>(cache[i], f);
+        amax = absmax_n<V>(f, amax);
+      }
+    }
+    amax = floor_amax(block_max256(amax, red));
+    const float s = amax / kE4M3Max;
+    if (threadIdx.x == 0) scale[row] = s;
+#pragma unroll
+    for (int i = 0; i < VPT; ++i) {
+      const int64_t v = threadIdx.x + (int64_t)i * kQuantThreads;
+      if (v < nvec) {
+        unpack16<T>(cache[i], f);
+        store_quant<V>(qr + v * V, f, s);
+      }
+    }
+  } else {
+    for (int64_t v = threadIdx.x; v < nvec; v += kQuantThreads) {
+      unpack16<T>(xr[v], f);
+      amax = absmax_n<V>(f, amax);
+    }
+    amax = floor_amax(block_max256(amax, red));
+    const float s = amax / kE4M3Max;
+    if (threadIdx.x == 0) scale[row] = s;
+    for (int64_t v = threadIdx.x; v < nvec; v += kQuantThreads) {
+      unpack16<T>(xr[v], f);
+      store_quant<V>(qr + v * V, f, s);
+    }
+  }
+}
+
+// Any K, any alignment: scalar loads, two passes over the row.
+template <typename T>
+__global__ __launch_bounds__(kQuantThreads) void per_token_quant_scalar_kernel(
+    const typename T::storage* __restrict__ x, int64_t k, int64_t ldx,
+    uint8_t* __restrict__ q, int64_t ldq, float* __restrict__ scale) {
+  __shared__ float red[kQuantThreads / kWave];
+  const int64_t row = blockIdx.x;
+  const typename T::storage* xr = x + row * ldx;
+  float amax = 0.0f;
+  for (int64_t i = threadIdx.x; i < k; i += kQuantThreads) amax = nanmax(amax, fabsf(to_f32<T>(xr[i])));
+  amax = floor_amax(block_max256(amax, red));
+  const float s = amax / kE4M3Max;
+  if (threadIdx.x == 0) scale[row] = s;
+  for (int64_t i = threadIdx.x; i < k; i += kQuantThreads) {
+    q[row * ldq + i] = e4m3_encode(clamp_e4m3(to_f32<T>(xr[i]) / s));
+  }
+}
+
+// ------------------------------------------------- per-(row, group) quantizers
+// MX rule (reference quant.py:47-55): e = clamp(ceil(log2(max(amax/448, 1e-38))),
+// -126, 127) with log2 evaluated in fp32. The fp32 log2 is formed as the fp32
+// rounding of a double-precision log2, i.e. the correctly rounded fp32 result; the
+// only inputs where rounding decides the ceiling are r just above a power of two,
+// where log2(r) lies within half an fp32 ulp of an integer.
+struct MxScale {
+  float inv;     // 2^-e (exact, e <= 120 for every finite fp32 amax)
+  uint8_t code;  // 0 for an all-zero group, else e + 127
+  bool zero;
+};
+__device__ inline MxScale mx_scale(float amax) {
+  MxScale r;
+  float ratio = amax / kE4M3Max;
+  ratio = ratio < 1e-38f ? 1e-38f : ratio;
+  const float l = (float)log2((double)ratio);
+  float e = ceilf(l);
+  e = e < -126.0f ? -126.0f : (e > 127.0f ? 127.0f : e);
+  const int ei = (int)e;
+  r.zero = (amax == 0.0f);
+  r.code = r.zero ? (uint8_t)0 : (uint8_t)(ei + 127);
+  r.inv = u2f((uint32_t)(127 - ei) << 23);
+  return r;
+}
+
+// GL lanes cooperate on one group; each lane holds VPL 16-byte vectors of it.
+template <typename T, int GL, int VPL, bool MX>
+__global__ __launch_bounds__(kQuantThreads) void group_quant_vec_kernel(
+    const typename T::storage* __restrict__ x, int64_t rows, int64_t k, int64_t ldx,
+    int64_t group, uint8_t* __restrict__ q, int64_t ldq, void* __restrict__ scale_out) {
+  constexpr int V = Vec16<T>::N;
+  const int64_t gpr = k / group;
+  const int64_t t = (int64_t)blockIdx.x * kQuantThreads + threadIdx.x;
+  const int64_t gi = t / GL;
+  const int lig = (int)(t % GL);
+  const bool live = gi < rows * gpr;
+  const int64_t row = live ? gi / gpr : 0;
+  const int64_t g = live ? gi % gpr : 0;
+  const uint4* xg = reinterpret_cast<const uint4*>(x + row * ldx + g * group);
+  uint8_t* qg = q + row * ldq + g * group;
+  uint4 cache[VPL];
+  float f[V];
+  float amax = 0.0f;
+#pragma unroll
+  for (int j = 0; j < VPL; ++j) {
+    if (live) {
+      cache[j] = xg[lig + j * GL];
+      unpack16<T>(cache[j], f);
+      amax = absmax_n<V>(f, amax);
+    }
+  }
+  amax = wave_max<GL>(amax);  // every lane of the group takes part (GL divides 64)
+  if (!live) return;
+  if constexpr (MX) {
+    const MxScale ms = mx_scale(amax);
+    if (lig == 0) reinterpret_cast<uint8_t*>(scale_out)[row * gpr + g] = ms.code;
+#pragma unroll
+    for (int j = 0; j < VPL; ++j) {
+      unpack16<T>(cache[j], f);
+      uint32_t w[V / 4] = {};
+      if (!ms.zero) {
+#pragma unroll
+        for (int i = 0; i < V; ++i) {
+          w[i / 4] |= (uint32_t)e4m3_encode(clamp_e4m3(f[i] * ms.inv)) << (8 * (i % 4));
+        }
+      }
+      uint8_t* dst = qg + (int64_t)(lig + j * GL) * V;
+      if constexpr (V == 8) {
+        *reinterpret_cast<uint2*>(dst) = make_uint2(w[0], w[1]);
+      } else {
+        *reinterpret_cast<uint32_t*>(dst) = w[0];
+      }
+    }
+  } else {
+    const float s = floor_amax(amax) / kE4M3Max;
+    if (lig == 0) reinterpret_cast<float*>(scale_out)[row * gpr + g] = s;
+#pragma unroll
+    for (int j = 0; j < VPL; ++j) {
+      unpack16<T>(cache[j], f);
+      store_quant<V>(qg + (int64_t)(lig + j * GL) * V, f, s);
+    }
+  }
+}
+
+// Any group size / alignment: one thread per group, two passes.
+template <typename T, bool MX>
+__global__ __launch_bounds__(kQuantThreads) void group_quant_scalar_kernel(
+    const typename T::storage* __restrict__ x, int64_t rows, int64_t k, int64_t ldx,
+    int64_t group, uint8_t* __restrict__ q, int64_t ldq, void* __restrict__ scale_out) {
+  const int64_t gpr = k / group;
+  const int64_t gi = (int64_t)blockIdx.x * kQuantThreads + threadIdx.x;
+  if (gi >= rows * gpr) return;
+  const int64_t row = gi / gpr, g = gi % gpr;
+  const typename T::storage* xg = x + row * ldx + g * group;
+  uint8_t* qg = q + row * ldq + g * group;
+  float amax = 0.0f;
+  for (int64_t i = 0; i < group; ++i) amax = nanmax(amax, fabsf(to_f32<T>(xg[i])));
+  if constexpr (MX) {
+    const MxScale ms = mx_scale(amax);
+    reinterpret_cast<uint8_t*>(scale_out)[gi] = ms.code;
+    for (int64_t i = 0; i < group; ++i) {
+      qg[i] = ms.zero ? (uint8_t)0 : e4m3_encode(clamp_e4m3(to_f32<T>(xg[i]) * ms.inv));
+    }
+  } else {
+    const float s = floor_amax(amax) / kE4M3Max;
+    reinterpret_cast<float*>(scale_out)[gi] = s;
+    for (int64_t i = 0; i < group; ++i) qg[i] = e4m3_encode(clamp_e4m3(to_f32<T>(xg[i]) / s));
+  }
+}
+
+// ------------------------------------------------------------- static (a4)
+template <typename T>
+__global__ __launch_bounds__(kQuantThreads) void static_quant_kernel(
+    const typename T::storage* __restrict__ x, int64_t n, const void* __restrict__ scale,
+    int scale_dtype, uint8_t* __restrict__ q) {
+  const float s = load_f32(scale, scale_dtype, 0);
+  const int64_t stride = (int64_t)gridDim.x * kQuantThreads;
+  for (int64_t i = (int64_t)blockIdx.x * kQuantThreads + threadIdx.x; i < n; i += stride) {
+    q[i] = e4m3_encode(clamp_e4m3(to_f32<T>(x[i]) / s));
+  }
+}
+
+template <typename T>
+__global__ __launch_bounds__(kQuantThreads) void static_quant_vec_kernel(
+    const typename T::storage* __restrict__ x, int64_t nvec, const void* __restrict__ scale,
+    int scale_dtype, uint8_t* __restrict__ q) {
+  constexpr int V = Vec16<T>::N;
+  const float s = load_f32(scale, scale_dtype, 0);
+  const uint4* xv = reinterpret_cast<const uint4*>(x);
+  const int64_t stride = (int64_t)gridDim.x * kQuantThreads;
+  float f[V];
+  for (int64_t v = (int64_t)blockIdx.x * kQuantThreads + threadIdx.x; v < nvec; v += stride) {
+    unpack16<T>(xv[v], f);
+    store_quant<V>(q + v * V, f, s);
+  }
+}
+
+// ------------------------------------------------------------ host launchers
+template <typename T>
+int launch_per_token(const void* x, int64_t rows, int64_t k, int64_t ldx, void* q, int64_t ldq,
+                     float* scale, hipStream_t st) {
+  using S = typename T::storage;
+  constexpr int V = Vec16<T>::N;
+  const S* xs = static_cast<const S*>(x);
+  uint8_t* qb = static_cast<uint8_t*>(q);
+  const bool vec_ok = aligned16(x) && (k % V == 0) && ((ldx * (int64_t)sizeof(S)) % 16 == 0) &&
+                      ((reinterpret_cast<uintptr_t>(q) % V) == 0) && (ldq % V == 0);
+  const dim3 grid((unsigned)rows), block(kQuantThreads);
+  if (!vec_ok) {
+    hipLaunchKernelGGL(per_token_quant_scalar_kernel<T>, grid, block, 0, st, xs, k, ldx, qb, ldq, scale);
+    return check_launch("per_token_quant_fp8");
+  }
+  const int64_t per_thread = cdiv(k / V, kQuantThreads);
+#define AYK_PT(VPT) \
+  hipLaunchKernelGGL((per_token_quant_vec_kernel<T, VPT>), grid, block, 0, st, xs, k, ldx, qb, ldq, scale)
+  if (per_thread <= 1) AYK_PT(1);
+  else if (per_thread <= 2) AYK_PT(2);
+  else if (per_thread <= 4) AYK_PT(4);
+  else if (per_thread <= 8) AYK_PT(8);
+  else if (per_thread <= 16) AYK_PT(16);
+  else AYK_PT(0);
+#undef AYK_PT
+  return check_launch("per_token_quant_fp8");
+}
+
+template <typename T, bool MX>
+int launch_group(const void* x, int64_t rows, int64_t k, int64_t ldx, int64_t group, void* q,
+                 int64_t ldq, void* scale, hipStream_t st) {
+  using S = typename T::storage;
+  constexpr int V = Vec16<T>::N;
+  const S* xs = static_cast<const S*>(x);
+  uint8_t* qb = static_cast<uint8_t*>(q);
+  const int64_t groups = rows * (k / group);
+  const int64_t vecs = group / V;
+  const bool vec_ok = (group % V == 0) && aligned16(x) && ((ldx * (int64_t)sizeof(S)) % 16 == 0) &&
+                      ((reinterpret_cast<uintptr_t>(q) % V) == 0) && (ldq % V == 0) &&
+                      (vecs & (vecs - 1)) == 0 && vecs <= 64 * 8;
+  if (!vec_ok) {
+    const dim3 grid((unsigned)cdiv(groups, kQuantThreads));
+    hipLaunchKernelGGL((group_quant_scalar_kernel<T, MX>), grid, dim3(kQuantThreads), 0, st, xs,
+                       rows, k, ldx, group, qb, ldq, scale);
+    return check_launch(MX ? "per_token_group_quant_mxfp8" : "per_token_group_quant_fp8");
+  }
+  const int gl = (int)(vecs < 64 ? vecs : 64);
+  const int vpl = (int)(vecs / gl);
+  const dim3 grid((unsigned)cdiv(groups * gl, kQuantThreads)), block(kQuantThreads);
+#define AYK_GQ(GL, VPL)                                                                          \
+  hipLaunchKernelGGL((group_quant_vec_kernel<T, GL, VPL, MX>), grid, block, 0, st, xs, rows, k, \
+                     ldx, group, qb, ldq, scale)
+  switch (gl) {
+    case 1: AYK_GQ(1, 1); break;
+    case 2: AYK_GQ(2, 1); break;
+    case 4: AYK_GQ(4, 1); break;
+    case 8: AYK_GQ(8, 1); break;
+    case 16: AYK_GQ(16, 1); break;
+    case 32: AYK_GQ(32, 1); break;
+    default:
+      switch (vpl) {
+        case 1: AYK_GQ(64, 1); break;
+        case 2: AYK_GQ(64, 2); break;
+        case 4: AYK_GQ(64, 4); break;
+        default: AYK_GQ(64, 8); break;
+      }
+  }
+#undef AYK_GQ
+  return check_launch(MX ? "per_token_group_quant_mxfp8" : "per_token_group_quant_fp8");
+}
+
+template <typename T>
+int launch_static(const void* x, int64_t n, const void* scale, int sdt, void* q, hipStream_t st) {
+  using S = typename T::storage;
+  constexpr int V = Vec16<T>::N;
+  const S* xs = static_cast<const S*>(x);
+  uint8_t* qb = static_cast<uint8_t*>(q);
+  if (aligned16(x) && n % V == 0 && (reinterpret_cast<uintptr_t>(q) % V) == 0) {
+    const int64_t nvec = n / V;
+    const int64_t blocks = cdiv(nvec, kQuantThreads);
+    const dim3 grid((unsigned)(blocks < 8192 ? blocks : 8192));
+    hipLaunchKernelGGL(static_quant_vec_kernel<T>, grid, dim3(kQuantThreads), 0, st, xs, nvec, scale, sdt, qb);
+  } else {
+    const int64_t blocks = cdiv(n, kQuantThreads);
+    const dim3 grid((unsigned)(blocks < 8192 ? blocks : 8192));
+    hipLaunchKernelGGL(static_quant_kernel<T>, grid, dim3(kQuantThreads), 0, st, xs, n, scale, sdt, qb);
+  }
+  return check_launch("static_quant_fp8");
+}
+
+int check_act_dtype(int dt, const char* op) {
+  if (dt != AYK_F32 && dt != AYK_F16 && dt != AYK_BF16) {
+    return fail(AYK_EINVAL, "%s: x dtype must be float32, float16 or bfloat16 (got %d)", op, dt);
+  }
+  return AYK_OK;
+}
+
+}  // namespace
+}  // namespace ayk
+
+using namespace ayk;
+
+extern "C" {
+
+int ayk_per_token_quant_fp8(const void* x, int x_dtype, int64_t rows, int64_t k, int64_t ldx,
+                            void* q, int64_t ldq, float* scale, ayk_stream_t stream) {
+  if (int rc = check_act_dtype(x_dtype, "per_token_quant_fp8")) return rc;
+  if (rows < 0 || k < 1 || ldx < k || ldq < k) {
+    return fail(AYK_EINVAL, "per_token_quant_fp8: bad shape rows=%lld k=%lld ldx=%lld ldq=%lld",
+                (long long)rows, (long long)k, (long long)ldx, (long long)ldq);
+  }
+  if (rows > 0x7FFFFFFF) return fail(AYK_EINVAL, "per_token_quant_fp8: rows=%lld exceeds the grid", (long long)rows);
+  if (rows == 0) return AYK_OK;
+  if (int rc = check_device()) return rc;
+  hipStream_t st = static_cast<hipStream_t>(stream);
+  switch (x_dtype) {
+    case AYK_BF16: return launch_per_token<BF16T>(x, rows, k, ldx, q, ldq, scale, st);
+    case AYK_F16: return launch_per_token<F16T>(x, rows, k, ldx, q, ldq, scale, st);
+    default: return launch_per_token<F32T>(x, rows, k, ldx, q, ldq, scale, st);
+  }
+}
+
+static int group_args(const char* op, int x_dtype, int64_t rows, int64_t k, int64_t ldx,
+                      int64_t group, int64_t ldq, bool pow2) {
+  if (int rc = check_act_dtype(x_dtype, op)) return rc;
+  if (group < 1 || (pow2 && (group & (group - 1)))) {
+    return fail(AYK_EINVAL, "%s: group_size=%lld must be a positive%s", op, (long long)group,
+                pow2 ? " power of two" : " integer");
+  }
+  if (rows < 0 || k < 1 || k % group || ldx < k || ldq < k) {
+    return fail(AYK_EINVAL, "%s: bad shape rows=%lld k=%lld group=%lld", op, (long long)rows,
+                (long long)k, (long long)group);
+  }
+  if (rows * (k / group) > (int64_t)0x7FFFFFFF * 8) return fail(AYK_EINVAL, "%s: too many groups", op);
+  return AYK_OK;
+}
+
+int ayk_per_token_group_quant_fp8(const void* x, int x_dtype, int64_t rows, int64_t k,
+                                  int64_t ldx, int64_t group, void* q, int64_t ldq,
+                                  float* scale, ayk_stream_t stream) {
+  if (int rc = group_args("per_token_group_quant_fp8", x_dtype, rows, k, ldx, group, ldq, true)) return rc;
+  if (rows == 0) return AYK_OK;
+  if (int rc = check_device()) return rc;
+  hipStream_t st = static_cast<hipStream_t>(stream);
+  switch (x_dtype) {
+    case AYK_BF16: return launch_group<BF16T, false>(x, rows, k, ldx, group, q, ldq, scale, st);
+    case AYK_F16: return launch_group<F16T, false>(x, rows, k, ldx, group, q, ldq, scale, st);
+    default: return launch_group<F32T, false>(x, rows, k, ldx, group, q, ldq, scale, st);
+  }
+}
+
+int ayk_per_token_group_quant_mxfp8(const void* x, int x_dtype, int64_t rows, int64_t k,
+                                    int64_t ldx, int64_t group, void* q, int64_t ldq,
+                                    uint8_t* code, ayk_stream_t stream) {
+  if (int rc = group_args("per_token_group_quant_mxfp8", x_dtype, rows, k, ldx, group, ldq, false)) return rc;
+  if (rows == 0) return AYK_OK;
+  if (int rc = check_device()) return rc;
+  hipStream_t st = static_cast<hipStream_t>(stream);
+  switch (x_dtype) {
+    case AYK_BF16: return launch_group<BF16T, true>(x, rows, k, ldx, group, q, ldq, code, st);
+    case AYK_F16: return launch_group<F16T, true>(x, rows, k, ldx, group, q, ldq, code, st);
+    default: return launch_group<F32T, true>(x, rows, k, ldx, group, q, ldq, code, st);
+  }
+}
+
+int ayk_static_quant_fp8(const void* x, int x_dtype, int64_t n, const void* scale,
+                         int scale_dtype, void* q, ayk_stream_t stream) {
+  if (int rc = check_act_dtype(x_dtype, "static_quant_fp8")) return rc;
+  if (scale_dtype != AYK_F32 && scale_dtype != AYK_F16 && scale_dtype != AYK_BF16) {
+    return fail(AYK_EINVAL, "static_quant_fp8: scale dtype must be float32, float16 or bfloat16");
+  }
+  if (n < 0) return fail(AYK_EINVAL, "static_quant_fp8: negative size");
+  if (n == 0) return AYK_OK;
+  if (int rc = check_device()) return rc;
+  hipStream_t st = static_cast<hipStream_t>(stream);
+  switch (x_dtype) {
+    case AYK_BF16: return launch_static<BF16T>(x, n, scale, scale_dtype, q, st);
+    case AYK_F16: return launch_static<F16T>(x, n, scale, scale_dtype, q, st);
+    default: return launch_static<F32T>(x, n, scale, scale_dtype, q, st);
+  }
+}
+
+}  // extern "C"

@@ -1,0 +1,160 @@
+/*
+ * ayaka_fp8.h -- C ABI of the MI355X (gfx950) FP8 linear library `libayaka_fp8.so`.
+ *
+ * One entry point per `torch.ops.ayaka.*` operator of the reference's FP8 linear
+ * path. Every pointer is a raw device pointer (HIP memory on the current device),
+ * every size an int64, every element type a value of `ayk_dtype`, and every call is
+ * enqueued on the given stream without host synchronisation. No entry point
+ * allocates device memory: the split-K GEMVs take a caller-provided workspace whose
+ * size is returned by the matching `*_workspace_bytes` query.
+ *
+ * Return value: AYK_OK (0), or a nonzero `ayk_status` with a message retrievable by
+ * `ayk_last_error()` (thread-local, valid until the next failing call on the thread).
+ *
+ * Layout conventions (all row-major, innermost stride 1):
+ *   activations a / x : [M, K], row stride lda/ldx elements
+ *   weights w / b     : [N, K] e4m3 bytes, row stride ldw/ldb bytes
+ *   outputs out       : [M, N], row stride ldo elements
+ */
+#ifndef AYAKA_FP8_H
+#define AYAKA_FP8_H
+
+#include <stddef.h>
+#include <stdint.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+/* Opaque stream handle: a hipStream_t (0 = the legacy default stream). */
+typedef void* ayk_stream_t;
+
+typedef enum ayk_dtype {
+  AYK_F32 = 0,
+  AYK_F16 = 1,
+  AYK_BF16 = 2,
+  AYK_E4M3 = 3, /* OCP float8 e4m3fn */
+  AYK_U8 = 4    /* raw bytes; as a scale: UE8M0 exponent codes */
+} ayk_dtype;
+
+typedef enum ayk_status {
+  AYK_OK = 0,
+  AYK_EINVAL = 1,     /* bad argument: shape, stride, dtype or alignment */
+  AYK_EARCH = 2,      /* the current device is not gfx950 */
+  AYK_ELAUNCH = 3,    /* the HIP launch failed */
+  AYK_EWORKSPACE = 4  /* workspace missing or too small */
+} ayk_status;
+
+/* Message of the last failing call on this thread ("" if none). */
+const char* ayk_last_error(void);
+
+/* Library ABI version (major * 100 + minor). */
+int ayk_abi_version(void);
+
+/* 1 if `device` is a gfx950 GPU this library has code for, else 0. */
+int ayk_device_supported(int device);
+
+/* ---------------------------------------------------------------- quantizers
+ * All quantizers write OCP e4m3fn with round-to-nearest-even after clamping the
+ * fp32 quotient to [-448, 448]. `x_dtype` is AYK_F32, AYK_F16 or AYK_BF16.     */
+
+/* Replaces ayaka::per_token_quant_fp8
+ * (python/ayaka/kernel/triton/quant/fp8_quant.py:452; oracle reference/quant.py:59-66).
+ * scale[m] = max(max|x[m,:]|, 1e-10) / 448 ; q = e4m3(clamp(x / scale[m])). */
+int ayk_per_token_quant_fp8(const void* x, int x_dtype, int64_t rows, int64_t k,
+                            int64_t ldx, void* q, int64_t ldq, float* scale,
+                            ayk_stream_t stream);
+
+/* Replaces ayaka::per_token_group_quant_fp8 (fp8_quant.py:297; oracle quant.py:19-29).
+ * One fp32 scale per (row, group) stored [rows, k/group] row-major.
+ * group: positive power of two dividing k. */
+int ayk_per_token_group_quant_fp8(const void* x, int x_dtype, int64_t rows, int64_t k,
+                                  int64_t ldx, int64_t group, void* q, int64_t ldq,
+                                  float* scale, ayk_stream_t stream);
+
+/* Replaces ayaka::per_token_group_quant_mxfp8 (fp8_quant.py:374; oracle quant.py:40-56).
+ * code[m, g] = 0 for an all-zero group, else clamp(ceil(log2(amax/448)), -126, 127) + 127.
+ * group: positive, divides k. */
+int ayk_per_token_group_quant_mxfp8(const void* x, int x_dtype, int64_t rows, int64_t k,
+                                    int64_t ldx, int64_t group, void* q, int64_t ldq,
+                                    uint8_t* code, ayk_stream_t stream);
+
+/* Replaces ayaka::static_quant_fp8 (fp8_quant.py:517; oracle quant.py:69-79).
+ * q[i] = e4m3(clamp(x[i] / scale[0])) over n contiguous elements; the scale is read
+ * on the device (`scale_dtype` F32/F16/BF16). */
+int ayk_static_quant_fp8(const void* x, int x_dtype, int64_t n, const void* scale,
+                         int scale_dtype, void* q, ayk_stream_t stream);
+
+/* ------------------------------------------------------------------ GEMMs
+ * Output dtype `out_dtype` is AYK_F32, AYK_F16 or AYK_BF16; `bias` may be NULL.
+ * fp32 accumulation everywhere; one rounding to the output dtype.             */
+
+/* Replaces ayaka::fp8_scaled_mm (gemm/fp8_gemm.py:246; oracle reference/gemm.py:17-37).
+ * out = (a @ b^T) * scale_a * scale_b + bias, with b the [N, K] weight.
+ * scale_a: scalar (sa_per_row = 0) or [M]; scale_b: scalar (sb_per_col = 0) or [N].
+ * Requires K % 16 == 0, lda/ldb multiples of 16 and 16-byte aligned a/b. */
+int ayk_fp8_scaled_mm(const void* a, int64_t lda, const void* b, int64_t ldb,
+                      int64_t M, int64_t N, int64_t K,
+                      const void* scale_a, int sa_dtype, int sa_per_row,
+                      const void* scale_b, int sb_dtype, int sb_per_col,
+                      const void* bias, int bias_dtype,
+                      void* out, int out_dtype, int64_t ldo, ayk_stream_t stream);
+
+/* Replaces ayaka::fp8_blockwise_mm (gemm/fp8_gemm.py:370; oracle reference/gemm.py:40-70).
+ * out = sum_kb (a[:, kb] @ b[:, kb]^T) * scale_a[m, kb] * scale_b[n / 128, kb] + bias.
+ * scale_a: [M, ceil(K/128)] (or [ceil(K/128), M] when sa_col_major), scale_b:
+ * [ceil(N/128), ceil(K/128)], both contiguous. Same alignment rules as above. */
+int ayk_fp8_blockwise_mm(const void* a, int64_t lda, const void* b, int64_t ldb,
+                         int64_t M, int64_t N, int64_t K,
+                         const void* scale_a, int sa_dtype, int sa_col_major,
+                         const void* scale_b, int sb_dtype,
+                         const void* bias, int bias_dtype,
+                         void* out, int out_dtype, int64_t ldo, ayk_stream_t stream);
+
+/* Replaces ayaka::mxfp8_scaled_mm (gemm/fp8_mxfp8_gemm.py:163; oracle reference/gemm.py:73-92).
+ * out = sum_g (a[:, g] @ w[:, g]^T) * 2^(a_scale[m,g]-127) * 2^(w_scale[n,g]-127) + bias
+ * over 32-wide K groups g; UE8M0 code 0 decodes to 0 and 0xFF to NaN.
+ * K % 32 == 0; a_scale [M, K/32] (row stride ld_as), w_scale [N, K/32] (ld_ws). */
+int ayk_mxfp8_scaled_mm(const void* a, int64_t lda, const uint8_t* a_scale, int64_t ld_as,
+                        const void* w, int64_t ldw, const uint8_t* w_scale, int64_t ld_ws,
+                        int64_t M, int64_t N, int64_t K,
+                        const void* bias, int bias_dtype,
+                        void* out, int out_dtype, int64_t ldo, ayk_stream_t stream);
+
+/* Replaces ayaka::fp8_weight_only_gemv (gemm/fp8_gemv.py:323; oracle reference/gemm.py:129-157).
+ * out[n] = sum_k x[k] * w[n, k] * scale[(n / by) * scale_row_stride + k / bx]
+ * x: [K] F16/BF16; scale_dtype: AYK_U8 (UE8M0), AYK_F32 or AYK_BF16; out dtype == x dtype.
+ * The workspace holds split-K partials (see ayk_fp8_weight_only_gemv_workspace_bytes). */
+int ayk_fp8_weight_only_gemv(const void* x, int x_dtype, const void* w, int64_t ldw,
+                             int64_t N, int64_t K, const void* scale, int scale_dtype,
+                             int64_t scale_row_stride, int64_t block_size_y,
+                             int64_t block_size_x, void* out,
+                             void* workspace, size_t workspace_bytes, ayk_stream_t stream);
+size_t ayk_fp8_weight_only_gemv_workspace_bytes(int64_t N, int64_t K);
+
+/* Replaces ayaka::fp8_weight_only_gemm (gemm/fp8_w8a16_gemm.py:144; oracle
+ * reference/gemm.py:95-126). The [M, K] form of ayk_fp8_weight_only_gemv; out dtype ==
+ * x dtype. Each dequantized weight w * scale is rounded to the activation dtype before
+ * the product, as the reference does. */
+int ayk_fp8_weight_only_gemm(const void* x, int x_dtype, int64_t ldx, int64_t M,
+                             const void* w, int64_t ldw, int64_t N, int64_t K,
+                             const void* scale, int scale_dtype, int64_t scale_row_stride,
+                             int64_t block_size_y, int64_t block_size_x,
+                             void* out, int64_t ldo, ayk_stream_t stream);
+
+/* Replaces ayaka::fp8_blockwise_gemv (gemm/fp8_gemv.py:433; oracle reference/gemm.py:160-189).
+ * out[n] = sum_kb (a[kb] . b[n, kb]) * scale_a[kb] * scale_b[n / 128, kb] + bias[n],
+ * a: [K] e4m3, scale_a [ceil(K/128)], scale_b [ceil(N/128), ceil(K/128)] contiguous. */
+int ayk_fp8_blockwise_gemv(const void* a, const void* b, int64_t ldb, int64_t N, int64_t K,
+                           const void* scale_a, int sa_dtype,
+                           const void* scale_b, int sb_dtype,
+                           const void* bias, int bias_dtype,
+                           void* out, int out_dtype,
+                           void* workspace, size_t workspace_bytes, ayk_stream_t stream);
+size_t ayk_fp8_blockwise_gemv_workspace_bytes(int64_t N, int64_t K);
+
+#ifdef __cplusplus
+}
+#endif
+
+#endif /* AYAKA_FP8_H */

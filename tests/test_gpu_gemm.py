@@ -1,0 +1,215 @@
+"""GPU parity of the GEMV / GEMM operators against the CPU oracle.
+
+Every case draws seeded inputs, runs the HIP operator and compares with the oracle
+under the rule in ``tests/_tol.py`` (per-element relative error <= 1e-2, absolute
+floor 1e-3 of the output scale). Shapes cover tile tails in M, N and K, the
+padded-K path, every scale dtype, and decode M in {1, 4, 16, 32}.
+"""
+
+import sys
+
+import pytest
+import torch
+
+from oracle import fp8_oracle as ora
+from tests._tol import assert_linear_close
+
+pytestmark = pytest.mark.gpu
+FP8 = torch.float8_e4m3fn
+
+
+def _say(msg: str) -> None:
+    print(msg, flush=True)
+    sys.stdout.flush()
+
+
+def _gen(seed: int) -> torch.Generator:
+    return torch.Generator().manual_seed(seed)
+
+
+def _fp8(shape, seed, scale=1.0):
+    return (torch.randn(*shape, generator=_gen(seed)) * scale).clamp(-448, 448).to(FP8)
+
+
+# ------------------------------------------------------------------ weight-only GEMV
+@pytest.mark.parametrize("xdt", [torch.bfloat16, torch.float16])
+@pytest.mark.parametrize(
+    "n,k,by,bx,sdt",
+    [
+        (3072, 1024, 1, 1024, "float32"),  # per-channel (rowwise / per-tensor decode)
+        (3072, 1024, 3072, 1024, "float32"),  # one scalar scale broadcast
+        (300, 4096, 1, 4096, "float32"),
+        (4096, 14336, 1, 14336, "float32"),  # Cfg2 down (split-K)
+        (520, 7168, 128, 128, "float32"),  # block-128 decode
+        (700, 1792, 128, 128, "bfloat16"),
+        (256, 2048, 1, 32, "e8m0"),  # per-32 UE8M0
+        (100, 100, 1, 100, "float32"),  # K % 16 != 0: generic path
+        (64, 96, 16, 24, "bfloat16"),  # scale block not a multiple of 16: generic path
+    ],
+)
+def test_weight_only_gemv(gpu, xdt, n, k, by, bx, sdt):
+    from ayaka.kernel.hip import fp8_weight_only_gemv
+
+    _say(f"fp8_weight_only_gemv x={xdt} n={n} k={k} by={by} bx={bx} scale={sdt}")
+    w = _fp8((n, k), seed=n + k)
+    srs = -(-k // bx)
+    rows = -(-n // by)
+    if sdt == "e8m0":
+        scale = torch.randint(110, 130, (rows, srs), generator=_gen(1), dtype=torch.uint8)
+    else:
+        scale = (torch.rand(rows, srs, generator=_gen(2)) * 0.02 + 1e-3).to(torch.float32 if sdt == "float32" else torch.bfloat16)
+    x = torch.randn(k, generator=_gen(3)).to(xdt)
+    y = fp8_weight_only_gemv(x.to(gpu), w.to(gpu), scale.to(gpu), srs, by, bx, sdt)
+    ref = ora.fp8_weight_only_gemv(x, w, scale, srs, by, bx, sdt)
+    assert y.dtype == xdt
+    assert_linear_close(y, ref, "weight_only_gemv")
+    out = torch.empty(n, dtype=xdt, device=gpu)
+    r = fp8_weight_only_gemv(x.to(gpu), w.to(gpu), scale.to(gpu), srs, by, bx, sdt, out=out)
+    assert r is out
+    assert torch.equal(out.cpu(), y.cpu()), "repeat launches must be bit-identical"
+
+
+@pytest.mark.parametrize("n,k", [(512, 1024), (333, 2048), (2048, 7168)])
+def test_blockwise_gemv(gpu, n, k):
+    from ayaka.kernel.hip import fp8_blockwise_gemv
+
+    _say(f"fp8_blockwise_gemv n={n} k={k}")
+    a = _fp8((k,), seed=5, scale=20)
+    b = _fp8((n, k), seed=6, scale=20)
+    sa = torch.rand(-(-k // 128), generator=_gen(7)) * 0.1
+    sb = torch.rand(-(-n // 128), -(-k // 128), generator=_gen(8)) * 0.01
+    bias = torch.randn(n, generator=_gen(9))
+    y = fp8_blockwise_gemv(a.to(gpu), b.to(gpu), sa.to(gpu), sb.to(gpu), bias.to(gpu))
+    assert y.dtype == torch.float32
+    assert_linear_close(y, ora.fp8_blockwise_gemv(a, b, sa, sb, bias), "blockwise_gemv")
+
+
+# ------------------------------------------------------------------ W8A8 GEMMs
+MNK = [(8, 3072, 1024), (17, 300, 256), (64, 256, 384), (200, 1000, 1024), (256, 512, 2048), (129, 130, 528)]
+
+
+@pytest.mark.parametrize("m,n,k", MNK)
+@pytest.mark.parametrize("rowwise", [True, False])
+def test_fp8_scaled_mm(gpu, m, n, k, rowwise):
+    from ayaka.kernel.hip import fp8_scaled_mm
+
+    _say(f"fp8_scaled_mm m={m} n={n} k={k} rowwise={rowwise}")
+    a = _fp8((m, k), seed=m, scale=40)
+    w = _fp8((n, k), seed=n, scale=40)
+    sa = (torch.rand(m, generator=_gen(1)) * 0.01 + 1e-3) if rowwise else torch.tensor(0.004)
+    sb = (torch.rand(n, generator=_gen(2)) * 0.01 + 1e-3) if rowwise else torch.tensor(0.002)
+    bias = torch.randn(n, generator=_gen(3)).to(torch.bfloat16)
+    ref = ora.fp8_scaled_mm(a, w, sa, sb, bias)
+    y = fp8_scaled_mm(a.to(gpu), w.to(gpu).t(), sa.to(gpu), sb.to(gpu), bias.to(gpu))
+    assert y.dtype == torch.float32
+    assert_linear_close(y, ref, "fp8_scaled_mm fp32")
+    out = torch.empty(m, n, dtype=torch.bfloat16, device=gpu)
+    r = fp8_scaled_mm(a.to(gpu), w.to(gpu).t(), sa.to(gpu), sb.to(gpu), bias.to(gpu), out=out)
+    assert r is out
+    assert_linear_close(out, ref, "fp8_scaled_mm bf16")
+
+
+def test_fp8_scaled_mm_row_major_b_and_odd_k(gpu):
+    from ayaka.kernel.hip import fp8_scaled_mm
+
+    _say("fp8_scaled_mm [K,N] b and K=40")
+    a = _fp8((33, 40), seed=1, scale=10)
+    w = _fp8((70, 40), seed=2, scale=10)
+    b_kn = w.t().contiguous()  # row-major [K, N]
+    y = fp8_scaled_mm(a.to(gpu), b_kn.to(gpu), torch.tensor(0.5, device=gpu), torch.tensor(0.25, device=gpu))
+    assert_linear_close(y, ora.fp8_scaled_mm(a, w, torch.tensor(0.5), torch.tensor(0.25)), "scaled_mm odd K")
+
+
+@pytest.mark.parametrize("m,n,k", [(2, 256, 256), (32, 640, 1024), (256, 384, 2048), (300, 200, 1280), (129, 1024, 7168)])
+@pytest.mark.parametrize("sdt", [torch.float32, torch.bfloat16])
+@pytest.mark.parametrize("col_major", [False, True])
+def test_fp8_blockwise_mm(gpu, m, n, k, sdt, col_major):
+    from ayaka.kernel.hip import fp8_blockwise_mm
+
+    _say(f"fp8_blockwise_mm m={m} n={n} k={k} sdt={sdt} col_major={col_major}")
+    kb, nb = -(-k // 128), -(-n // 128)
+    a = _fp8((m, k), seed=m + 1, scale=30)
+    w = _fp8((n, k), seed=n + 2, scale=30)
+    # block scales spread log-uniformly over 1e-3 .. 1 exercise the per-128 rescale
+    sa = torch.exp(torch.rand(m, kb, generator=_gen(4)) * -6.9).float()
+    sb = torch.exp(torch.rand(nb, kb, generator=_gen(5)) * -6.9).to(sdt)
+    sa_arg = sa.t().contiguous() if col_major else sa
+    ref = ora.fp8_blockwise_mm(a, w, sa_arg, sb, None, col_major)
+    out = torch.empty(m, n, dtype=torch.bfloat16, device=gpu)
+    fp8_blockwise_mm(a.to(gpu), w.to(gpu), sa_arg.to(gpu), sb.to(gpu), out=out, a_scale_col_major=col_major)
+    assert_linear_close(out, ref, "blockwise_mm")
+
+
+@pytest.mark.parametrize("m,n,k", [(1, 512, 1024), (1, 1000, 8192), (64, 256, 512), (100, 300, 1024), (512, 512, 2048), (33, 96, 96)])
+def test_mxfp8_scaled_mm(gpu, m, n, k):
+    from ayaka.kernel.hip import mxfp8_scaled_mm
+
+    _say(f"mxfp8_scaled_mm m={m} n={n} k={k}")
+    torch.manual_seed(m + n + k)
+    x = torch.distributions.StudentT(3.0).sample((m, k))
+    wf = torch.randn(n, k, generator=_gen(2))
+    qa, ca = ora.per_token_group_quant_mxfp8(x, 32)
+    qw, cw = ora.per_token_group_quant_mxfp8(wf, 32)
+    bias = torch.randn(n, generator=_gen(3))
+    ref = ora.mxfp8_scaled_mm(qa, ca, qw, cw, bias)
+    out = torch.empty(m, n, dtype=torch.bfloat16, device=gpu)
+    mxfp8_scaled_mm(qa.to(gpu), ca.to(gpu), qw.to(gpu), cw.to(gpu), bias.to(gpu), out=out)
+    assert_linear_close(out, ref, "mxfp8_scaled_mm")
+
+
+@pytest.mark.parametrize("m", [4, 16, 32, 100])
+@pytest.mark.parametrize("case", ["channel", "block128", "e8m0_32"])
+def test_weight_only_gemm(gpu, m, case):
+    from ayaka.kernel.hip import fp8_weight_only_gemm
+
+    n, k = 640, 1024
+    _say(f"fp8_weight_only_gemm m={m} case={case}")
+    w = _fp8((n, k), seed=10)
+    if case == "channel":
+        by, bx, sdt = 1, k, "float32"
+        scale = torch.rand(n, 1, generator=_gen(1)) * 0.01 + 1e-3
+    elif case == "block128":
+        by, bx, sdt = 128, 128, "bfloat16"
+        scale = (torch.rand(n // 128, k // 128, generator=_gen(1)) * 0.01 + 1e-3).to(torch.bfloat16)
+    else:
+        by, bx, sdt = 1, 32, "e8m0"
+        scale = torch.randint(115, 125, (n, k // 32), generator=_gen(1), dtype=torch.uint8)
+    x = torch.randn(m, k, generator=_gen(2)).to(torch.bfloat16)
+    y = fp8_weight_only_gemm(x.to(gpu), w.to(gpu), scale.to(gpu), -(-k // bx), by, bx, sdt)
+    ref = ora.fp8_weight_only_gemm(x, w, scale, -(-k // bx), by, bx, sdt)
+    assert y.dtype == torch.bfloat16
+    assert_linear_close(y, ref, "weight_only_gemm")
+
+
+# ------------------------------------------------------------------ linear entry points
+@pytest.mark.parametrize("m", [1, 8, 40])
+@pytest.mark.parametrize("recipe", ["w8a8_rowwise", "w8a8_dynamic_per_tensor", "w8a8_block128"])
+def test_fp8_linear_entry_points(gpu, m, recipe):
+    from ayaka.kernel.hip import fp8_block_linear, fp8_pertensor_linear, fp8_rowwise_linear
+
+    n, k = 384, 1024
+    _say(f"fp8 linear recipe={recipe} m={m}")
+    wf = torch.randn(n, k, generator=_gen(1)) * 0.02
+    if recipe == "w8a8_block128":
+        blocks = wf.reshape(n // 128, 128, k // 128, 128).abs().amax(dim=(1, 3))
+        scale = blocks / 448.0
+        w = (wf / scale.repeat_interleave(128, 0).repeat_interleave(128, 1)).clamp(-448, 448).to(FP8)
+    elif recipe == "w8a8_rowwise":
+        scale = wf.abs().amax(dim=1) / 448.0
+        w = (wf / scale[:, None]).to(FP8)
+    else:
+        scale = (wf.abs().amax() / 448.0).reshape(())
+        w = (wf / scale).to(FP8)
+    x = torch.randn(2, m, k, generator=_gen(2)).to(torch.bfloat16) if m > 1 else torch.randn(1, k, generator=_gen(2)).to(torch.bfloat16)
+    bias = torch.randn(n, generator=_gen(3)).to(torch.bfloat16)
+    # W8A8 GEMM paths fuse the bias before the single rounding; M == 1 adds it after.
+    ref = ora.fp8_linear(recipe, x, w, scale, bias, bias_in_fp32=True)
+    fn = {"w8a8_rowwise": fp8_rowwise_linear, "w8a8_dynamic_per_tensor": fp8_rowwise_linear,
+          "w8a8_block128": fp8_block_linear}[recipe]
+    y = fn(x.to(gpu), w.to(gpu), scale.to(gpu), bias.to(gpu))
+    assert y.shape == ref.shape and y.dtype == torch.bfloat16
+    assert_linear_close(y, ref, recipe)
+    if recipe == "w8a8_dynamic_per_tensor":
+        y2 = fp8_pertensor_linear(x.to(gpu), w.to(gpu), scale.to(gpu), bias.to(gpu))
+        ref2 = ora.fp8_linear("w8a16", x, w, scale.reshape(1, 1).expand(1, 1), bias, weight_block=(n, k))
+        assert_linear_close(y2, ref2, "pertensor weight-only")
