@@ -22,7 +22,7 @@
 namespace ayk {
 namespace {
 
-constexpr int kGemvThreads = 256;
+constexpr int kGemvThreads = 128;  // 2 wavefronts: small blocks schedule best for streaming
 constexpr int kGemvWaves = kGemvThreads / kWave;
 constexpr int kChunk = 16;                      // K elements per lane vector
 constexpr int64_t kWaveK = (int64_t)kWave * kChunk;  // K elements per wave sweep
@@ -95,24 +95,34 @@ __device__ inline float act_scale(const GemvArgs& a, int64_t k0) {
   else return 1.0f;
 }
 
-template <int ACT, int WS, int AS, int R>
+// Weights are read once per call, so they are loaded non-temporally (they should
+// not displace the activation vector or other live data from L2 / MALL).
+typedef unsigned v4u __attribute__((ext_vector_type(4)));
+__device__ inline uint4 load_stream(const uint8_t* p) {
+  const v4u v = __builtin_nontemporal_load(reinterpret_cast<const v4u*>(p));
+  return make_uint4(v.x, v.y, v.z, v.w);
+}
+
+// R weight rows per wavefront; U sweeps (U * 1024 K elements) of loads issued
+// before any of them is consumed, i.e. R * U 16-byte loads in flight per lane.
+template <int ACT, int WS, int AS, int R, int U>
 __global__ __launch_bounds__(kGemvThreads) void gemv_kernel(GemvArgs a) {
   const int lane = threadIdx.x % kWave;
   const int wave = threadIdx.x / kWave;
   const int64_t row0 = ((int64_t)blockIdx.x * kGemvWaves + wave) * R;
   const int64_t kbeg = (int64_t)blockIdx.y * a.k_per_split;
   const int64_t kend = min(a.K, kbeg + a.k_per_split);
-  int64_t rows[R];
-#pragma unroll
-  for (int r = 0; r < R; ++r) rows[r] = min(row0 + r, a.N - 1);  // clamp: loads stay in bounds
+  const uint8_t* wrow[R];
   float acc[R];
-#pragma unroll
-  for (int r = 0; r < R; ++r) acc[r] = 0.0f;
-
   // Scale row offsets are computed once; per-chunk column indices use 32-bit math.
   int64_t sbase[R];
 #pragma unroll
-  for (int r = 0; r < R; ++r) sbase[r] = (rows[r] / a.by) * a.srs;
+  for (int r = 0; r < R; ++r) {
+    const int64_t n = min(row0 + r, a.N - 1);  // clamp: loads stay in bounds
+    wrow[r] = a.w + n * a.ldw;
+    acc[r] = 0.0f;
+    sbase[r] = (n / a.by) * a.srs;
+  }
   float row_scale[R];
   if constexpr (WS == WS_ROW) {
 #pragma unroll
@@ -120,24 +130,33 @@ __global__ __launch_bounds__(kGemvThreads) void gemv_kernel(GemvArgs a) {
   }
   const uint32_t bx = (uint32_t)a.bx;
 
-  for (int64_t k0 = kbeg + (int64_t)lane * kChunk; k0 < kend; k0 += kWaveK) {
-    float xf[16];
-    load_x_chunk<ACT>(a.x, k0 / kChunk, xf);
-    uint4 wv[R];
+  for (int64_t kb = kbeg + (int64_t)lane * kChunk; kb < kend; kb += kWaveK * U) {
+    uint4 wv[U][R];
 #pragma unroll
-    for (int r = 0; r < R; ++r) wv[r] = *reinterpret_cast<const uint4*>(a.w + rows[r] * a.ldw + k0);
-    const float sa = act_scale<AS>(a, k0);
-    const uint32_t kcol = WS == WS_CHUNK ? (uint32_t)k0 / bx : 0u;
+    for (int u = 0; u < U; ++u) {
+      const int64_t k0 = kb + u * kWaveK;
 #pragma unroll
-    for (int r = 0; r < R; ++r) {
-      const float d = dot16(wv[r], xf);
-      if constexpr (WS == WS_ROW && AS == AS_NONE) {
-        acc[r] += d;
-      } else if constexpr (WS == WS_ROW) {
-        acc[r] = fmaf(d, sa, acc[r]);
-      } else {
-        const float sw = load_f32(a.wscale, a.wscale_dtype, sbase[r] + kcol);
-        acc[r] = fmaf(d, sw * sa, acc[r]);
+      for (int r = 0; r < R; ++r) wv[u][r] = k0 < kend ? load_stream(wrow[r] + k0) : make_uint4(0, 0, 0, 0);
+    }
+#pragma unroll
+    for (int u = 0; u < U; ++u) {
+      const int64_t k0 = kb + u * kWaveK;
+      if (k0 >= kend) break;
+      float xf[16];
+      load_x_chunk<ACT>(a.x, k0 / kChunk, xf);
+      const float sa = act_scale<AS>(a, k0);
+      const uint32_t kcol = WS == WS_CHUNK ? (uint32_t)k0 / bx : 0u;
+#pragma unroll
+      for (int r = 0; r < R; ++r) {
+        const float d = dot16(wv[u][r], xf);
+        if constexpr (WS == WS_ROW && AS == AS_NONE) {
+          acc[r] += d;
+        } else if constexpr (WS == WS_ROW) {
+          acc[r] = fmaf(d, sa, acc[r]);
+        } else {
+          const float sw = load_f32(a.wscale, a.wscale_dtype, sbase[r] + kcol);
+          acc[r] = fmaf(d, sw * sa, acc[r]);
+        }
       }
     }
   }
@@ -195,10 +214,11 @@ __global__ __launch_bounds__(kGemvThreads) void gemv_generic_kernel(GemvArgs a) 
   }
 }
 
-constexpr int kRows = 4;  // weight rows per wavefront
+constexpr int kRows = 2;    // weight rows per wavefront
+constexpr int kUnroll = 4;  // K sweeps in flight per wavefront
 
 // Split plan from shapes only (graph-capture safe): the smallest power-of-two K
-// split that gives >= 2048 row-waves (8 per CU), never splitting below one sweep.
+// split that gives >= 4096 wavefronts (16 per CU), never splitting below one sweep.
 struct SplitPlan {
   int split;
   int64_t k_per_split;
@@ -207,7 +227,7 @@ SplitPlan gemv_split_plan(int64_t N, int64_t K) {
   const int64_t waves = cdiv(N, kRows);
   const int64_t sweeps = cdiv(K, kWaveK);
   int split = 1;
-  while (waves * split < 2048 && split * 2 <= sweeps && split < 64) split *= 2;
+  while (waves * split < 4096 && split * 2 <= sweeps && split < 64) split *= 2;
   const int64_t kps = cdiv(sweeps, split) * kWaveK;
   split = (int)cdiv(K, kps);
   return {split, kps};
@@ -216,7 +236,7 @@ SplitPlan gemv_split_plan(int64_t N, int64_t K) {
 template <int ACT, int WS, int AS>
 void launch_gemv_fast(GemvArgs& a, int split, hipStream_t st) {
   const dim3 grid((unsigned)cdiv(a.N, (int64_t)kGemvWaves * kRows), (unsigned)split);
-  hipLaunchKernelGGL((gemv_kernel<ACT, WS, AS, kRows>), grid, dim3(kGemvThreads), 0, st, a);
+  hipLaunchKernelGGL((gemv_kernel<ACT, WS, AS, kRows, kUnroll>), grid, dim3(kGemvThreads), 0, st, a);
 }
 
 template <int ACT, int AS>
