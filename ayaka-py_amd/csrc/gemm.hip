@@ -23,6 +23,7 @@
 // global loads are issued before the current step's MFMAs. LDS rows are padded to
 // 144 bytes so the 32 rows a wavefront reads at one K offset fall on distinct banks.
 #include "ayk_common.h"
+#include "gemm_tiles.h"
 
 namespace ayk {
 
@@ -284,6 +285,254 @@ __global__ __launch_bounds__(kThreads) void fp8_gemm_kernel(GemmArgs g) {
   }
 }
 
+// ---------------------------------------------------------------------------------
+// Large-tile kernel (K % 128 == 0, M and N of at least one tile): a 256 x 256 output
+// tile per workgroup, one 128 x 128 wavefront tile (4 x 4 MFMA tiles, 256 accumulator
+// registers) on each of the four SIMDs.
+//
+//  * Operands move HBM/L2 -> LDS with gfx950's direct-to-LDS 16-byte loads
+//    (global_load_lds_dwordx4): no staging registers, no VALU. One such load writes
+//    64 lanes x 16 B = 8 tile rows of 128 B contiguously, so the LDS layout is set by
+//    choosing which 16-byte chunk each lane fetches: row r stores logical chunk c at
+//    physical chunk c ^ ((r >> 1) & 7). The 32 rows a wavefront reads at one K offset
+//    then fall on 16 distinct 16-byte bank groups per half-wave.
+//  * Two LDS stages of 64 KB in two distinct LDS objects, the K loop unrolled by two:
+//    the next K step's loads are in flight during the current step's 32 MFMAs, and
+//    fragments of the second 64-K half are read during the first half's MFMAs.
+//  * Workgroup b runs on XCD b % 8. Tiles are numbered so that each XCD owns a
+//    contiguous range of an M-grouped order (8 M tiles per group): the ~32 tiles an
+//    XCD runs at once share 8 activation and 4 weight panels through its L2.
+//  * Rows past M / N are clamped to the last row (their results are never stored),
+//    so every load is in bounds; K must be a multiple of 128.
+constexpr int kBigTile = 256;
+// Word 3 of a raw (unstructured, stride 0) buffer resource on gfx9-family GPUs.
+constexpr int kBufferFlags = 0x00020000;
+constexpr int kBigStage = 2 * kBigTile * BK;  // weights + activations, bytes
+
+// Four consecutive bias values n .. n+3 (n + 3 < N, n % 4 == 0) as floats.
+__device__ inline void load_bias4(const GemmArgs& g, int64_t n, float* b) {
+  if (g.bias_dtype == AYK_F32) {
+    const float4 v = *reinterpret_cast<const float4*>(reinterpret_cast<const float*>(g.bias) + n);
+    b[0] = v.x; b[1] = v.y; b[2] = v.z; b[3] = v.w;
+  } else {
+    const uint2 v = *reinterpret_cast<const uint2*>(reinterpret_cast<const uint16_t*>(g.bias) + n);
+    const uint32_t w[2] = {v.x, v.y};
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+      const uint16_t bits = (uint16_t)(w[i / 2] >> (16 * (i % 2)));
+      b[i] = g.bias_dtype == AYK_BF16 ? bf16_bits_to_f32(bits) : f16_bits_to_f32(bits);
+    }
+  }
+}
+
+template <int OUT>
+__device__ inline void store4_typed(const GemmArgs& g, int64_t m, int64_t n, const float* v) {
+  if (OUT == AYK_F32) {
+    *reinterpret_cast<float4*>(reinterpret_cast<float*>(g.out) + m * g.ldo + n) = make_float4(v[0], v[1], v[2], v[3]);
+  } else {
+    uint16_t b[4];
+#pragma unroll
+    for (int i = 0; i < 4; ++i) b[i] = OUT == AYK_BF16 ? f32_to_bf16_bits(v[i]) : f32_to_f16_bits(v[i]);
+    *reinterpret_cast<uint2*>(reinterpret_cast<uint16_t*>(g.out) + m * g.ldo + n) =
+        make_uint2((uint32_t)b[0] | ((uint32_t)b[1] << 16), (uint32_t)b[2] | ((uint32_t)b[3] << 16));
+  }
+}
+
+// Epilogue of the large-tile kernel for a 128 x 128 wavefront tile at (m0, n0):
+// per-row / per-column fp32 scales (SCALED), bias, one rounding, 4 consecutive n
+// per store. The fast path needs N % 4 == 0 and a 4-element-aligned output row
+// (checked by the launcher); rows / columns past M / N are skipped.
+template <int MODE, int OUT>
+__device__ inline void big_epilogue(const GemmArgs& g, const v16f (&acc)[4][4], int64_t m0, int64_t n0) {
+  const int lane = threadIdx.x & 63, h = lane >> 5, frow = lane & 31;
+  const float* sa_p = reinterpret_cast<const float*>(g.sa);
+  const float* sb_p = reinterpret_cast<const float*>(g.sb);
+#pragma unroll
+  for (int j = 0; j < 4; ++j) {
+    const int64_t m = m0 + j * 32 + frow;
+    const bool row_ok = m < g.M;
+    float sa = 1.0f;
+    if constexpr (MODE == MODE_SCALED) sa = sa_p[g.sa_vec ? (row_ok ? m : 0) : 0];
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+#pragma unroll
+      for (int grp = 0; grp < 4; ++grp) {
+        const int64_t n = n0 + i * 32 + grp * 8 + h * 4;
+        if (!row_ok || n >= g.N) continue;
+        float sb[4] = {1.0f, 1.0f, 1.0f, 1.0f};
+        if constexpr (MODE == MODE_SCALED) {
+          if (g.sb_vec) {
+            const float4 t = *reinterpret_cast<const float4*>(sb_p + n);
+            sb[0] = t.x; sb[1] = t.y; sb[2] = t.z; sb[3] = t.w;
+          } else {
+            sb[0] = sb[1] = sb[2] = sb[3] = sb_p[0];
+          }
+        }
+        float bias[4] = {0.0f, 0.0f, 0.0f, 0.0f};
+        if (g.bias) load_bias4(g, n, bias);
+        float v[4];
+#pragma unroll
+        for (int qq = 0; qq < 4; ++qq) {
+          float y = acc[i][j][grp * 4 + qq];
+          if constexpr (MODE == MODE_SCALED) y = (y * sa) * sb[qq];
+          v[qq] = y + bias[qq];
+        }
+        store4_typed<OUT>(g, m, n, v);
+      }
+    }
+  }
+}
+
+template <int MODE>
+__global__ __launch_bounds__(kThreads, 1) void fp8_gemm_big_kernel(GemmArgs g) {
+  constexpr int FN = 4, FM = 4;                  // 32x32 MFMA tiles per wavefront (n, m)
+  constexpr int kLoads = kBigStage / 1024 / 4;   // direct loads per wavefront per stage
+  // Two distinct LDS objects (not one array indexed by stage), so the compiler can
+  // tell that reads of one stage never alias the in-flight direct loads of the other
+  // and does not wait for those loads before reading.
+  __shared__ __attribute__((aligned(1024))) uint8_t lds0[kBigStage];
+  __shared__ __attribute__((aligned(1024))) uint8_t lds1[kBigStage];
+
+  const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+  const int wn = wave >> 1, wm = wave & 1;
+  const int h = lane >> 5, frow = lane & 31;
+  int tm, tn;
+  big_tile_coords(blockIdx.x, g.tiles_m, (int)cdiv(g.N, kBigTile), tm, tn);
+  const int64_t n_base = (int64_t)tn * kBigTile, m_base = (int64_t)tm * kBigTile;
+  const int nk = (int)(g.K / BK);
+
+  // Direct loads: wavefronts 0-1 fetch the 256 weight rows, 2-3 the 256 activation
+  // rows (128 each), as buffer loads into LDS. Load instruction jj of a wavefront
+  // fills LDS tile rows r = 8 * (16 * wave + jj) + lane/8; lane fetches logical chunk
+  // (lane & 7) ^ ((r >> 1) & 7), which depends only on the lane and jj's parity. The
+  // buffer resource starts at the wavefront's first row and ends at the operand's last
+  // row: rows past M / N read as zero (their results are never stored), no clamping.
+  // Per load: a per-lane vector offset (row, chunk) and a wave-uniform scalar offset
+  // (jj's 8 rows + K step), so no 64-bit address is kept per load.
+  const int q = lane >> 3, pc = lane & 7;
+  const int wave_u = __builtin_amdgcn_readfirstlane(wave);  // keep the descriptor in SGPRs
+  const bool w_wave = wave_u < 2;
+  const int64_t ld = w_wave ? g.ldw : g.lda;
+  const int64_t row0 = (w_wave ? n_base : m_base) + (wave_u & 1) * 128;
+  const OperandWindow win = operand_window(row0, w_wave ? g.N : g.M, ld);
+  const __amdgpu_buffer_rsrc_t op_rsrc = __builtin_amdgcn_make_buffer_rsrc(
+      const_cast<uint8_t*>((w_wave ? g.w : g.a) + win.base_offset), (short)0, win.records, kBufferFlags);
+  const int voff[2] = {(int)(q * ld) + ((pc ^ ((q >> 1) & 7)) << 4), (int)(q * ld) + ((pc ^ ((4 + (q >> 1)) & 7)) << 4)};
+  auto issue_stage = [&](int kt, uint8_t* dst) {
+#pragma unroll
+    for (int jj = 0; jj < kLoads; ++jj) {
+      const int soff = __builtin_amdgcn_readfirstlane((int)(jj * 8 * ld) + kt * BK);
+      __builtin_amdgcn_raw_ptr_buffer_load_lds(op_rsrc, (__attribute__((address_space(3))) void*)(dst + (wave_u * kLoads + jj) * 1024),
+                                               16, voff[jj & 1], soff, 0, 0);
+    }
+  };
+  // Fragment reads. A fragment row is frow + (a multiple of 32), so its swizzle term
+  // (row >> 1) & 7 == (frow >> 1) & 7 is the same for every fragment of this lane: the
+  // four chunk offsets below plus compile-time row offsets address all of them.
+  const int fsw = (frow >> 1) & 7;
+  const int choff[4] = {(h ^ fsw) << 4, ((2 + h) ^ fsw) << 4, ((4 + h) ^ fsw) << 4, ((6 + h) ^ fsw) << 4};
+  auto frag = [&](const uint8_t* buf, int tile_row0, int ks) -> v8i {
+    const uint8_t* base = buf + (tile_row0 + frow) * BK;
+    const uint4 lo = *reinterpret_cast<const uint4*>(base + choff[2 * ks]);
+    const uint4 hi = *reinterpret_cast<const uint4*>(base + choff[2 * ks + 1]);
+    v8i r;
+    r[0] = (int)lo.x; r[1] = (int)lo.y; r[2] = (int)lo.z; r[3] = (int)lo.w;
+    r[4] = (int)hi.x; r[5] = (int)hi.y; r[6] = (int)hi.z; r[7] = (int)hi.w;
+    return r;
+  };
+  // MX: the four UE8M0 codes of one row for K step kt (one dword; K/32 % 4 == 0).
+  uint32_t wsc[FN], asc[FM];
+  // MX codes via buffer loads as well: rows past M / N read zero codes (never stored).
+  const OperandWindow wcw = MODE == MODE_MX ? operand_window(n_base + (wave_u >> 1) * 128, g.N, g.ld_sb) : OperandWindow{0, 0};
+  const OperandWindow acw = MODE == MODE_MX ? operand_window(m_base + (wave_u & 1) * 128, g.M, g.ld_sa) : OperandWindow{0, 0};
+  const __amdgpu_buffer_rsrc_t wcode_rsrc = __builtin_amdgcn_make_buffer_rsrc(
+      const_cast<uint8_t*>(reinterpret_cast<const uint8_t*>(g.sb) + wcw.base_offset), (short)0, wcw.records, kBufferFlags);
+  const __amdgpu_buffer_rsrc_t acode_rsrc = __builtin_amdgcn_make_buffer_rsrc(
+      const_cast<uint8_t*>(reinterpret_cast<const uint8_t*>(g.sa) + acw.base_offset), (short)0, acw.records, kBufferFlags);
+  auto load_mx_codes = [&](int kt) {
+    if constexpr (MODE == MODE_MX) {
+#pragma unroll
+      for (int i = 0; i < FN; ++i)
+        wsc[i] = (uint32_t)__builtin_amdgcn_raw_buffer_load_b32(wcode_rsrc, (int)((i * 32 + frow) * g.ld_sb), kt * 4, 0);
+#pragma unroll
+      for (int j = 0; j < FM; ++j)
+        asc[j] = (uint32_t)__builtin_amdgcn_raw_buffer_load_b32(acode_rsrc, (int)((j * 32 + frow) * g.ld_sa), kt * 4, 0);
+    }
+  };
+
+  // Declaring an AGPR clobber makes the compiler select the AGPR form of the MFMAs,
+  // so the 256 accumulators live in the accumulation registers and the 256
+  // architectural VGPRs stay free for fragments and addresses.
+  asm volatile("" ::: "a255");
+  v16f acc[FN][FM];
+#pragma unroll
+  for (int i = 0; i < FN; ++i)
+#pragma unroll
+    for (int j = 0; j < FM; ++j)
+#pragma unroll
+      for (int r = 0; r < 16; ++r) acc[i][j][r] = 0.0f;
+
+  // One K step from `cur` while the next step's loads stream into `nxt`. Fragments
+  // are double-buffered: the 64-K half ks+1 is read from LDS while the 16 MFMAs of
+  // half ks execute.
+  auto stage = [&](int kt, const uint8_t* cur, uint8_t* nxt) {
+    if (kt + 1 < nk) issue_stage(kt + 1, nxt);
+    uint32_t wcur[FN], acur[FM];
+#pragma unroll
+    for (int i = 0; i < FN; ++i) wcur[i] = wsc[i];
+#pragma unroll
+    for (int j = 0; j < FM; ++j) acur[j] = asc[j];
+    if (kt + 1 < nk) load_mx_codes(kt + 1);
+#pragma unroll
+    for (int ks = 0; ks < BK / 64; ++ks) {
+      v8i af[FM], wf[FN];
+#pragma unroll
+      for (int j = 0; j < FM; ++j) af[j] = frag(cur, kBigTile + wm * 128 + j * 32, ks);
+#pragma unroll
+      for (int i = 0; i < FN; ++i) wf[i] = frag(cur, wn * 128 + i * 32, ks);
+      const int shift = 8 * (ks * 2 + h);
+#pragma unroll
+      for (int i = 0; i < FN; ++i) {
+        const int sw = MODE == MODE_MX ? (int)((wcur[i] >> shift) & 0xFF) : kScaleOne;
+#pragma unroll
+        for (int j = 0; j < FM; ++j) {
+          const int sa = MODE == MODE_MX ? (int)((acur[j] >> shift) & 0xFF) : kScaleOne;
+          acc[i][j] = mfma(wf[i], af[j], acc[i][j], sw, sa);
+        }
+      }
+    }
+    __syncthreads();
+  };
+
+  // The loop body is the unconditional pair of steps (lds0, lds1): a conditional
+  // second step would make the accumulators a phi across a branch, and the compiler
+  // then copies all 256 of them between AGPRs and VGPRs every iteration. An odd step
+  // count peels the first step, staged in lds1.
+  const int k0 = nk & 1;
+  issue_stage(0, k0 ? lds1 : lds0);
+  load_mx_codes(0);
+  __syncthreads();
+  if (k0) stage(0, lds1, lds0);
+  for (int kt = k0; kt < nk; kt += 2) {
+    stage(kt, lds0, lds1);
+    stage(kt + 1, lds1, lds0);
+  }
+
+  if (g.out_dtype == AYK_BF16) big_epilogue<MODE, AYK_BF16>(g, acc, m_base + wm * 128, n_base + wn * 128);
+  else if (g.out_dtype == AYK_F16) big_epilogue<MODE, AYK_F16>(g, acc, m_base + wm * 128, n_base + wn * 128);
+  else big_epilogue<MODE, AYK_F32>(g, acc, m_base + wm * 128, n_base + wn * 128);
+}
+
+template <int MODE>
+int launch_big(GemmArgs g, hipStream_t st, const char* op) {
+  static_assert(MODE != MODE_BLOCK, "block scales use the general kernel");
+  g.tiles_m = (int)cdiv(g.M, kBigTile);
+  const int64_t tiles = (int64_t)g.tiles_m * cdiv(g.N, kBigTile);
+  if (tiles > 0x7FFFFFFF) return fail(AYK_EINVAL, "%s: problem too large", op);
+  hipLaunchKernelGGL((fp8_gemm_big_kernel<MODE>), dim3((unsigned)tiles), dim3(kThreads), 0, st, g);
+  return check_launch(op);
+}
+
 template <int MODE, int BN, int BM, int WN, int WM>
 int launch_cfg(GemmArgs g, hipStream_t st, const char* op) {
   g.tiles_m = (int)cdiv(g.M, BM);
@@ -295,6 +544,16 @@ int launch_cfg(GemmArgs g, hipStream_t st, const char* op) {
 
 template <int MODE>
 int launch_gemm(const GemmArgs& g, hipStream_t st, const char* op) {
+  // The large-tile kernel's epilogue needs fp32 scales, N % 4 == 0 and a 4-aligned
+  // output row stride; anything else runs the general kernel.
+  if constexpr (MODE != MODE_BLOCK) {
+  const bool big_ok = g.K % BK == 0 && g.M >= 256 && g.N >= 256 && g.N % 4 == 0 &&
+                      g.ldo % 4 == 0 && aligned16(g.out) &&
+                      (MODE == MODE_MX || (g.sa_dtype == AYK_F32 && g.sb_dtype == AYK_F32 &&
+                                           (!g.sb_vec || aligned16(g.sb)))) &&
+                      (g.bias == nullptr || (reinterpret_cast<uintptr_t>(g.bias) & 15) == 0);
+  if (big_ok) return launch_big<MODE>(g, st, op);
+  }
   if (g.M <= 32) return launch_cfg<MODE, 128, 32, 4, 1>(g, st, op);
   if (g.M <= 64) return launch_cfg<MODE, 128, 64, 2, 2>(g, st, op);
   return launch_cfg<MODE, 128, 128, 2, 2>(g, st, op);

@@ -85,7 +85,8 @@ def test_blockwise_gemv(gpu, n, k):
 
 
 # ------------------------------------------------------------------ W8A8 GEMMs
-MNK = [(8, 3072, 1024), (17, 300, 256), (64, 256, 384), (200, 1000, 1024), (256, 512, 2048), (129, 130, 528)]
+MNK = [(8, 3072, 1024), (17, 300, 256), (64, 256, 384), (200, 1000, 1024), (256, 512, 2048), (129, 130, 528),
+       (300, 520, 1024), (513, 772, 2048), (1024, 1024, 3584)]  # the last three take the 256x256 kernel
 
 
 @pytest.mark.parametrize("m,n,k", MNK)
@@ -140,7 +141,8 @@ def test_fp8_blockwise_mm(gpu, m, n, k, sdt, col_major):
     assert_linear_close(out, ref, "blockwise_mm")
 
 
-@pytest.mark.parametrize("m,n,k", [(1, 512, 1024), (1, 1000, 8192), (64, 256, 512), (100, 300, 1024), (512, 512, 2048), (33, 96, 96)])
+@pytest.mark.parametrize("m,n,k", [(1, 512, 1024), (1, 1000, 8192), (64, 256, 512), (100, 300, 1024), (512, 512, 2048), (33, 96, 96),
+                                   (300, 520, 1024), (777, 1028, 2048)])
 def test_mxfp8_scaled_mm(gpu, m, n, k):
     from ayaka.kernel.hip import mxfp8_scaled_mm
 
