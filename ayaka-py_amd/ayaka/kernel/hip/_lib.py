@@ -60,7 +60,8 @@ SIGNATURES: dict[str, list[Any]] = {
     "ayk_mxfp8_scaled_mm": [_p, _l, _p, _l, _p, _l, _p, _l, _l, _l, _l, _p, _i, _p, _i, _l, _p],
     "ayk_fp8_weight_only_gemv": [_p, _i, _p, _l, _l, _l, _p, _i, _l, _l, _l, _p, _p, _z, _p],
     "ayk_fp8_weight_only_gemv_workspace_bytes": [_l, _l],
-    "ayk_fp8_weight_only_gemm": [_p, _i, _l, _l, _p, _l, _l, _l, _p, _i, _l, _l, _l, _p, _l, _p],
+    "ayk_fp8_weight_only_gemm": [_p, _i, _l, _l, _p, _l, _l, _l, _p, _i, _l, _l, _l, _p, _l, _p, _z, _p],
+    "ayk_fp8_weight_only_gemm_workspace_bytes": [_l, _l, _l, _l],
     "ayk_fp8_blockwise_gemv": [_p, _p, _l, _l, _l, _p, _i, _p, _i, _p, _i, _p, _i, _p, _z, _p],
     "ayk_fp8_blockwise_gemv_workspace_bytes": [_l, _l],
 }
@@ -68,6 +69,7 @@ _RESTYPES: dict[str, Any] = {
     "ayk_last_error": ctypes.c_char_p,
     "ayk_fp8_weight_only_gemv_workspace_bytes": _z,
     "ayk_fp8_blockwise_gemv_workspace_bytes": _z,
+    "ayk_fp8_weight_only_gemm_workspace_bytes": _z,
 }
 
 _lock = threading.Lock()

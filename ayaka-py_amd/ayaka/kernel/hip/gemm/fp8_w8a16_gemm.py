@@ -87,12 +87,15 @@ def fp8_weight_only_gemm(
     x_k = _aligned_rows(input, 8)
     w_k = _aligned_rows(weight_view, 16)
     scale = weight_scale if weight_scale.is_contiguous() else weight_scale.contiguous()
+    nbytes = _lib.query("ayk_fp8_weight_only_gemm_workspace_bytes", rows, columns, inner, block_size_x)
+    ws = torch.empty(nbytes, dtype=torch.uint8, device=input.device) if nbytes else None
     _lib.call(
         "ayk_fp8_weight_only_gemm", x_k.data_ptr(), _lib.dtype_code(input.dtype),
         int(x_k.stride(0)) if rows > 1 else int(x_k.shape[1]), rows,
         w_k.data_ptr(), int(w_k.stride(0)) if columns > 1 else int(w_k.shape[1]), columns, inner,
         scale.data_ptr(), _SCALE_CODES[scale_dtype], scale_row_stride, block_size_y, block_size_x,
-        result.data_ptr(), int(result.stride(0)) if rows > 1 else columns, _lib.stream_of(input),
+        result.data_ptr(), int(result.stride(0)) if rows > 1 else columns,
+        _lib.ptr(ws), nbytes, _lib.stream_of(input),
     )
     return result
 

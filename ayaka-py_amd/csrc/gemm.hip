@@ -338,47 +338,99 @@ __device__ inline void store4_typed(const GemmArgs& g, int64_t m, int64_t n, con
   }
 }
 
-// Epilogue of the large-tile kernel for a 128 x 128 wavefront tile at (m0, n0):
-// per-row / per-column fp32 scales (SCALED), bias, one rounding, 4 consecutive n
-// per store. The fast path needs N % 4 == 0 and a 4-element-aligned output row
-// (checked by the launcher); rows / columns past M / N are skipped.
+// Epilogue of the large-tile kernel, staged through LDS (free once the K loop ends).
+// A lane's accumulators hold 4 consecutive n of one row m per store group, spread over
+// 32 rows per instruction; writing them straight to HBM costs one cache line per lane
+// pair. Instead, for each of the four 32-row MFMA slabs j, every wavefront scales,
+// biases and converts its values and writes them to a [64 m][256 n] LDS staging tile
+// (the two row halves come from wm = 0 / 1); then all 256 threads store that tile row by
+// row with 16-byte coalesced stores. Rows past M and columns past N are not stored
+// (N % 4 == 0 and a 4-aligned row stride are checked by the launcher).
+template <int OUT>
+struct OutBytes { static constexpr int v = OUT == AYK_F32 ? 4 : 2; };
+
 template <int MODE, int OUT>
-__device__ inline void big_epilogue(const GemmArgs& g, const v16f (&acc)[4][4], int64_t m0, int64_t n0) {
-  const int lane = threadIdx.x & 63, h = lane >> 5, frow = lane & 31;
+__device__ inline void big_epilogue(const GemmArgs& g, const v16f (&acc)[4][4], int64_t m_tile, int64_t n_tile,
+                                    uint8_t* stage_lds) {
+  constexpr int EB = OutBytes<OUT>::v;
+  constexpr int kRowBytes = 256 * EB + 16;        // padded staging row
+  constexpr int kStageRows = EB == 4 ? 32 : 64;   // rows staged at once (fits 64 KB)
+  constexpr int kPasses = 64 / kStageRows;        // fp32: one pass per row half (wm)
+  static_assert(kStageRows * kRowBytes <= kBigStage, "staging tile must fit one LDS stage buffer");
+  const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+  const int wn = wave >> 1, wm = wave & 1, h = lane >> 5, frow = lane & 31;
   const float* sa_p = reinterpret_cast<const float*>(g.sa);
   const float* sb_p = reinterpret_cast<const float*>(g.sb);
 #pragma unroll
   for (int j = 0; j < 4; ++j) {
-    const int64_t m = m0 + j * 32 + frow;
-    const bool row_ok = m < g.M;
+    const int64_t m = m_tile + wm * 128 + j * 32 + frow;
     float sa = 1.0f;
-    if constexpr (MODE == MODE_SCALED) sa = sa_p[g.sa_vec ? (row_ok ? m : 0) : 0];
+    if constexpr (MODE == MODE_SCALED) sa = sa_p[g.sa_vec ? (m < g.M ? m : 0) : 0];
 #pragma unroll
-    for (int i = 0; i < 4; ++i) {
+    for (int pass = 0; pass < kPasses; ++pass) {
+      if (kPasses == 1 || wm == pass) {
+        uint8_t* srow = stage_lds + ((kPasses == 1 ? wm * 32 : 0) + frow) * kRowBytes;
 #pragma unroll
-      for (int grp = 0; grp < 4; ++grp) {
-        const int64_t n = n0 + i * 32 + grp * 8 + h * 4;
-        if (!row_ok || n >= g.N) continue;
-        float sb[4] = {1.0f, 1.0f, 1.0f, 1.0f};
-        if constexpr (MODE == MODE_SCALED) {
-          if (g.sb_vec) {
-            const float4 t = *reinterpret_cast<const float4*>(sb_p + n);
-            sb[0] = t.x; sb[1] = t.y; sb[2] = t.z; sb[3] = t.w;
-          } else {
-            sb[0] = sb[1] = sb[2] = sb[3] = sb_p[0];
+        for (int i = 0; i < 4; ++i) {
+#pragma unroll
+          for (int grp = 0; grp < 4; ++grp) {
+            const int nl = wn * 128 + i * 32 + grp * 8 + h * 4;  // column within the tile
+            const int64_t n = n_tile + nl;
+            float sb[4] = {1.0f, 1.0f, 1.0f, 1.0f};
+            float bias[4] = {0.0f, 0.0f, 0.0f, 0.0f};
+            if (n < g.N) {
+              if constexpr (MODE == MODE_SCALED) {
+                if (g.sb_vec) {
+                  const float4 t = *reinterpret_cast<const float4*>(sb_p + n);
+                  sb[0] = t.x; sb[1] = t.y; sb[2] = t.z; sb[3] = t.w;
+                } else {
+                  sb[0] = sb[1] = sb[2] = sb[3] = sb_p[0];
+                }
+              }
+              if (g.bias) load_bias4(g, n, bias);
+            }
+            float v[4];
+#pragma unroll
+            for (int qq = 0; qq < 4; ++qq) {
+              float y = acc[i][j][grp * 4 + qq];
+              if constexpr (MODE == MODE_SCALED) y = (y * sa) * sb[qq];
+              v[qq] = y + bias[qq];
+            }
+            if constexpr (OUT == AYK_F32) {
+              *reinterpret_cast<float4*>(srow + nl * 4) = make_float4(v[0], v[1], v[2], v[3]);
+            } else {
+              uint16_t b[4];
+#pragma unroll
+              for (int qq = 0; qq < 4; ++qq) b[qq] = OUT == AYK_BF16 ? f32_to_bf16_bits(v[qq]) : f32_to_f16_bits(v[qq]);
+              *reinterpret_cast<uint2*>(srow + nl * 2) =
+                  make_uint2((uint32_t)b[0] | ((uint32_t)b[1] << 16), (uint32_t)b[2] | ((uint32_t)b[3] << 16));
+            }
           }
         }
-        float bias[4] = {0.0f, 0.0f, 0.0f, 0.0f};
-        if (g.bias) load_bias4(g, n, bias);
-        float v[4];
-#pragma unroll
-        for (int qq = 0; qq < 4; ++qq) {
-          float y = acc[i][j][grp * 4 + qq];
-          if constexpr (MODE == MODE_SCALED) y = (y * sa) * sb[qq];
-          v[qq] = y + bias[qq];
-        }
-        store4_typed<OUT>(g, m, n, v);
       }
+      __syncthreads();
+      // Staged row r: with one pass, r < 32 is tile row j*32 + r (wm = 0) and r >= 32
+      // is 128 + j*32 + (r - 32) (wm = 1); with two passes, pass*128 + j*32 + r.
+      constexpr int kChunksPerRow = 256 * EB / 16;
+      constexpr int kRowsPerStep = 256 / kChunksPerRow;
+#pragma unroll
+      for (int r0 = 0; r0 < kStageRows; r0 += kRowsPerStep) {
+        const int r = r0 + tid / kChunksPerRow;
+        const int c = tid % kChunksPerRow;
+        const int tile_row = kPasses == 1 ? (r < 32 ? j * 32 + r : 128 + j * 32 + (r - 32)) : pass * 128 + j * 32 + r;
+        const int64_t gm = m_tile + tile_row;
+        const int64_t gn = n_tile + (int64_t)c * (16 / EB);
+        if (gm < g.M && gn < g.N) {
+          const uint4 val = *reinterpret_cast<const uint4*>(stage_lds + r * kRowBytes + c * 16);
+          uint8_t* dst = reinterpret_cast<uint8_t*>(g.out) + (gm * g.ldo + gn) * EB;
+          if (gn + 16 / EB <= g.N) {
+            *reinterpret_cast<uint4*>(dst) = val;
+          } else {  // N % 4 == 0: the first 8 bytes of the chunk are in range
+            *reinterpret_cast<uint2*>(dst) = make_uint2(val.x, val.y);
+          }
+        }
+      }
+      __syncthreads();
     }
   }
 }
@@ -475,14 +527,22 @@ __global__ __launch_bounds__(kThreads, 1) void fp8_gemm_big_kernel(GemmArgs g) {
   // One K step from `cur` while the next step's loads stream into `nxt`. Fragments
   // are double-buffered: the 64-K half ks+1 is read from LDS while the 16 MFMAs of
   // half ks execute.
+  //
+  // The body has no branches: the next step's loads are issued unconditionally (the
+  // last step re-loads itself into the buffer nobody reads again), so the whole loop
+  // body is one basic block and the MFMAs cannot be moved below the barrier.
   auto stage = [&](int kt, const uint8_t* cur, uint8_t* nxt) {
-    if (kt + 1 < nk) issue_stage(kt + 1, nxt);
+    const int kn = kt + 1 < nk ? kt + 1 : kt;
     uint32_t wcur[FN], acur[FM];
 #pragma unroll
     for (int i = 0; i < FN; ++i) wcur[i] = wsc[i];
 #pragma unroll
     for (int j = 0; j < FM; ++j) acur[j] = asc[j];
-    if (kt + 1 < nk) load_mx_codes(kt + 1);
+    issue_stage(kn, nxt);
+    load_mx_codes(kn);
+    // Keep the next step's loads at the top of the step (the scheduler would otherwise
+    // sink them next to the barrier that waits for them).
+    __builtin_amdgcn_sched_barrier(0);
 #pragma unroll
     for (int ks = 0; ks < BK / 64; ++ks) {
       v8i af[FM], wf[FN];
@@ -501,6 +561,10 @@ __global__ __launch_bounds__(kThreads, 1) void fp8_gemm_big_kernel(GemmArgs g) {
         }
       }
     }
+    // MFMAs touch no memory, so the compiler may sink them below the barrier, whose
+    // wait for all loads would then stall on the loads just issued for the next step
+    // before any MFMA of this step. Pin them above it.
+    __builtin_amdgcn_sched_barrier(0);
     __syncthreads();
   };
 
@@ -518,9 +582,11 @@ __global__ __launch_bounds__(kThreads, 1) void fp8_gemm_big_kernel(GemmArgs g) {
     stage(kt + 1, lds1, lds0);
   }
 
-  if (g.out_dtype == AYK_BF16) big_epilogue<MODE, AYK_BF16>(g, acc, m_base + wm * 128, n_base + wn * 128);
-  else if (g.out_dtype == AYK_F16) big_epilogue<MODE, AYK_F16>(g, acc, m_base + wm * 128, n_base + wn * 128);
-  else big_epilogue<MODE, AYK_F32>(g, acc, m_base + wm * 128, n_base + wn * 128);
+  // The last step's barrier guarantees no wavefront still reads lds0 / lds1 and every
+  // direct load has landed (the last issue re-loaded a step into the idle buffer).
+  if (g.out_dtype == AYK_BF16) big_epilogue<MODE, AYK_BF16>(g, acc, m_base, n_base, lds0);
+  else if (g.out_dtype == AYK_F16) big_epilogue<MODE, AYK_F16>(g, acc, m_base, n_base, lds0);
+  else big_epilogue<MODE, AYK_F32>(g, acc, m_base, n_base, lds0);
 }
 
 template <int MODE>
@@ -544,11 +610,13 @@ int launch_cfg(GemmArgs g, hipStream_t st, const char* op) {
 
 template <int MODE>
 int launch_gemm(const GemmArgs& g, hipStream_t st, const char* op) {
-  // The large-tile kernel's epilogue needs fp32 scales, N % 4 == 0 and a 4-aligned
-  // output row stride; anything else runs the general kernel.
+  // The large-tile kernel needs K % 128 == 0, fp32 scales, N % 4 == 0 and 16-byte
+  // aligned output rows (its epilogue stores 16-byte chunks); anything else runs the
+  // general kernel.
   if constexpr (MODE != MODE_BLOCK) {
+  const int64_t out_bytes = g.out_dtype == AYK_F32 ? 4 : 2;
   const bool big_ok = g.K % BK == 0 && g.M >= 256 && g.N >= 256 && g.N % 4 == 0 &&
-                      g.ldo % 4 == 0 && aligned16(g.out) &&
+                      (g.ldo * out_bytes) % 16 == 0 && aligned16(g.out) &&
                       (MODE == MODE_MX || (g.sa_dtype == AYK_F32 && g.sb_dtype == AYK_F32 &&
                                            (!g.sb_vec || aligned16(g.sb)))) &&
                       (g.bias == nullptr || (reinterpret_cast<uintptr_t>(g.bias) & 15) == 0);

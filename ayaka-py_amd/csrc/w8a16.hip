@@ -211,6 +211,278 @@ __global__ __launch_bounds__(kThreads) void w8a16_gemm_kernel(W16Args g) {
   }
 }
 
+// ---------------------------------------------------------------------------------
+// Decode W8A16 for 2 <= M <= 32: HBM-bound, so the design is the GEMV's (stream each
+// weight byte once with 16-byte loads, fill the CUs with a K split) with the M
+// activation rows multiplied on matrix cores instead of VALU FMAs.
+//
+// A workgroup of four wavefronts owns 128 weight rows over one K range. Its
+// activation slice x[0:M, K range] (and, for block scales, the scales of its rows
+// and K range) is staged once in LDS, so that inside the main loop only weight loads
+// use the vector-memory counter: that counter retires in issue order, so any other
+// global load issued behind the weight prefetch would have to wait for it.
+//
+// A wavefront owns 32 rows. Per 128-K step a lane loads four 16-byte pieces of its row
+// (lane half h = lane / 32 takes bytes 32c + 16h .. +16 of row lane % 32, c = 0..3);
+// D steps are in flight in a register ring. The loads are ordinary (L2-allocating):
+// one instruction covers only 32 bytes of each of 32 rows, and the four instructions
+// of a step complete each 128-byte line in L2, where a streaming hint would send the
+// pieces to HBM separately (measured: ~1.8x slower). Each weight is dequantized (w * scale)
+// and rounded to the activation dtype before the product, as the reference's W8A16
+// kernel does, and feeds v_mfma_f32_32x32x16_{bf16,f16} as A, against B = the
+// activation rows read from LDS in the same K order (B columns m >= M repeat row
+// M - 1 and their D columns are never stored). K-split partials [split, M, N] are
+// summed in a fixed order by the reduce kernel.
+
+constexpr int kSkRows = 128;          // weight rows per workgroup (4 wavefronts x 32)
+constexpr int kSkLdsBudget = 80 * 1024;  // two workgroups per CU
+
+// LDS bytes of the staged activation slice (`pitch` elements per row): whole
+// 64-vector groups, the unit of one direct-to-LDS wavefront load.
+__host__ __device__ inline size_t x_lds_bytes(int64_t M, int pitch) {
+  return (size_t)((M * (pitch / 8) + 63) / 64) * 64 * 16;
+}
+
+struct SkinnyArgs {
+  const uint16_t* x;
+  int64_t ldx;
+  int64_t M;
+  const uint8_t* w;
+  int64_t ldw;
+  int64_t N, K;
+  const void* scale;
+  int scale_dtype;
+  int64_t srs, by, bx;
+  uint16_t* out;
+  int64_t ldo;
+  float* part;          // [split, M, N] when gridDim.y > 1
+  int64_t k_per_split;  // multiple of D * 128
+  int x_pitch;          // LDS row pitch of the activation slice, elements
+  int s_cols;           // LDS scale columns per row (block scales)
+};
+
+// Eight e4m3 bytes (two dwords) -> the eight products w * s rounded to 16-bit floats.
+template <bool BF16>
+__device__ inline v8s convert8(uint32_t lo, uint32_t hi, float s) {
+  float f[8];
+  e4m3x4_to_f32(lo, f);
+  e4m3x4_to_f32(hi, f + 4);
+  v8s r;
+#pragma unroll
+  for (int e = 0; e < 8; ++e) {
+    const float v = f[e] * s;
+    if constexpr (BF16) r[e] = (short)__builtin_bit_cast(uint16_t, (__bf16)v);
+    else r[e] = (short)__builtin_bit_cast(uint16_t, (_Float16)v);
+  }
+  return r;
+}
+
+template <bool BF16, bool ROW_SCALE, int D>
+__global__ __launch_bounds__(256) void w8a16_skinny_kernel(SkinnyArgs a) {
+  extern __shared__ __attribute__((aligned(16))) uint8_t sk_lds[];
+  uint16_t* xs = reinterpret_cast<uint16_t*>(sk_lds);
+  float* ss = reinterpret_cast<float*>(sk_lds + x_lds_bytes(a.M, a.x_pitch));
+  const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+  const int h = lane >> 5, lr = lane & 31;
+  const int64_t nwg = (int64_t)blockIdx.x * kSkRows;
+  const int64_t n0 = nwg + wave * 32;
+  const int64_t kbeg = (int64_t)blockIdx.y * a.k_per_split;
+  const int64_t kend = min(a.K, kbeg + a.k_per_split);
+  const int klen = (int)(kend - kbeg);
+
+  const int64_t nrow = min(n0 + lr, a.N - 1);  // rows past N re-read row N - 1
+  const uint8_t* wrow = a.w + nrow * a.ldw + h * 16;
+  uint4 ring[D][4];
+  auto load = [&](int d, int64_t k) {
+#pragma unroll
+    for (int c = 0; c < 4; ++c) ring[d][c] = *reinterpret_cast<const uint4*>(wrow + k + c * 32);
+  };
+  // The first D weight steps go out before the staging below, so that their HBM
+  // latency overlaps it.
+#pragma unroll
+  for (int d = 0; d < D; ++d) load(d, kbeg + d * 128);
+
+  // Stage the activation slice with direct-to-LDS loads (no staging registers): one
+  // wavefront instruction fills 64 consecutive 16-byte LDS vectors; vector p of the
+  // padded layout holds x[p / pv][kbeg + 8 * (p % pv) ..] (pv = klen / 8 + 1 vectors
+  // per row, the last one padding, which - like vectors past the last row - is
+  // filled from a clamped, valid address).
+  {
+    const int pv = a.x_pitch / 8, vpr = klen / 8;
+    const int total = (int)a.M * pv;
+    for (int p0 = wave * 64; p0 < total; p0 += 256) {
+      const int p = min(p0 + lane, total - 1);
+      const int m = p / pv, c = min(p - m * pv, vpr - 1);
+      __builtin_amdgcn_global_load_lds(
+          reinterpret_cast<const void*>(a.x + m * a.ldx + kbeg + c * 8),
+          (__attribute__((address_space(3))) void*)(sk_lds + (size_t)__builtin_amdgcn_readfirstlane(p0) * 16), 16, 0, 0);
+    }
+  }
+  if constexpr (!ROW_SCALE) {
+    const int64_t c0 = kbeg / a.bx, cmax = (a.K - 1) / a.bx;
+    for (int i = tid; i < kSkRows * a.s_cols; i += 256) {
+      const int r = i / a.s_cols, c = i - r * a.s_cols;
+      const int64_t n = min(nwg + r, a.N - 1);
+      ss[i] = load_f32(a.scale, a.scale_dtype, (n / a.by) * a.srs + min(c0 + c, cmax));
+    }
+  }
+  __syncthreads();
+  if (n0 >= a.N) return;  // whole wavefront past N (uniform; no barrier follows)
+
+  const float row_s = ROW_SCALE ? load_f32(a.scale, a.scale_dtype, (nrow / a.by) * a.srs) : 1.0f;
+  const uint16_t* xrow = xs + min(lr, (int)a.M - 1) * a.x_pitch + h * 16;
+  const float* srow = ss + (wave * 32 + lr) * a.s_cols;
+  const uint32_t bx = (uint32_t)a.bx;
+  const uint32_t c0 = (uint32_t)(kbeg / a.bx);
+
+  v16f acc;
+#pragma unroll
+  for (int r = 0; r < 16; ++r) acc[r] = 0.0f;
+  auto step = [&](int d, int kl) {  // kl: K offset of the step within the slice
+#pragma unroll
+    for (int c = 0; c < 4; ++c) {
+      const int kc = kl + c * 32;
+      const uint4 xa = *reinterpret_cast<const uint4*>(xrow + kc);
+      const uint4 xb = *reinterpret_cast<const uint4*>(xrow + kc + 8);
+      float s = row_s;
+      // 16 consecutive K of a lane share one scale (bx % 32 == 0, checked on the host)
+      if constexpr (!ROW_SCALE) s = srow[(uint32_t)(kbeg + kc + h * 16) / bx - c0];
+      const v8s w0 = convert8<BF16>(ring[d][c].x, ring[d][c].y, s);
+      const v8s w1 = convert8<BF16>(ring[d][c].z, ring[d][c].w, s);
+      acc = mfma16<BF16>(w0, __builtin_bit_cast(v8s, xa), acc);
+      acc = mfma16<BF16>(w1, __builtin_bit_cast(v8s, xb), acc);
+    }
+  };
+
+  // klen is a multiple of D * 128: a steady loop that refills every slot it
+  // consumes, then a final round without refills.
+  int kl = 0;
+  for (; kl + D * 128 < klen; kl += D * 128) {
+#pragma unroll
+    for (int d = 0; d < D; ++d) {
+      step(d, kl + d * 128);
+      load(d, kbeg + kl + (D + d) * 128);
+    }
+  }
+#pragma unroll
+  for (int d = 0; d < D; ++d) step(d, kl + d * 128);
+
+  // D[n][m]: lane holds m = lr and n = n0 + 8*(r/4) + 4*h + r%4.
+  if (lr >= a.M) return;
+#pragma unroll
+  for (int grp = 0; grp < 4; ++grp) {
+    const int64_t nb = n0 + grp * 8 + h * 4;
+#pragma unroll
+    for (int q = 0; q < 4; ++q) {
+      const int64_t n = nb + q;
+      if (n >= a.N) continue;
+      if (gridDim.y == 1) a.out[lr * a.ldo + n] = round16<BF16>(acc[grp * 4 + q]);
+      else a.part[((int64_t)blockIdx.y * a.M + lr) * a.N + n] = acc[grp * 4 + q];
+    }
+  }
+}
+
+// Fixed-order sum over the K split, one rounding. Eight partials are loaded before
+// any is added (the adds stay in split order), so the loads overlap.
+template <bool BF16>
+__global__ __launch_bounds__(256) void w8a16_skinny_reduce(SkinnyArgs a, int split) {
+  const int64_t i = (int64_t)blockIdx.x * 256 + threadIdx.x;
+  const int64_t mn = a.M * a.N;
+  if (i >= mn) return;
+  const float* p = a.part + i;
+  float v = 0.0f;
+  int s = 0;
+  for (; s + 8 <= split; s += 8) {
+    float t[8];
+#pragma unroll
+    for (int j = 0; j < 8; ++j) t[j] = p[(int64_t)(s + j) * mn];
+#pragma unroll
+    for (int j = 0; j < 8; ++j) v += t[j];
+  }
+  for (; s < split; ++s) v += p[(int64_t)s * mn];
+  const int64_t m = i / a.N, n = i - m * a.N;
+  a.out[m * a.ldo + n] = round16<BF16>(v);
+}
+
+// Launch plan, a function of the shapes and the scale block width only (the
+// workspace query must reproduce it). The K split is the smallest power of two giving
+// >= 1024 wavefronts (each keeps D * 4 KiB of weights in flight); more splits cost
+// more partial-sum traffic than they gain (measured on Llama-3-8B shapes).
+struct SkinnyPlan {
+  bool ok;         // shape supported by the skinny kernel
+  int depth;       // D: 128-K steps in flight
+  int split;       // K split (grid.y)
+  int64_t kps;     // K per split, multiple of depth * 128
+  int x_pitch;     // elements
+  int s_cols;      // 0 for a per-row scale
+  size_t lds;      // dynamic LDS bytes
+};
+SkinnyPlan skinny_plan(int64_t M, int64_t N, int64_t K, int64_t bx) {
+  SkinnyPlan p{};
+  const bool row_scale = bx >= K;
+  if (M < 1 || M > 32 || N < 1 || K < 128 || K % 128 || (!row_scale && bx % 32)) return p;
+  p.depth = K % 512 == 0 ? 4 : (K % 256 == 0 ? 2 : 1);
+  const int64_t unit = 128 * p.depth, units = K / unit;
+  auto lds_for = [&](int64_t kps, int& pitch, int& cols) {
+    pitch = (int)kps + 8;  // 16-byte pad: rows start on distinct LDS banks
+    cols = row_scale ? 0 : (int)(kps / bx + 2);
+    return x_lds_bytes(M, pitch) + (size_t)kSkRows * cols * 4;
+  };
+  const int64_t waves = cdiv(N, 32);
+  int64_t split = 1;
+  while (waves * split < 1024 && split * 2 <= units) split *= 2;
+  for (;;) {
+    const int64_t kps = cdiv(units, split) * unit;
+    const size_t lds = lds_for(kps, p.x_pitch, p.s_cols);
+    if (lds <= (size_t)kSkLdsBudget) {
+      p.kps = kps;
+      p.lds = lds;
+      p.split = (int)cdiv(K, kps);
+      p.ok = true;
+      return p;
+    }
+    if (split >= units) return p;
+    split *= 2;
+  }
+}
+
+size_t skinny_workspace(const SkinnyPlan& p, int64_t M, int64_t N) {
+  return p.ok && p.split > 1 ? (size_t)p.split * (size_t)M * (size_t)N * sizeof(float) : 0;
+}
+
+template <bool BF16, bool ROW_SCALE>
+void launch_skinny_kernel(const SkinnyPlan& p, const SkinnyArgs& a, hipStream_t st) {
+  const dim3 grid((unsigned)cdiv(a.N, kSkRows), (unsigned)p.split);
+  const unsigned lds = (unsigned)p.lds;
+  switch (p.depth) {
+    case 4: hipLaunchKernelGGL((w8a16_skinny_kernel<BF16, ROW_SCALE, 4>), grid, dim3(256), lds, st, a); break;
+    case 2: hipLaunchKernelGGL((w8a16_skinny_kernel<BF16, ROW_SCALE, 2>), grid, dim3(256), lds, st, a); break;
+    default: hipLaunchKernelGGL((w8a16_skinny_kernel<BF16, ROW_SCALE, 1>), grid, dim3(256), lds, st, a); break;
+  }
+}
+
+template <bool BF16>
+int launch_skinny(const SkinnyPlan& p, SkinnyArgs a, size_t ws_bytes, hipStream_t st) {
+  a.k_per_split = p.kps;
+  a.x_pitch = p.x_pitch;
+  a.s_cols = p.s_cols;
+  if (p.split > 1) {
+    const size_t need = skinny_workspace(p, a.M, a.N);
+    if (a.part == nullptr || ws_bytes < need) {
+      return fail(AYK_EWORKSPACE, "fp8_weight_only_gemm: workspace of %zu bytes required, %zu given", need, ws_bytes);
+    }
+  }
+  if (p.s_cols == 0) launch_skinny_kernel<BF16, true>(p, a, st);
+  else launch_skinny_kernel<BF16, false>(p, a, st);
+  if (int rc = check_launch("fp8_weight_only_gemm")) return rc;
+  if (p.split > 1) {
+    const dim3 rg((unsigned)cdiv(a.M * a.N, 256));
+    hipLaunchKernelGGL((w8a16_skinny_reduce<BF16>), rg, dim3(256), 0, st, a, p.split);
+    return check_launch("fp8_weight_only_gemm");
+  }
+  return AYK_OK;
+}
+
 template <bool BF16, int BN, int BM, int WN, int WM>
 int launch_w16(W16Args g, hipStream_t st) {
   g.tiles_m = (int)cdiv(g.M, BM);
@@ -234,10 +506,16 @@ using namespace ayk;
 
 extern "C" {
 
+size_t ayk_fp8_weight_only_gemm_workspace_bytes(int64_t M, int64_t N, int64_t K, int64_t block_size_x) {
+  if (M < 2) return 0;
+  return skinny_workspace(skinny_plan(M, N, K, block_size_x), M, N);
+}
+
 int ayk_fp8_weight_only_gemm(const void* x, int x_dtype, int64_t ldx, int64_t M, const void* w,
                              int64_t ldw, int64_t N, int64_t K, const void* scale, int scale_dtype,
                              int64_t scale_row_stride, int64_t block_size_y, int64_t block_size_x,
-                             void* out, int64_t ldo, ayk_stream_t stream) {
+                             void* out, int64_t ldo, void* workspace, size_t workspace_bytes,
+                             ayk_stream_t stream) {
   const char* op = "fp8_weight_only_gemm";
   if (x_dtype != AYK_BF16 && x_dtype != AYK_F16) return fail(AYK_EINVAL, "%s: input must be float16 or bfloat16", op);
   if (scale_dtype != AYK_U8 && scale_dtype != AYK_F32 && scale_dtype != AYK_BF16) {
@@ -266,6 +544,19 @@ int ayk_fp8_weight_only_gemm(const void* x, int x_dtype, int64_t ldx, int64_t M,
   g.out = static_cast<uint16_t*>(out);
   g.ldo = ldo;
   hipStream_t st = static_cast<hipStream_t>(stream);
+  // Decode batch sizes: the skinny streaming kernel (whole 128-K steps, scale blocks
+  // of >= 32 K, activation rows 16-byte aligned).
+  if (M >= 2 && ldx % 8 == 0) {
+    const SkinnyPlan p = skinny_plan(M, N, K, block_size_x);
+    if (p.ok) {
+      SkinnyArgs a{};
+      a.x = g.x; a.ldx = ldx; a.M = M; a.w = g.w; a.ldw = ldw; a.N = N; a.K = K;
+      a.scale = scale; a.scale_dtype = scale_dtype; a.srs = scale_row_stride; a.by = block_size_y; a.bx = block_size_x;
+      a.out = g.out; a.ldo = ldo; a.part = static_cast<float*>(workspace);
+      return x_dtype == AYK_BF16 ? launch_skinny<true>(p, a, workspace_bytes, st)
+                                 : launch_skinny<false>(p, a, workspace_bytes, st);
+    }
+  }
   return x_dtype == AYK_BF16 ? dispatch_w16<true>(g, st) : dispatch_w16<false>(g, st);
 }
 

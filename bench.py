@@ -170,6 +170,36 @@ def _bench_gemm(device, reps=10):
     return results
 
 
+def _bench_decode_m(layers, reps=20):
+    """W8A16 at the other Cfg2 decode batch sizes (M = 4, 16, 32): GB/s per projection
+    (algorithmic bytes: fp8 weights + scales + bf16 x and out), each launch timed in a
+    graph of back-to-back launches rotating the weight copies."""
+    from ayaka.kernel.hip import fp8_weight_only_gemm
+
+    out = {}
+    for m in (4, 16, 32):
+        row = {}
+        for name, n, k, copies, x in layers:
+            xm = x.reshape(1, k).repeat(m, 1).contiguous()
+            y = torch.empty(m, n, dtype=torch.bfloat16, device=x.device)
+
+            def launches():
+                for i in range(reps):
+                    w, s = copies[i % COPIES]
+                    fp8_weight_only_gemm(xm, w, s.reshape(n, 1), 1, 1, k, "float32", out=y)
+
+            graph = _capture(launches)
+            start, end = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+            start.record()
+            graph.replay()
+            end.record()
+            end.synchronize()
+            us = start.elapsed_time(end) * 1e3 / reps
+            row[name] = {"us": round(us, 2), "gbs": round(_gemv_bytes(n, k, m) / (us * 1e-6) / 1e9, 1)}
+        out[f"M={m}"] = row
+    return out
+
+
 def _cpu_baseline():
     """The reference's CPU path (oracle restatement) on one Cfg2 M = 1 pass."""
     from oracle import fp8_oracle as ora
@@ -268,6 +298,7 @@ def main() -> int:
                      "avg_launch_us": round(avg_ms * 1e3, 2), "median_launch_us": round(med_ms * 1e3, 2),
                      "bytes_per_launch": _gemv_bytes(n, k), "traffic": None},
     }
+    result["decode_w8a16"] = _bench_decode_m(layers)
     if not args.no_gemm:
         result["gemm"] = _bench_gemm(device)
     if not args.no_cpu:

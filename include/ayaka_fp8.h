@@ -135,12 +135,19 @@ size_t ayk_fp8_weight_only_gemv_workspace_bytes(int64_t N, int64_t K);
 /* Replaces ayaka::fp8_weight_only_gemm (gemm/fp8_w8a16_gemm.py:144; oracle
  * reference/gemm.py:95-126). The [M, K] form of ayk_fp8_weight_only_gemv; out dtype ==
  * x dtype. Each dequantized weight w * scale is rounded to the activation dtype before
- * the product, as the reference does. */
+ * the product, as the reference does (with a per-row scale, block_size_x >= K, the
+ * exact fp8 weight enters the product and the scale multiplies the fp32 sum).
+ * Decode batches (M <= 32) may use a K split whose partials live in the workspace;
+ * ayk_fp8_weight_only_gemm_workspace_bytes(M, N, K, block_size_x) gives its size
+ * (0: none needed). */
 int ayk_fp8_weight_only_gemm(const void* x, int x_dtype, int64_t ldx, int64_t M,
                              const void* w, int64_t ldw, int64_t N, int64_t K,
                              const void* scale, int scale_dtype, int64_t scale_row_stride,
                              int64_t block_size_y, int64_t block_size_x,
-                             void* out, int64_t ldo, ayk_stream_t stream);
+                             void* out, int64_t ldo, void* workspace, size_t workspace_bytes,
+                             ayk_stream_t stream);
+size_t ayk_fp8_weight_only_gemm_workspace_bytes(int64_t M, int64_t N, int64_t K,
+                                                int64_t block_size_x);
 
 /* Replaces ayaka::fp8_blockwise_gemv (gemm/fp8_gemv.py:433; oracle reference/gemm.py:160-189).
  * out[n] = sum_kb (a[kb] . b[n, kb]) * scale_a[kb] * scale_b[n / 128, kb] + bias[n],

@@ -110,6 +110,26 @@ def test_fp8_scaled_mm(gpu, m, n, k, rowwise):
     assert_linear_close(out, ref, "fp8_scaled_mm bf16")
 
 
+@pytest.mark.parametrize("out_dtype", [torch.float16, torch.bfloat16, torch.float32])
+def test_fp8_scaled_mm_big_tile_strided_out(gpu, out_dtype):
+    """256x256-tile kernel: every output dtype, a padded output row stride, M/N tails."""
+    from ayaka.kernel.hip import fp8_scaled_mm
+
+    m, n, k = 520, 1284, 1280
+    _say(f"fp8_scaled_mm big tile out={out_dtype}")
+    a = _fp8((m, k), seed=21, scale=40)
+    w = _fp8((n, k), seed=22, scale=40)
+    sa = torch.rand(m, generator=_gen(1)) * 0.01 + 1e-3
+    sb = torch.rand(n, generator=_gen(2)) * 0.01 + 1e-3
+    bias = torch.randn(n, generator=_gen(3))
+    ref = ora.fp8_scaled_mm(a, w, sa, sb, bias)
+    buf = torch.full((m, n + 12), 7.0, dtype=out_dtype, device=gpu)  # row stride n + 12
+    out = buf[:, :n]
+    fp8_scaled_mm(a.to(gpu), w.to(gpu).t(), sa.to(gpu), sb.to(gpu), bias.to(gpu), out=out)
+    assert_linear_close(out, ref, f"big tile {out_dtype}")
+    assert torch.all(buf[:, n:].float() == 7.0), "wrote past the output columns"
+
+
 def test_fp8_scaled_mm_row_major_b_and_odd_k(gpu):
     from ayaka.kernel.hip import fp8_scaled_mm
 
@@ -215,3 +235,34 @@ def test_fp8_linear_entry_points(gpu, m, recipe):
         y2 = fp8_pertensor_linear(x.to(gpu), w.to(gpu), scale.to(gpu), bias.to(gpu))
         ref2 = ora.fp8_linear("w8a16", x, w, scale.reshape(1, 1).expand(1, 1), bias, weight_block=(n, k))
         assert_linear_close(y2, ref2, "pertensor weight-only")
+
+
+@pytest.mark.parametrize(
+    "m,n,k,case,xdt",
+    [
+        (2, 600, 1152, "channel", torch.bfloat16),   # ragged N, uneven K split
+        (5, 4096, 4096, "block128", torch.bfloat16),  # split 1 shape family
+        (32, 96, 8192, "e8m0_32", torch.float16),     # deep split, partial last wave
+        (17, 8320, 256, "channel", torch.float16),    # many wavefronts, no split
+    ],
+)
+def test_weight_only_gemm_decode_shapes(gpu, m, n, k, case, xdt):
+    """Decode batches (M <= 32) take the K-split streaming kernel."""
+    from ayaka.kernel.hip import fp8_weight_only_gemm
+
+    _say(f"fp8_weight_only_gemm decode m={m} n={n} k={k} case={case} {xdt}")
+    w = _fp8((n, k), seed=11)
+    if case == "channel":
+        by, bx, sdt = 1, k, "float32"
+        scale = torch.rand(n, 1, generator=_gen(1)) * 0.01 + 1e-3
+    elif case == "block128":
+        by, bx, sdt = 128, 128, "float32"
+        scale = torch.rand(-(-n // 128), k // 128, generator=_gen(1)) * 0.01 + 1e-3
+    else:
+        by, bx, sdt = 1, 32, "e8m0"
+        scale = torch.randint(115, 125, (n, k // 32), generator=_gen(1), dtype=torch.uint8)
+    x = torch.randn(m, k, generator=_gen(2)).to(xdt)
+    y = fp8_weight_only_gemm(x.to(gpu), w.to(gpu), scale.to(gpu), -(-k // bx), by, bx, sdt)
+    ref = ora.fp8_weight_only_gemm(x, w, scale, -(-k // bx), by, bx, sdt)
+    assert y.dtype == xdt and y.shape == (m, n)
+    assert_linear_close(y, ref, "weight_only_gemm")
