@@ -159,6 +159,24 @@ __device__ inline float wave_sum(float v) {
   return v;
 }
 
+// Full-wavefront sum with DPP moves instead of LDS permutes: pairwise and quad swaps,
+// rotations within each 16-lane row, then the row broadcasts 15 and 31 carry row
+// totals upward; lane 63 ends with the sum, which is returned to every lane. The
+// addition order is fixed, so results are deterministic.
+template <int CTRL, int ROW_MASK>
+__device__ inline float dpp_move(float x) {
+  return __builtin_bit_cast(float, __builtin_amdgcn_update_dpp(0, __builtin_bit_cast(int, x), CTRL, ROW_MASK, 0xF, false));
+}
+__device__ inline float wave_sum_dpp(float v) {
+  v += dpp_move<0xB1, 0xF>(v);   // quad_perm [1,0,3,2]
+  v += dpp_move<0x4E, 0xF>(v);   // quad_perm [2,3,0,1]
+  v += dpp_move<0x124, 0xF>(v);  // row_ror:4
+  v += dpp_move<0x128, 0xF>(v);  // row_ror:8
+  v += dpp_move<0x142, 0xA>(v);  // row_bcast:15 into rows 1, 3
+  v += dpp_move<0x143, 0xC>(v);  // row_bcast:31 into rows 2, 3
+  return __builtin_bit_cast(float, __builtin_amdgcn_readlane(__builtin_bit_cast(int, v), 63));
+}
+
 // ---------------------------------------------------------------- misc helpers
 __host__ __device__ constexpr int64_t cdiv(int64_t a, int64_t b) { return (a + b - 1) / b; }
 

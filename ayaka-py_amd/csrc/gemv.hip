@@ -48,6 +48,8 @@ struct GemvArgs {
   int out_dtype;
   float* part;       // [split, N] partials when split > 1
   int64_t k_per_split;  // multiple of kWaveK
+  int64_t pairs_per_wave;  // streaming kernel: row pairs owned by one wavefront
+  int ws_is_f16;           // streaming kernel, 2-byte chunk scales: fp16 (1) or bf16 (0)
 };
 
 // Load the 16 activation values of chunk `c` (elements 16c .. 16c+15) as floats.
@@ -214,6 +216,177 @@ __global__ __launch_bounds__(kGemvThreads) void gemv_generic_kernel(GemvArgs a) 
   }
 }
 
+// ---------------------------------------------------------------------------------
+// Streaming GEMV: the main path when N is large enough to fill the GPU without a K
+// split. Each wavefront owns every W-th row pair (W = all wavefronts) and walks its
+// pairs' (pair, 1024-K sweep) items in order and keeps kRing
+// items of weight loads in flight in a register ring, across row boundaries, so the
+// memory pipeline never drains between rows. Everything else an item needs is staged
+// once per workgroup in LDS (x, activation scales, row scales, bias) or travels in the
+// ring beside its weights (chunk scales): the vector-memory counter retires loads in
+// issue order, so a load issued behind the prefetch would wait for all of it.
+constexpr int kStreamThreads = 256;
+constexpr int kStreamWaves = kStreamThreads / kWave;
+constexpr int kRing = 4;   // items in flight per wavefront (2 rows x 16 B per lane each; 4 measured best)
+constexpr int kPair = 2;   // rows per item
+constexpr int kStreamLdsMax = 64 * 1024;
+
+template <int SZ>
+__device__ inline uint32_t load_scale_bits(const void* p, int64_t i) {
+  if constexpr (SZ == 1) return reinterpret_cast<const uint8_t*>(p)[i];
+  else if constexpr (SZ == 2) return reinterpret_cast<const uint16_t*>(p)[i];
+  else return reinterpret_cast<const uint32_t*>(p)[i];
+}
+template <int SZ>
+__device__ inline float decode_scale_bits(uint32_t b, int is_f16) {
+  if constexpr (SZ == 1) return e8m0_decode(b);
+  else if constexpr (SZ == 2) return is_f16 ? f16_bits_to_f32((uint16_t)b) : bf16_bits_to_f32((uint16_t)b);
+  else return u2f(b);
+}
+
+// LDS plan of the streaming kernel (shared by host and device).
+struct StreamLds {
+  int x_bytes;      // staged activation, padded to whole 1 KiB direct-load groups
+  int as_count;     // activation scales (floats)
+  int rows;         // rows per workgroup (row scales and bias, floats each)
+  __host__ __device__ int total() const { return x_bytes + 4 * as_count + 8 * rows; }
+};
+__host__ __device__ inline StreamLds stream_lds(int act, int as, int64_t K, int64_t ppw) {
+  StreamLds l;
+  const int64_t xb = act == 2 ? K : 2 * K;
+  l.x_bytes = (int)((xb + 1023) / 1024 * 1024);
+  l.as_count = as == 1 ? (int)((K + 127) / 128) : (as == 2 ? (int)((K + 31) / 32) : 0);
+  l.rows = (int)(kStreamWaves * ppw * kPair);
+  return l;
+}
+
+template <int ACT, int WS, int AS, int SZ>
+__global__ __launch_bounds__(kStreamThreads) void gemv_stream_kernel(GemvArgs a) {
+  extern __shared__ __attribute__((aligned(16))) uint8_t st_lds[];
+  const StreamLds L = stream_lds(ACT, AS, a.K, a.pairs_per_wave);
+  float* ascale_s = reinterpret_cast<float*>(st_lds + L.x_bytes);
+  float* rscale_s = ascale_s + L.as_count;
+  float* bias_s = rscale_s + L.rows;
+  const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+  const int64_t npairs = cdiv(a.N, kPair);
+  const int64_t S = cdiv(a.K, kWaveK);  // sweeps per row
+  // Wavefront gw owns pairs gw + j * W, j < pairs_per_wave (W = all wavefronts), so
+  // at any moment the wavefronts stream one compact window of the weight matrix.
+  const int64_t W = (int64_t)gridDim.x * kStreamWaves;
+  const int64_t gw = (int64_t)blockIdx.x * kStreamWaves + wave;
+  const int64_t my_pairs = gw < npairs ? min(a.pairs_per_wave, (npairs - 1 - gw) / W + 1) : 0;
+  auto pair_index = [&](int64_t j) { return gw + j * W; };
+  auto lds_row = [&](int64_t j, int r) { return (int)((wave * a.pairs_per_wave + j) * kPair + r); };
+  const int64_t n_items = my_pairs * S;
+  const int lane_k = lane * kChunk;
+
+  // Ring slot contents and the issue cursor (pair, sweep) of item `it`.
+  uint4 rw[kRing][kPair];
+  uint32_t rs[kRing][kPair];
+  int64_t ip = 0, is = 0;  // issue cursor: pair offset, sweep
+  auto issue = [&](int slot) {
+    // Past the wavefront's last item: re-read its last item (valid, L2-resident).
+    const bool past = ip >= my_pairs;
+    const int64_t p = past ? my_pairs - 1 : ip, sw = past ? S - 1 : is;
+    const int64_t k0 = min(sw * kWaveK + lane_k, a.K - kChunk);
+#pragma unroll
+    for (int r = 0; r < kPair; ++r) {
+      const int64_t n = min(pair_index(p) * kPair + r, a.N - 1);
+      rw[slot][r] = *reinterpret_cast<const uint4*>(a.w + n * a.ldw + k0);
+      if constexpr (WS == WS_CHUNK) rs[slot][r] = load_scale_bits<SZ>(a.wscale, (n / a.by) * a.srs + (uint32_t)k0 / (uint32_t)a.bx);
+    }
+    if (++is == S) { is = 0; ++ip; }
+  };
+  if (n_items > 0) {
+#pragma unroll
+    for (int d = 0; d < kRing; ++d) issue(d);
+  }
+
+  // Stage x with direct-to-LDS loads (64 lanes x 16 B per instruction), then the
+  // small per-workgroup tables with ordinary loads.
+  {
+    const int nvec = L.x_bytes / 16;
+    const int64_t last = (ACT == ACT_E4M3 ? a.K : 2 * a.K) / 16 - 1;  // K % 16 == 0
+    for (int v0 = wave * 64; v0 < nvec; v0 += kStreamThreads) {
+      const int64_t v = min((int64_t)(v0 + lane), last);
+      __builtin_amdgcn_global_load_lds(reinterpret_cast<const uint8_t*>(a.x) + v * 16,
+                                       (__attribute__((address_space(3))) void*)(st_lds + (size_t)__builtin_amdgcn_readfirstlane(v0) * 16),
+                                       16, 0, 0);
+    }
+  }
+  for (int i = tid; i < L.as_count; i += kStreamThreads) {
+    if constexpr (AS == AS_BLOCK128) ascale_s[i] = load_f32(a.ascale, a.ascale_dtype, i);
+    else if constexpr (AS == AS_MX32) ascale_s[i] = e8m0_decode(reinterpret_cast<const uint8_t*>(a.ascale)[i]);
+  }
+  for (int i = tid; i < L.rows; i += kStreamThreads) {
+    const int64_t wv = i / (a.pairs_per_wave * kPair), j = (i / kPair) % a.pairs_per_wave;
+    const int64_t n = min(((int64_t)blockIdx.x * kStreamWaves + wv + j * W) * kPair + i % kPair, a.N - 1);
+    if constexpr (WS == WS_ROW) rscale_s[i] = load_f32(a.wscale, a.wscale_dtype, (n / a.by) * a.srs);
+    bias_s[i] = a.bias ? load_f32(a.bias, a.bias_dtype, n) : 0.0f;
+  }
+  __syncthreads();
+  if (n_items == 0) return;
+
+  float acc[kPair] = {0.0f, 0.0f};
+  int64_t cp = 0, cs = 0;  // consume cursor
+  auto consume = [&](int slot) {
+    const int64_t k0 = cs * kWaveK + lane_k;
+    const bool valid = k0 < a.K;
+    const int64_t kx = valid ? k0 : 0;
+    float xf[16];
+    if constexpr (ACT == ACT_E4M3) {
+      const uint4 v = *reinterpret_cast<const uint4*>(st_lds + kx);
+      e4m3x4_to_f32(v.x, xf); e4m3x4_to_f32(v.y, xf + 4); e4m3x4_to_f32(v.z, xf + 8); e4m3x4_to_f32(v.w, xf + 12);
+    } else {
+      const uint4* p = reinterpret_cast<const uint4*>(st_lds + 2 * kx);
+      const uint4 lo = p[0], hi = p[1];
+      const uint32_t w[8] = {lo.x, lo.y, lo.z, lo.w, hi.x, hi.y, hi.z, hi.w};
+#pragma unroll
+      for (int i = 0; i < 8; ++i) {
+        if constexpr (ACT == ACT_BF16) { xf[2 * i] = u2f(w[i] << 16); xf[2 * i + 1] = u2f(w[i] & 0xFFFF0000u); }
+        else { xf[2 * i] = f16_bits_to_f32((uint16_t)(w[i] & 0xFFFFu)); xf[2 * i + 1] = f16_bits_to_f32((uint16_t)(w[i] >> 16)); }
+      }
+    }
+    float sa = 1.0f;
+    if constexpr (AS == AS_BLOCK128) sa = ascale_s[kx / 128];
+    else if constexpr (AS == AS_MX32) sa = ascale_s[kx / 32];
+#pragma unroll
+    for (int r = 0; r < kPair; ++r) {
+      const float d = valid ? dot16(rw[slot][r], xf) : 0.0f;
+      if constexpr (WS == WS_CHUNK) acc[r] = fmaf(d, decode_scale_bits<SZ>(rs[slot][r], a.ws_is_f16) * sa, acc[r]);
+      else if constexpr (AS != AS_NONE) acc[r] = fmaf(d, sa, acc[r]);
+      else acc[r] += d;
+    }
+    if (++cs == S) {  // end of a row pair: reduce, scale, bias, store
+#pragma unroll
+      for (int r = 0; r < kPair; ++r) {
+        float v = wave_sum_dpp(acc[r]);
+        acc[r] = 0.0f;
+        const int64_t n = pair_index(cp) * kPair + r;
+        const int lr = lds_row(cp, r);
+        if constexpr (WS == WS_ROW) v *= rscale_s[lr];
+        v += bias_s[lr];
+        if (lane == 0 && n < a.N) store_f32(a.out, a.out_dtype, n, v);
+      }
+      cs = 0;
+      ++cp;
+    }
+  };
+
+  int64_t it = 0;
+  for (; it + kRing <= n_items; it += kRing) {
+#pragma unroll
+    for (int d = 0; d < kRing; ++d) {
+      consume(d);
+      issue(d);
+    }
+  }
+#pragma unroll
+  for (int d = 0; d < kRing; ++d) {
+    if (it + d < n_items) consume(d);
+  }
+}
+
 constexpr int kRows = 2;    // weight rows per wavefront
 constexpr int kUnroll = 4;  // K sweeps in flight per wavefront
 
@@ -239,6 +412,36 @@ void launch_gemv_fast(GemvArgs& a, int split, hipStream_t st) {
   hipLaunchKernelGGL((gemv_kernel<ACT, WS, AS, kRows, kUnroll>), grid, dim3(kGemvThreads), 0, st, a);
 }
 
+// Streaming plan: used when N alone yields >= 2048 wavefronts of one row pair each
+// and the staged tables fit in LDS. Each wavefront then owns ceil(pairs / 2048)
+// consecutive pairs (8 wavefronts per CU).
+constexpr int64_t kStreamWavesTarget = 2048;
+bool stream_plan(int act, int as, int64_t N, int64_t K, int64_t& ppw, int& lds) {
+  const int64_t npairs = cdiv(N, kPair);
+  if (npairs < kStreamWavesTarget) return false;
+  ppw = cdiv(npairs, kStreamWavesTarget);
+  lds = stream_lds(act, as, K, ppw).total();
+  return lds <= kStreamLdsMax;
+}
+
+template <int ACT, int WS, int AS, int SZ>
+void launch_stream(GemvArgs& a, int lds, hipStream_t st) {
+  const int64_t waves = cdiv(cdiv(a.N, kPair), a.pairs_per_wave);
+  const dim3 grid((unsigned)cdiv(waves, kStreamWaves));
+  hipLaunchKernelGGL((gemv_stream_kernel<ACT, WS, AS, SZ>), grid, dim3(kStreamThreads), (unsigned)lds, st, a);
+}
+
+template <int ACT, int AS>
+void dispatch_stream(GemvArgs& a, bool row_scale, int lds, hipStream_t st) {
+  if (row_scale) return launch_stream<ACT, WS_ROW, AS, 4>(a, lds, st);
+  a.ws_is_f16 = a.wscale_dtype == AYK_F16;
+  switch (a.wscale_dtype) {
+    case AYK_U8: return launch_stream<ACT, WS_CHUNK, AS, 1>(a, lds, st);
+    case AYK_F32: return launch_stream<ACT, WS_CHUNK, AS, 4>(a, lds, st);
+    default: return launch_stream<ACT, WS_CHUNK, AS, 2>(a, lds, st);
+  }
+}
+
 template <int ACT, int AS>
 int run_gemv(GemvArgs a, bool row_scale, size_t ws_bytes, const char* op, hipStream_t st) {
   const bool fast = aligned16(a.w) && aligned16(a.x) && a.ldw % 16 == 0 && a.K % kChunk == 0 &&
@@ -246,6 +449,11 @@ int run_gemv(GemvArgs a, bool row_scale, size_t ws_bytes, const char* op, hipStr
   if (!fast) {
     const dim3 grid((unsigned)cdiv(a.N, kGemvWaves));
     hipLaunchKernelGGL((gemv_generic_kernel<ACT, AS>), grid, dim3(kGemvThreads), 0, st, a);
+    return check_launch(op);
+  }
+  int lds = 0;
+  if (stream_plan(ACT, AS, a.N, a.K, a.pairs_per_wave, lds)) {
+    dispatch_stream<ACT, AS>(a, row_scale, lds, st);
     return check_launch(op);
   }
   const SplitPlan plan = gemv_split_plan(a.N, a.K);
@@ -267,8 +475,11 @@ int run_gemv(GemvArgs a, bool row_scale, size_t ws_bytes, const char* op, hipStr
   return AYK_OK;
 }
 
-size_t gemv_workspace(int64_t N, int64_t K) {
+size_t gemv_workspace(int act, int as, int64_t N, int64_t K) {
   if (N <= 0 || K <= 0) return 0;
+  int64_t ppw;
+  int lds;
+  if (K % kChunk == 0 && stream_plan(act, as, N, K, ppw, lds)) return 0;
   const SplitPlan plan = gemv_split_plan(N, K);
   return plan.split > 1 ? (size_t)plan.split * (size_t)N * sizeof(float) : 0;
 }
@@ -306,6 +517,11 @@ int mx_gemv(const void* a, const uint8_t* a_scale, const void* w, int64_t ldw,
                        dim3(kGemvThreads), 0, st, g);
     return check_launch("mxfp8_scaled_mm(M=1)");
   }
+  int lds = 0;
+  if (stream_plan(ACT_E4M3, AS_MX32, N, K, g.pairs_per_wave, lds)) {
+    launch_stream<ACT_E4M3, WS_CHUNK, AS_MX32, 1>(g, lds, st);
+    return check_launch("mxfp8_scaled_mm(M=1)");
+  }
   g.k_per_split = cdiv(K, kWaveK) * kWaveK;
   launch_gemv_fast<ACT_E4M3, WS_CHUNK, AS_MX32>(g, 1, st);
   return check_launch("mxfp8_scaled_mm(M=1)");
@@ -317,8 +533,8 @@ using namespace ayk;
 
 extern "C" {
 
-size_t ayk_fp8_weight_only_gemv_workspace_bytes(int64_t N, int64_t K) { return gemv_workspace(N, K); }
-size_t ayk_fp8_blockwise_gemv_workspace_bytes(int64_t N, int64_t K) { return gemv_workspace(N, K); }
+size_t ayk_fp8_weight_only_gemv_workspace_bytes(int64_t N, int64_t K) { return gemv_workspace(ACT_BF16, AS_NONE, N, K); }
+size_t ayk_fp8_blockwise_gemv_workspace_bytes(int64_t N, int64_t K) { return gemv_workspace(ACT_E4M3, AS_BLOCK128, N, K); }
 
 int ayk_fp8_weight_only_gemv(const void* x, int x_dtype, const void* w, int64_t ldw, int64_t N,
                              int64_t K, const void* scale, int scale_dtype,

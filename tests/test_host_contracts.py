@@ -319,5 +319,5 @@ def test_c_abi_rejects_bad_arguments_without_a_gpu():
     assert lib.ayk_fp8_weight_only_gemv(None, _lib.AYK_F32, None, 16, 4, 16, None, 0, 1, 1, 16, None, None, 0, None) == _lib.AYK_EINVAL
     # zero-sized problems are no-ops that succeed without touching a device
     assert lib.ayk_per_token_quant_fp8(None, _lib.AYK_BF16, 0, 16, 16, None, 16, None, None) == _lib.AYK_OK
-    assert lib.ayk_fp8_weight_only_gemv_workspace_bytes(4096, 14336) > 0
+    assert lib.ayk_fp8_weight_only_gemv_workspace_bytes(512, 14336) > 0  # split-K shape
     assert lib.ayk_fp8_weight_only_gemv_workspace_bytes(28672, 4096) == 0
