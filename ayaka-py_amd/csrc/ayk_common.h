@@ -117,6 +117,34 @@ __device__ inline float load_f32(const void* p, int dtype, int64_t i) {
     default: return 0.0f;
   }
 }
+// The same load split in two: the raw dword now, the conversion later. A value that
+// is only used after later loads were issued does not make the wavefront wait for
+// those loads (the vector-memory counter retires in issue order). The load is a single
+// branch-free instruction: the aligned dword that contains element i (it lies in the
+// same page as the element, so it is always readable); bits_to_f32 extracts and
+// converts it.
+struct RawBits {
+  uint32_t word;
+  uint32_t shift;
+};
+__device__ inline int dtype_size(int dtype) { return dtype == AYK_F32 ? 4 : (dtype == AYK_U8 ? 1 : 2); }
+__device__ inline RawBits load_bits(const void* p, int dtype, int64_t i) {
+  // Pointer arithmetic stays on `p` so the compiler keeps the global address space
+  // (a flat load would be waited for conservatively).
+  const int64_t byte = i * dtype_size(dtype);
+  const uint32_t mis = (uint32_t)((reinterpret_cast<uintptr_t>(p) + (uintptr_t)byte) & 3);
+  return {*reinterpret_cast<const uint32_t*>(static_cast<const uint8_t*>(p) + byte - mis), mis * 8};
+}
+// Branch-free: every decoding is computed and one is selected (a branch here would
+// cost the compiler its exact wait counts for loads still in flight).
+__device__ inline float bits_to_f32(RawBits r, int dtype) {
+  const uint32_t b = r.word >> r.shift;
+  const float f32 = u2f(r.word);
+  const float f16 = f16_bits_to_f32((uint16_t)b);
+  const float bf16 = bf16_bits_to_f32(b & 0xFFFFu);
+  const float u8 = e8m0_decode(b & 0xFFu);
+  return dtype == AYK_F32 ? f32 : (dtype == AYK_F16 ? f16 : (dtype == AYK_BF16 ? bf16 : u8));
+}
 __device__ inline void store_f32(void* p, int dtype, int64_t i, float v) {
   switch (dtype) {
     case AYK_F32: reinterpret_cast<float*>(p)[i] = v; break;

@@ -50,6 +50,7 @@ struct GemvArgs {
   int64_t k_per_split;  // multiple of kWaveK
   int64_t pairs_per_wave;  // streaming kernel: row pairs owned by one wavefront
   int ws_is_f16;           // streaming kernel, 2-byte chunk scales: fp16 (1) or bf16 (0)
+  int bx_shift;            // streaming kernel, chunk scales: log2(bx), or -1 if bx is not a power of two
 };
 
 // Load the 16 activation values of chunk `c` (elements 16c .. 16c+15) as floats.
@@ -218,18 +219,27 @@ __global__ __launch_bounds__(kGemvThreads) void gemv_generic_kernel(GemvArgs a) 
 
 // ---------------------------------------------------------------------------------
 // Streaming GEMV: the main path when N is large enough to fill the GPU without a K
-// split. Each wavefront owns every W-th row pair (W = all wavefronts) and walks its
-// pairs' (pair, 1024-K sweep) items in order and keeps kRing
-// items of weight loads in flight in a register ring, across row boundaries, so the
-// memory pipeline never drains between rows. Everything else an item needs is staged
-// once per workgroup in LDS (x, activation scales, row scales, bias) or travels in the
-// ring beside its weights (chunk scales): the vector-memory counter retires loads in
-// issue order, so a load issued behind the prefetch would wait for all of it.
+// split. Each wavefront owns every W-th row pair (W = all wavefronts), walks its
+// pairs' (pair, 1024-K sweep) items in order, and keeps kRing items of weight loads in
+// flight in a register ring, across row boundaries, so the memory pipeline never
+// drains between rows.
+//
+// The vector-memory counter retires loads in issue order, so a wavefront must never
+// wait on a load issued behind the ring: it would wait for the whole ring. Hence the
+// start-up order: (1) x is copied to LDS with direct-to-LDS loads; (2) each lane loads
+// the raw row scale and bias of one of the wavefront's rows (read back with readlane
+// and converted at that row's end); (3) the ring is issued; (4) one wait for "all but
+// the ring's loads" and a workgroup barrier make x visible. Chunk scales (block-128 /
+// MX / per-K-block weight scales) and activation scales travel in the ring beside
+// their weights. Everything between the loads and their use is kept branch-free: a
+// load issued inside a branch, or a branch between the ring's prologue and the loop,
+// costs the compiler its exact wait counts, and it then waits for the whole ring.
 constexpr int kStreamThreads = 256;
 constexpr int kStreamWaves = kStreamThreads / kWave;
-constexpr int kRing = 4;   // items in flight per wavefront (2 rows x 16 B per lane each; 4 measured best)
+constexpr int kRing = 3;   // items in flight per wavefront (2 rows x 16 B per lane each; 3 measured best of 2-6)
 constexpr int kPair = 2;   // rows per item
 constexpr int kStreamLdsMax = 64 * 1024;
+constexpr int kStreamRowsMax = kWave;       // rows per wavefront: one register lane each
 
 template <int SZ>
 __device__ inline uint32_t load_scale_bits(const void* p, int64_t i) {
@@ -246,134 +256,203 @@ __device__ inline float decode_scale_bits(uint32_t b, int is_f16) {
 
 // LDS plan of the streaming kernel (shared by host and device).
 struct StreamLds {
-  int x_bytes;      // staged activation, padded to whole 1 KiB direct-load groups
-  int as_count;     // activation scales (floats)
-  int rows;         // rows per workgroup (row scales and bias, floats each)
-  __host__ __device__ int total() const { return x_bytes + 4 * as_count + 8 * rows; }
+  int x_bytes;   // staged activation, padded to whole 1 KiB direct-load groups
+  __host__ __device__ int total() const { return x_bytes; }
 };
-__host__ __device__ inline StreamLds stream_lds(int act, int as, int64_t K, int64_t ppw) {
+__host__ __device__ inline StreamLds stream_lds(int act, int64_t K) {
   StreamLds l;
   const int64_t xb = act == 2 ? K : 2 * K;
   l.x_bytes = (int)((xb + 1023) / 1024 * 1024);
-  l.as_count = as == 1 ? (int)((K + 127) / 128) : (as == 2 ? (int)((K + 31) / 32) : 0);
-  l.rows = (int)(kStreamWaves * ppw * kPair);
   return l;
+}
+
+// s_waitcnt with only the vector-memory count constrained (gfx9 encoding: vmcnt in
+// bits [3:0] and [15:14], expcnt [6:4] and lgkmcnt [11:8] left at their maxima).
+template <int N>
+__device__ inline void wait_vmcnt() {
+  static_assert(N >= 0 && N < 64, "vmcnt range");
+  __builtin_amdgcn_s_waitcnt((N & 15) | ((N >> 4) << 14) | (7 << 4) | (15 << 8));
 }
 
 template <int ACT, int WS, int AS, int SZ>
 __global__ __launch_bounds__(kStreamThreads) void gemv_stream_kernel(GemvArgs a) {
   extern __shared__ __attribute__((aligned(16))) uint8_t st_lds[];
-  const StreamLds L = stream_lds(ACT, AS, a.K, a.pairs_per_wave);
-  float* ascale_s = reinterpret_cast<float*>(st_lds + L.x_bytes);
-  float* rscale_s = ascale_s + L.as_count;
-  float* bias_s = rscale_s + L.rows;
-  const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
-  const int64_t npairs = cdiv(a.N, kPair);
-  const int64_t S = cdiv(a.K, kWaveK);  // sweeps per row
+  const StreamLds L = stream_lds(ACT, a.K);
+  const int tid = threadIdx.x, lane = tid & 63;
+  const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
+  // The plan keeps N, K < 2^31: all cursors are 32-bit and wave-uniform (SGPRs).
+  const int N = (int)a.N, K = (int)a.K;
+  const int npairs = (N + kPair - 1) / kPair;
+  const int S = (K + (int)kWaveK - 1) / (int)kWaveK;  // sweeps per row
   // Wavefront gw owns pairs gw + j * W, j < pairs_per_wave (W = all wavefronts), so
   // at any moment the wavefronts stream one compact window of the weight matrix.
-  const int64_t W = (int64_t)gridDim.x * kStreamWaves;
-  const int64_t gw = (int64_t)blockIdx.x * kStreamWaves + wave;
-  const int64_t my_pairs = gw < npairs ? min(a.pairs_per_wave, (npairs - 1 - gw) / W + 1) : 0;
-  auto pair_index = [&](int64_t j) { return gw + j * W; };
-  auto lds_row = [&](int64_t j, int r) { return (int)((wave * a.pairs_per_wave + j) * kPair + r); };
-  const int64_t n_items = my_pairs * S;
+  const int W = (int)gridDim.x * kStreamWaves;
+  const int gw = (int)blockIdx.x * kStreamWaves + wave;
+  const int ppw = (int)a.pairs_per_wave;
+  const int my_pairs = gw < npairs ? min(ppw, (npairs - 1 - gw) / W + 1) : 0;
+  const int n_items = my_pairs * S;
   const int lane_k = lane * kChunk;
+  // K offset of the lane in the last sweep, clamped so its 16-byte load stays in the
+  // row (its products are discarded when the chunk is past K).
+  const int lane_k_last = min((S - 1) * (int)kWaveK + lane_k, K - kChunk) - (S - 1) * (int)kWaveK;
 
-  // Ring slot contents and the issue cursor (pair, sweep) of item `it`.
-  uint4 rw[kRing][kPair];
-  uint32_t rs[kRing][kPair];
-  int64_t ip = 0, is = 0;  // issue cursor: pair offset, sweep
-  auto issue = [&](int slot) {
-    // Past the wavefront's last item: re-read its last item (valid, L2-resident).
-    const bool past = ip >= my_pairs;
-    const int64_t p = past ? my_pairs - 1 : ip, sw = past ? S - 1 : is;
-    const int64_t k0 = min(sw * kWaveK + lane_k, a.K - kChunk);
-#pragma unroll
-    for (int r = 0; r < kPair; ++r) {
-      const int64_t n = min(pair_index(p) * kPair + r, a.N - 1);
-      rw[slot][r] = *reinterpret_cast<const uint4*>(a.w + n * a.ldw + k0);
-      if constexpr (WS == WS_CHUNK) rs[slot][r] = load_scale_bits<SZ>(a.wscale, (n / a.by) * a.srs + (uint32_t)k0 / (uint32_t)a.bx);
-    }
-    if (++is == S) { is = 0; ++ip; }
-  };
-  if (n_items > 0) {
-#pragma unroll
-    for (int d = 0; d < kRing; ++d) issue(d);
-  }
-
-  // Stage x with direct-to-LDS loads (64 lanes x 16 B per instruction), then the
-  // small per-workgroup tables with ordinary loads.
+  // (1) x -> LDS, 64 lanes x 16 B per instruction.
   {
     const int nvec = L.x_bytes / 16;
-    const int64_t last = (ACT == ACT_E4M3 ? a.K : 2 * a.K) / 16 - 1;  // K % 16 == 0
+    const int last = (ACT == ACT_E4M3 ? K : 2 * K) / 16 - 1;  // K % 16 == 0
     for (int v0 = wave * 64; v0 < nvec; v0 += kStreamThreads) {
-      const int64_t v = min((int64_t)(v0 + lane), last);
-      __builtin_amdgcn_global_load_lds(reinterpret_cast<const uint8_t*>(a.x) + v * 16,
-                                       (__attribute__((address_space(3))) void*)(st_lds + (size_t)__builtin_amdgcn_readfirstlane(v0) * 16),
-                                       16, 0, 0);
+      const int v = min(v0 + lane, last);
+      __builtin_amdgcn_global_load_lds(reinterpret_cast<const uint8_t*>(a.x) + (size_t)v * 16,
+                                       (__attribute__((address_space(3))) void*)(st_lds + (size_t)v0 * 16), 16, 0, 0);
     }
   }
-  for (int i = tid; i < L.as_count; i += kStreamThreads) {
-    if constexpr (AS == AS_BLOCK128) ascale_s[i] = load_f32(a.ascale, a.ascale_dtype, i);
-    else if constexpr (AS == AS_MX32) ascale_s[i] = e8m0_decode(reinterpret_cast<const uint8_t*>(a.ascale)[i]);
+  // (2) lane l holds the raw row scale and bias of the wavefront's row l (pair l / 2,
+  //     row l % 2 of it) and, for chunk scales, the offset of its scale row. Lanes past
+  //     the wavefront's rows read row N - 1 (never used); a missing bias reads x[0].
+  RawBits row_s_bits{0, 0}, row_b_bits;
+  int64_t srow_lane;
+  {
+    const int n = min((gw + (lane / kPair) * W) * kPair + lane % kPair, N - 1);
+    srow_lane = (int64_t)((uint32_t)n / (uint32_t)a.by) * a.srs;
+    if constexpr (WS == WS_ROW) row_s_bits = load_bits(a.wscale, a.wscale_dtype, srow_lane);
+    row_b_bits = a.bias ? load_bits(a.bias, a.bias_dtype, n) : load_bits(a.x, AYK_F32, 0);
   }
-  for (int i = tid; i < L.rows; i += kStreamThreads) {
-    const int64_t wv = i / (a.pairs_per_wave * kPair), j = (i / kPair) % a.pairs_per_wave;
-    const int64_t n = min(((int64_t)blockIdx.x * kStreamWaves + wv + j * W) * kPair + i % kPair, a.N - 1);
-    if constexpr (WS == WS_ROW) rscale_s[i] = load_f32(a.wscale, a.wscale_dtype, (n / a.by) * a.srs);
-    bias_s[i] = a.bias ? load_f32(a.bias, a.bias_dtype, n) : 0.0f;
-  }
-  __syncthreads();
+  auto srow_of = [&](int row) -> int64_t {  // row: wave-uniform index < 64
+    const uint32_t lo = (uint32_t)__builtin_amdgcn_readlane((int)(uint32_t)srow_lane, row);
+    const uint32_t hi = (uint32_t)__builtin_amdgcn_readlane((int)(uint32_t)(srow_lane >> 32), row);
+    return (int64_t)(((uint64_t)hi << 32) | lo);
+  };
+
+  // (3) the ring. The issue cursor is (pair ordinal ip, sweep is) plus the uniform
+  //     address of that pair's first row; it saturates at the wavefront's last item,
+  //     which is re-read to keep the ring full at the end (and for a wavefront without
+  //     rows, pair 0 clamped to a valid row, never consumed).
+  uint4 rw[kRing][kPair];
+  uint32_t rs[kRing][kPair];
+  RawBits ra[kRing];  // activation scale of the lane's 16-K chunk (block-128 / MX)
+  const int as_dtype = AS == AS_MX32 ? AYK_U8 : a.ascale_dtype;
+  const int64_t pair_stride = (int64_t)W * kPair * a.ldw;
+  int ip = 0, is = 0;
+  int row0 = min(gw * kPair, N - 1);
+  const uint8_t* ibase = a.w + (int64_t)row0 * a.ldw;
+  int64_t r1off = row0 + 1 < N ? a.ldw : 0;
+  auto issue = [&](int slot) {
+    const int lk = is * (int)kWaveK + (is == S - 1 ? lane_k_last : lane_k);
+    rw[slot][0] = load_stream(ibase + lk);
+    rw[slot][1] = load_stream(ibase + r1off + lk);
+    if constexpr (WS == WS_CHUNK) {
+      const int kq = a.bx_shift >= 0 ? lk >> a.bx_shift : (int)((uint32_t)lk / (uint32_t)a.bx);
+#pragma unroll
+      for (int r = 0; r < kPair; ++r) rs[slot][r] = load_scale_bits<SZ>(a.wscale, srow_of(ip * kPair + r) + kq);
+    }
+    if constexpr (AS != AS_NONE) ra[slot] = load_bits(a.ascale, as_dtype, lk >> (AS == AS_MX32 ? 5 : 7));
+    // Advance, saturating at the last item.
+    const bool more = ip < my_pairs - 1 || is < S - 1;
+    const bool wrap = is == S - 1;
+    if (more) {
+      if (wrap) {
+        is = 0;
+        ++ip;
+        row0 += W * kPair;
+        ibase += pair_stride;
+        r1off = row0 + 1 < N ? a.ldw : 0;
+      } else {
+        ++is;
+      }
+    }
+  };
+  // Issued unconditionally (no branch), so the compiler's wait counts stay exact.
+  constexpr int kRingLoads = kRing * (kPair * (WS == WS_CHUNK ? 2 : 1) + (AS != AS_NONE ? 1 : 0));
+#pragma unroll
+  for (int d = 0; d < kRing; ++d) issue(d);
+
+  // (4) everything but the ring has landed (x in LDS); barrier.
+  wait_vmcnt<kRingLoads>();
+  __builtin_amdgcn_s_waitcnt(0xC07F);  // lgkmcnt(0)
+  __builtin_amdgcn_s_barrier();
   if (n_items == 0) return;
+  // Row l's scale / bias, converted at its row end (converting here, between the ring
+  // prologue and the loop, makes the compiler copy ring registers, which waits).
+  auto lane_value = [&](RawBits rb, int row, int dtype) {
+    const RawBits r{(uint32_t)__builtin_amdgcn_readlane((int)rb.word, row), (uint32_t)__builtin_amdgcn_readlane((int)rb.shift, row)};
+    return bits_to_f32(r, dtype);
+  };
 
   float acc[kPair] = {0.0f, 0.0f};
-  int64_t cp = 0, cs = 0;  // consume cursor
+  int cp = 0, cs = 0;  // consume cursor
   auto consume = [&](int slot) {
-    const int64_t k0 = cs * kWaveK + lane_k;
-    const bool valid = k0 < a.K;
-    const int64_t kx = valid ? k0 : 0;
-    float xf[16];
+    // Opaque from here on: otherwise the compiler hoists work on the prologue's ring
+    // values into the loop preheader, where it must wait for the whole ring.
+    if constexpr (WS == WS_CHUNK) {
+#pragma unroll
+      for (int r = 0; r < kPair; ++r) asm volatile("" : "+v"(rs[slot][r]));
+    }
+    if constexpr (AS != AS_NONE) asm volatile("" : "+v"(ra[slot].word), "+v"(ra[slot].shift));
+    const int k0 = cs * (int)kWaveK + lane_k;
+    const bool valid = k0 < K;
+    const int kx = valid ? k0 : 0;
+    // Products in packed 16-bit form: every e4m3 value is exact in bf16 and fp16, and
+    // a product of two of them is exact in fp32; v_dot2 sums two products into fp32.
+    uint32_t xp[8];  // x[kx .. kx+15] as 8 pairs (bf16 pairs for e4m3 x)
     if constexpr (ACT == ACT_E4M3) {
       const uint4 v = *reinterpret_cast<const uint4*>(st_lds + kx);
-      e4m3x4_to_f32(v.x, xf); e4m3x4_to_f32(v.y, xf + 4); e4m3x4_to_f32(v.z, xf + 8); e4m3x4_to_f32(v.w, xf + 12);
+      const uint32_t w4[4] = {v.x, v.y, v.z, v.w};
+#pragma unroll
+      for (int i = 0; i < 4; ++i) {
+        xp[2 * i] = __builtin_bit_cast(uint32_t, __builtin_amdgcn_cvt_scalef32_pk_bf16_fp8((int)w4[i], 1.0f, false));
+        xp[2 * i + 1] = __builtin_bit_cast(uint32_t, __builtin_amdgcn_cvt_scalef32_pk_bf16_fp8((int)w4[i], 1.0f, true));
+      }
     } else {
       const uint4* p = reinterpret_cast<const uint4*>(st_lds + 2 * kx);
       const uint4 lo = p[0], hi = p[1];
-      const uint32_t w[8] = {lo.x, lo.y, lo.z, lo.w, hi.x, hi.y, hi.z, hi.w};
-#pragma unroll
-      for (int i = 0; i < 8; ++i) {
-        if constexpr (ACT == ACT_BF16) { xf[2 * i] = u2f(w[i] << 16); xf[2 * i + 1] = u2f(w[i] & 0xFFFF0000u); }
-        else { xf[2 * i] = f16_bits_to_f32((uint16_t)(w[i] & 0xFFFFu)); xf[2 * i + 1] = f16_bits_to_f32((uint16_t)(w[i] >> 16)); }
-      }
+      xp[0] = lo.x; xp[1] = lo.y; xp[2] = lo.z; xp[3] = lo.w;
+      xp[4] = hi.x; xp[5] = hi.y; xp[6] = hi.z; xp[7] = hi.w;
     }
     float sa = 1.0f;
-    if constexpr (AS == AS_BLOCK128) sa = ascale_s[kx / 128];
-    else if constexpr (AS == AS_MX32) sa = ascale_s[kx / 32];
+    if constexpr (AS == AS_MX32) sa = e8m0_decode((ra[slot].word >> ra[slot].shift) & 0xFFu);
+    else if constexpr (AS == AS_BLOCK128) sa = bits_to_f32(ra[slot], as_dtype);
 #pragma unroll
     for (int r = 0; r < kPair; ++r) {
-      const float d = valid ? dot16(rw[slot][r], xf) : 0.0f;
-      if constexpr (WS == WS_CHUNK) acc[r] = fmaf(d, decode_scale_bits<SZ>(rs[slot][r], a.ws_is_f16) * sa, acc[r]);
-      else if constexpr (AS != AS_NONE) acc[r] = fmaf(d, sa, acc[r]);
-      else acc[r] += d;
+      const uint32_t w4[4] = {rw[slot][r].x, rw[slot][r].y, rw[slot][r].z, rw[slot][r].w};
+      constexpr bool kDirect = WS == WS_ROW && AS == AS_NONE;  // accumulate in the dot chain
+      float d = kDirect ? acc[r] : 0.0f;
+#pragma unroll
+      for (int i = 0; i < 4; ++i) {
+        if constexpr (ACT == ACT_F16) {
+          typedef _Float16 h2 __attribute__((ext_vector_type(2)));
+          const h2 w0 = __builtin_amdgcn_cvt_scalef32_pk_f16_fp8((int)w4[i], 1.0f, false);
+          const h2 w1 = __builtin_amdgcn_cvt_scalef32_pk_f16_fp8((int)w4[i], 1.0f, true);
+          d = __builtin_amdgcn_fdot2(w0, __builtin_bit_cast(h2, xp[2 * i]), d, false);
+          d = __builtin_amdgcn_fdot2(w1, __builtin_bit_cast(h2, xp[2 * i + 1]), d, false);
+        } else {
+          typedef __bf16 b2 __attribute__((ext_vector_type(2)));
+          const b2 w0 = __builtin_amdgcn_cvt_scalef32_pk_bf16_fp8((int)w4[i], 1.0f, false);
+          const b2 w1 = __builtin_amdgcn_cvt_scalef32_pk_bf16_fp8((int)w4[i], 1.0f, true);
+          d = __builtin_amdgcn_fdot2_f32_bf16(w0, __builtin_bit_cast(b2, xp[2 * i]), d, false);
+          d = __builtin_amdgcn_fdot2_f32_bf16(w1, __builtin_bit_cast(b2, xp[2 * i + 1]), d, false);
+        }
+      }
+      if constexpr (kDirect) acc[r] = valid ? d : acc[r];
+      else if constexpr (WS == WS_CHUNK) acc[r] = valid ? fmaf(d, decode_scale_bits<SZ>(rs[slot][r], a.ws_is_f16) * sa, acc[r]) : acc[r];
+      else acc[r] = valid ? fmaf(d, sa, acc[r]) : acc[r];
     }
     if (++cs == S) {  // end of a row pair: reduce, scale, bias, store
 #pragma unroll
       for (int r = 0; r < kPair; ++r) {
         float v = wave_sum_dpp(acc[r]);
         acc[r] = 0.0f;
-        const int64_t n = pair_index(cp) * kPair + r;
-        const int lr = lds_row(cp, r);
-        if constexpr (WS == WS_ROW) v *= rscale_s[lr];
-        v += bias_s[lr];
-        if (lane == 0 && n < a.N) store_f32(a.out, a.out_dtype, n, v);
+        const int n = (gw + cp * W) * kPair + r;
+        const int src = cp * kPair + r;  // wave-uniform lane index
+        if constexpr (WS == WS_ROW) v *= lane_value(row_s_bits, src, a.wscale_dtype);
+        if (a.bias) v += lane_value(row_b_bits, src, a.bias_dtype);
+        if (lane == 0 && n < N) store_f32(a.out, a.out_dtype, n, v);
       }
       cs = 0;
       ++cp;
     }
   };
 
-  int64_t it = 0;
+  int it = 0;
   for (; it + kRing <= n_items; it += kRing) {
 #pragma unroll
     for (int d = 0; d < kRing; ++d) {
@@ -420,12 +499,17 @@ bool stream_plan(int act, int as, int64_t N, int64_t K, int64_t& ppw, int& lds) 
   const int64_t npairs = cdiv(N, kPair);
   if (npairs < kStreamWavesTarget) return false;
   ppw = cdiv(npairs, kStreamWavesTarget);
-  lds = stream_lds(act, as, K, ppw).total();
-  return lds <= kStreamLdsMax;
+  (void)as;
+  lds = stream_lds(act, K).total();
+  return lds <= kStreamLdsMax && ppw * kPair <= kStreamRowsMax && N < INT32_MAX && K < INT32_MAX;
 }
 
 template <int ACT, int WS, int AS, int SZ>
 void launch_stream(GemvArgs& a, int lds, hipStream_t st) {
+  a.bx_shift = -1;
+  for (int sh = 0; sh < 31; ++sh) {
+    if ((int64_t)1 << sh == a.bx) a.bx_shift = sh;
+  }
   const int64_t waves = cdiv(cdiv(a.N, kPair), a.pairs_per_wave);
   const dim3 grid((unsigned)cdiv(waves, kStreamWaves));
   hipLaunchKernelGGL((gemv_stream_kernel<ACT, WS, AS, SZ>), grid, dim3(kStreamThreads), (unsigned)lds, st, a);
