@@ -286,28 +286,48 @@ __global__ __launch_bounds__(kThreads) void fp8_gemm_kernel(GemmArgs g) {
 }
 
 // ---------------------------------------------------------------------------------
-// Large-tile kernel (K % 128 == 0, M and N of at least one tile): a 256 x 256 output
+// Large-tile kernel (K % 64 == 0, M and N of at least one tile): a 256 x 256 output
 // tile per workgroup, one 128 x 128 wavefront tile (4 x 4 MFMA tiles, 256 accumulator
 // registers) on each of the four SIMDs.
 //
-//  * Operands move HBM/L2 -> LDS with gfx950's direct-to-LDS 16-byte loads
-//    (global_load_lds_dwordx4): no staging registers, no VALU. One such load writes
-//    64 lanes x 16 B = 8 tile rows of 128 B contiguously, so the LDS layout is set by
-//    choosing which 16-byte chunk each lane fetches: row r stores logical chunk c at
-//    physical chunk c ^ ((r >> 1) & 7). The 32 rows a wavefront reads at one K offset
-//    then fall on 16 distinct 16-byte bank groups per half-wave.
-//  * Two LDS stages of 64 KB in two distinct LDS objects, the K loop unrolled by two:
-//    the next K step's loads are in flight during the current step's 32 MFMAs, and
-//    fragments of the second 64-K half are read during the first half's MFMAs.
+//  * Operands move HBM/L2 -> LDS with gfx950's direct-to-LDS 16-byte buffer loads: no
+//    staging registers, no VALU. One load writes 64 lanes x 16 B = 16 tile rows of one
+//    64-byte K stage contiguously; the LDS layout is chosen through which 16-byte chunk
+//    each lane fetches (row r holds logical chunk c at c ^ ((r >> 2) & 3)), so the 32
+//    rows a fragment read touches fall on distinct bank groups.
+//  * A ring of four 32 KB stages (64 K each) in four distinct LDS objects, the K loop
+//    unrolled by four: loads run four steps ahead of the MFMAs. Each step waits for
+//    the next step's loads and passes one barrier in the middle of its MFMAs, and reads
+//    the next step's fragments while its second half executes (fragments are double
+//    buffered in registers), so neither the barrier nor the fragment reads leave the
+//    matrix cores idle.
 //  * Workgroup b runs on XCD b % 8. Tiles are numbered so that each XCD owns a
 //    contiguous range of an M-grouped order (8 M tiles per group): the ~32 tiles an
-//    XCD runs at once share 8 activation and 4 weight panels through its L2.
-//  * Rows past M / N are clamped to the last row (their results are never stored),
-//    so every load is in bounds; K must be a multiple of 128.
+//    XCD runs at once share 8 activation and 4 weight panels through its L2, and each
+//    starts its K walk at a different stage.
+//  * Every wait on the vector-memory counter is written out with its exact count
+//    (it retires in issue order); buffer windows end at the operand's last row, so
+//    rows past M / N read zero and are never stored.
 constexpr int kBigTile = 256;
+constexpr int kBigK = 64;                         // K bytes per stage
 // Word 3 of a raw (unstructured, stride 0) buffer resource on gfx9-family GPUs.
 constexpr int kBufferFlags = 0x00020000;
-constexpr int kBigStage = 2 * kBigTile * BK;  // weights + activations, bytes
+constexpr int kBigStage = 2 * kBigTile * kBigK;   // weights + activations of one stage, bytes
+constexpr int kEpilogueLds = 64 * 1024;           // epilogue staging tile (first stage object)
+
+// s_waitcnt with only the vector-memory count constrained (gfx9 encoding: vmcnt in
+// bits [3:0] and [15:14], expcnt [6:4] and lgkmcnt [11:8] left at their maxima).
+template <int N>
+__device__ inline void wait_vmcnt() {
+  static_assert(N >= 0 && N < 64, "vmcnt range");
+  __builtin_amdgcn_s_waitcnt((N & 15) | ((N >> 4) << 14) | (7 << 4) | (15 << 8));
+}
+// Workgroup barrier after this wavefront's LDS accesses completed (lgkmcnt(0)); unlike
+// __syncthreads it does not wait for outstanding global loads.
+__device__ inline void lds_barrier() {
+  __builtin_amdgcn_s_waitcnt(0xC07F);
+  __builtin_amdgcn_s_barrier();
+}
 
 // Four consecutive bias values n .. n+3 (n + 3 < N, n % 4 == 0) as floats.
 __device__ inline void load_bias4(const GemmArgs& g, int64_t n, float* b) {
@@ -349,6 +369,16 @@ __device__ inline void store4_typed(const GemmArgs& g, int64_t m, int64_t n, con
 template <int OUT>
 struct OutBytes { static constexpr int v = OUT == AYK_F32 ? 4 : 2; };
 
+// A raw buffer resource from wave-uniform values, forced into SGPRs: a descriptor the
+// compiler cannot prove uniform is wrapped in a readfirstlane loop at every load.
+__device__ inline __amdgpu_buffer_rsrc_t uniform_rsrc(const void* base, int32_t records) {
+  const uint64_t p = reinterpret_cast<uint64_t>(base);
+  const uint32_t lo = (uint32_t)__builtin_amdgcn_readfirstlane((int)(uint32_t)p);
+  const uint32_t hi = (uint32_t)__builtin_amdgcn_readfirstlane((int)(uint32_t)(p >> 32));
+  return __builtin_amdgcn_make_buffer_rsrc(reinterpret_cast<void*>(((uint64_t)hi << 32) | lo), (short)0,
+                                           __builtin_amdgcn_readfirstlane(records), kBufferFlags);
+}
+
 template <int MODE, int OUT>
 __device__ inline void big_epilogue(const GemmArgs& g, const v16f (&acc)[4][4], int64_t m_tile, int64_t n_tile,
                                     uint8_t* stage_lds) {
@@ -356,7 +386,7 @@ __device__ inline void big_epilogue(const GemmArgs& g, const v16f (&acc)[4][4], 
   constexpr int kRowBytes = 256 * EB + 16;        // padded staging row
   constexpr int kStageRows = EB == 4 ? 32 : 64;   // rows staged at once (fits 64 KB)
   constexpr int kPasses = 64 / kStageRows;        // fp32: one pass per row half (wm)
-  static_assert(kStageRows * kRowBytes <= kBigStage, "staging tile must fit one LDS stage buffer");
+  static_assert(kStageRows * kRowBytes <= kEpilogueLds, "staging tile must fit the first stage object");
   const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
   const int wn = wave >> 1, wm = wave & 1, h = lane >> 5, frow = lane & 31;
   const float* sa_p = reinterpret_cast<const float*>(g.sa);
@@ -437,13 +467,155 @@ __device__ inline void big_epilogue(const GemmArgs& g, const v16f (&acc)[4][4], 
 
 template <int MODE>
 __global__ __launch_bounds__(kThreads, 1) void fp8_gemm_big_kernel(GemmArgs g) {
+  static_assert(MODE == MODE_SCALED, "per-row / per-tensor scales only");
+  constexpr int FN = 4, FM = 4;                        // 32x32 MFMA tiles per wavefront (n, m)
+  constexpr int kDma = kBigStage / 1024 / 4;           // direct loads per wavefront per stage (8)
+  constexpr int kOps = kDma;                           // vector-memory ops per wavefront per stage
+  // Four stage buffers in four distinct LDS objects, so the compiler can tell that
+  // fragment reads of one stage never alias the in-flight direct loads of another. The
+  // first is twice as large: after the K loop it holds the epilogue's staging tile.
+  __shared__ __attribute__((aligned(1024))) uint8_t L0[kEpilogueLds];
+  __shared__ __attribute__((aligned(1024))) uint8_t L1[kBigStage];
+  __shared__ __attribute__((aligned(1024))) uint8_t L2[kBigStage];
+  __shared__ __attribute__((aligned(1024))) uint8_t L3[kBigStage];
+
+  const int tid = threadIdx.x, lane = tid & 63;
+  const int wave_u = __builtin_amdgcn_readfirstlane(tid >> 6);  // keep descriptors in SGPRs
+  const int wn = wave_u >> 1, wm = wave_u & 1;
+  const int h = lane >> 5, frow = lane & 31;
+  int tm, tn;
+  big_tile_coords(blockIdx.x, g.tiles_m, (int)cdiv(g.N, kBigTile), tm, tn);
+  const int64_t n_base = (int64_t)tn * kBigTile, m_base = (int64_t)tm * kBigTile;
+  const int nk = (int)(g.K / kBigK);           // real stages
+  const int nsteps = (nk + 3) & ~3;            // padded to the unroll (padding computes zeros)
+  // K stagger: workgroup b starts its K walk at stage (b / 8) mod nk. The 32 tiles an
+  // XCD runs together then read different K offsets of their shared panels at any
+  // moment, which spreads the load over the L2 and the memory behind it (measured
+  // +10-14% on long-K shapes). The accumulation order changes, not the result's
+  // tolerance.
+  const int stag = __builtin_amdgcn_readfirstlane((int)((blockIdx.x >> 3) % (unsigned)nk));
+
+  // Direct loads: wavefronts 0-1 fetch the 256 weight rows, 2-3 the 256 activation rows
+  // (128 each), 64 K bytes per stage. Load jj of a wavefront fills LDS rows
+  // 128 (w & 1) + 16 jj + L/4 (lane L) of its operand; lane L fetches logical chunk
+  // (L & 3) ^ ((L >> 4) & 3) and the hardware writes it at physical chunk L & 3, so
+  // row r holds logical chunk c at c ^ ((r >> 2) & 3). The buffer window of a wavefront
+  // ends at the operand's last row: rows past M / N read zero (never stored).
+  const bool w_wave = wave_u < 2;
+  const int64_t ld = w_wave ? g.ldw : g.lda;
+  const int ld_u = __builtin_amdgcn_readfirstlane((int)ld);
+  const OperandWindow win = operand_window((w_wave ? n_base : m_base) + (wave_u & 1) * 128, w_wave ? g.N : g.M, ld);
+  const __amdgpu_buffer_rsrc_t op_rsrc = uniform_rsrc((w_wave ? g.w : g.a) + win.base_offset, win.records);
+  const int voff = (lane >> 2) * ld_u + (((lane & 3) ^ ((lane >> 4) & 3)) << 4);
+  // Issue step s (< nsteps) into stage buffer `dst`. A padded step (s >= nk) reads at an
+  // offset past every buffer window, which returns zeros: its fragments are zero and it
+  // adds nothing.
+  auto issue = [&](int s, uint8_t* dst) {
+    int ks = (s < nk ? s : nk - 1) + stag;
+    ks = __builtin_amdgcn_readfirstlane(ks >= nk ? ks - nk : ks);
+    const int pad_off = __builtin_amdgcn_readfirstlane(s < nk ? 0 : 0x40000000);
+#pragma unroll
+    for (int jj = 0; jj < kDma; ++jj) {
+      const int soff = __builtin_amdgcn_readfirstlane(jj * 16 * ld_u + ks * kBigK + pad_off);
+      __builtin_amdgcn_raw_ptr_buffer_load_lds(op_rsrc, (__attribute__((address_space(3))) void*)(dst + (wave_u * kDma + jj) * 1024),
+                                               16, voff, soff, 0, 0);
+    }
+  };
+
+  // Fragment reads: row r = tile_row0 + frow, whose swizzle (r >> 2) & 3 equals
+  // (frow >> 2) & 3 for every fragment, so two per-lane offsets address all of them.
+  const int fsw = (frow >> 2) & 3;
+  const int c0 = (h ^ fsw) << 4, c1 = ((2 + h) ^ fsw) << 4;
+  auto frag = [&](const uint8_t* buf, int tile_row0) -> v8i {
+    const uint8_t* base = buf + (tile_row0 + frow) * kBigK;
+    const uint4 lo = *reinterpret_cast<const uint4*>(base + c0);
+    const uint4 hi = *reinterpret_cast<const uint4*>(base + c1);
+    v8i r;
+    r[0] = (int)lo.x; r[1] = (int)lo.y; r[2] = (int)lo.z; r[3] = (int)lo.w;
+    r[4] = (int)hi.x; r[5] = (int)hi.y; r[6] = (int)hi.z; r[7] = (int)hi.w;
+    return r;
+  };
+  v8i wf[2][FN], af[2][FM];  // fragments of the current and the next step
+  auto read_frags = [&](int set, const uint8_t* buf) {
+#pragma unroll
+    for (int i = 0; i < FN; ++i) wf[set][i] = frag(buf, wn * 128 + i * 32);
+#pragma unroll
+    for (int j = 0; j < FM; ++j) af[set][j] = frag(buf + kBigTile * kBigK, wm * 128 + j * 32);
+  };
+
+  // Declaring an AGPR clobber makes the compiler select the AGPR form of the MFMAs,
+  // so the 256 accumulators live in the accumulation registers and the 256
+  // architectural VGPRs stay free for fragments and addresses.
+  asm volatile("" ::: "a255");
+  v16f acc[FN][FM];
+#pragma unroll
+  for (int i = 0; i < FN; ++i)
+#pragma unroll
+    for (int j = 0; j < FM; ++j)
+#pragma unroll
+      for (int r = 0; r < 16; ++r) acc[i][j][r] = 0.0f;
+  auto mfmas = [&](int set, int j0) {
+#pragma unroll
+    for (int j = j0; j < j0 + 2; ++j)
+#pragma unroll
+      for (int i = 0; i < FN; ++i) acc[i][j] = mfma(wf[set][i], af[set][j], acc[i][j], kScaleOne, kScaleOne);
+  };
+
+  // Prologue: steps 0-3 in flight, step 0 visible, its fragments in set 0.
+  issue(0, L0);
+  issue(1, L1);
+  issue(2, L2);
+  issue(3, L3);
+  wait_vmcnt<3 * kOps>();
+  lds_barrier();
+  read_frags(0, L0);
+
+  // Step s: the first half of its MFMAs; then "step s + 1 has landed" (the wavefront's
+  // own loads: steps s + 2 and s + 3 may still be in flight) and a barrier, which also
+  // certifies that every wavefront has its step-s fragments in registers, so step s's
+  // buffer is refilled with step s + 4; then step s + 1's fragments are read while the
+  // second half of step s's MFMAs runs. Everything a wait depends on is issued in a
+  // fixed order, so the counts are exact; the body has no branches.
+  auto step = [&](int s, int set, uint8_t* cur, uint8_t* nxt) {
+    mfmas(set, 0);
+    __builtin_amdgcn_sched_barrier(0);
+    wait_vmcnt<2 * kOps>();
+    lds_barrier();
+    __builtin_amdgcn_sched_barrier(0);
+    issue(s + 4 < nsteps ? s + 4 : nsteps - 1, cur);
+    read_frags(set ^ 1, nxt);
+    mfmas(set, 2);
+  };
+  for (int s = 0; s < nsteps; s += 4) {
+    step(s, 0, L0, L1);
+    step(s + 1, 1, L1, L2);
+    step(s + 2, 0, L2, L3);
+    step(s + 3, 1, L3, L0);
+  }
+  // Every issued load has landed and no wavefront still reads a stage buffer.
+  wait_vmcnt<0>();
+  lds_barrier();
+  if (g.out_dtype == AYK_BF16) big_epilogue<MODE, AYK_BF16>(g, acc, m_base, n_base, L0);
+  else if (g.out_dtype == AYK_F16) big_epilogue<MODE, AYK_F16>(g, acc, m_base, n_base, L0);
+  else big_epilogue<MODE, AYK_F32>(g, acc, m_base, n_base, L0);
+}
+
+// MXFP8 large-tile kernel with 128-K stages: two 64 KB LDS stages, one code dword (four
+// UE8M0 codes) per fragment row and stage. The 64-K-stage kernel above would need one
+// code load per row and stage, which doubles its L2 request count; until its codes
+// travel in wider blocks, MXFP8 keeps this pipeline (K % 128 == 0).
+constexpr int kMx128Stage = 2 * kBigTile * BK;  // 64 KB
+
+template <int MODE>
+__global__ __launch_bounds__(kThreads, 1) void fp8_gemm_mx128_kernel(GemmArgs g) {
+  static_assert(MODE == MODE_MX, "MX codes only");
   constexpr int FN = 4, FM = 4;                  // 32x32 MFMA tiles per wavefront (n, m)
-  constexpr int kLoads = kBigStage / 1024 / 4;   // direct loads per wavefront per stage
+  constexpr int kLoads = kMx128Stage / 1024 / 4;   // direct loads per wavefront per stage
   // Two distinct LDS objects (not one array indexed by stage), so the compiler can
   // tell that reads of one stage never alias the in-flight direct loads of the other
   // and does not wait for those loads before reading.
-  __shared__ __attribute__((aligned(1024))) uint8_t lds0[kBigStage];
-  __shared__ __attribute__((aligned(1024))) uint8_t lds1[kBigStage];
+  __shared__ __attribute__((aligned(1024))) uint8_t lds0[kMx128Stage];
+  __shared__ __attribute__((aligned(1024))) uint8_t lds1[kMx128Stage];
 
   const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
   const int wn = wave >> 1, wm = wave & 1;
@@ -467,8 +639,7 @@ __global__ __launch_bounds__(kThreads, 1) void fp8_gemm_big_kernel(GemmArgs g) {
   const int64_t ld = w_wave ? g.ldw : g.lda;
   const int64_t row0 = (w_wave ? n_base : m_base) + (wave_u & 1) * 128;
   const OperandWindow win = operand_window(row0, w_wave ? g.N : g.M, ld);
-  const __amdgpu_buffer_rsrc_t op_rsrc = __builtin_amdgcn_make_buffer_rsrc(
-      const_cast<uint8_t*>((w_wave ? g.w : g.a) + win.base_offset), (short)0, win.records, kBufferFlags);
+  const __amdgpu_buffer_rsrc_t op_rsrc = uniform_rsrc((w_wave ? g.w : g.a) + win.base_offset, win.records);
   const int voff[2] = {(int)(q * ld) + ((pc ^ ((q >> 1) & 7)) << 4), (int)(q * ld) + ((pc ^ ((4 + (q >> 1)) & 7)) << 4)};
   auto issue_stage = [&](int kt, uint8_t* dst) {
 #pragma unroll
@@ -497,10 +668,8 @@ __global__ __launch_bounds__(kThreads, 1) void fp8_gemm_big_kernel(GemmArgs g) {
   // MX codes via buffer loads as well: rows past M / N read zero codes (never stored).
   const OperandWindow wcw = MODE == MODE_MX ? operand_window(n_base + (wave_u >> 1) * 128, g.N, g.ld_sb) : OperandWindow{0, 0};
   const OperandWindow acw = MODE == MODE_MX ? operand_window(m_base + (wave_u & 1) * 128, g.M, g.ld_sa) : OperandWindow{0, 0};
-  const __amdgpu_buffer_rsrc_t wcode_rsrc = __builtin_amdgcn_make_buffer_rsrc(
-      const_cast<uint8_t*>(reinterpret_cast<const uint8_t*>(g.sb) + wcw.base_offset), (short)0, wcw.records, kBufferFlags);
-  const __amdgpu_buffer_rsrc_t acode_rsrc = __builtin_amdgcn_make_buffer_rsrc(
-      const_cast<uint8_t*>(reinterpret_cast<const uint8_t*>(g.sa) + acw.base_offset), (short)0, acw.records, kBufferFlags);
+  const __amdgpu_buffer_rsrc_t wcode_rsrc = uniform_rsrc(reinterpret_cast<const uint8_t*>(g.sb) + wcw.base_offset, wcw.records);
+  const __amdgpu_buffer_rsrc_t acode_rsrc = uniform_rsrc(reinterpret_cast<const uint8_t*>(g.sa) + acw.base_offset, acw.records);
   auto load_mx_codes = [&](int kt) {
     if constexpr (MODE == MODE_MX) {
 #pragma unroll
@@ -595,7 +764,8 @@ int launch_big(GemmArgs g, hipStream_t st, const char* op) {
   g.tiles_m = (int)cdiv(g.M, kBigTile);
   const int64_t tiles = (int64_t)g.tiles_m * cdiv(g.N, kBigTile);
   if (tiles > 0x7FFFFFFF) return fail(AYK_EINVAL, "%s: problem too large", op);
-  hipLaunchKernelGGL((fp8_gemm_big_kernel<MODE>), dim3((unsigned)tiles), dim3(kThreads), 0, st, g);
+  if constexpr (MODE == MODE_MX) hipLaunchKernelGGL((fp8_gemm_mx128_kernel<MODE_MX>), dim3((unsigned)tiles), dim3(kThreads), 0, st, g);
+  else hipLaunchKernelGGL((fp8_gemm_big_kernel<MODE>), dim3((unsigned)tiles), dim3(kThreads), 0, st, g);
   return check_launch(op);
 }
 
@@ -610,12 +780,12 @@ int launch_cfg(GemmArgs g, hipStream_t st, const char* op) {
 
 template <int MODE>
 int launch_gemm(const GemmArgs& g, hipStream_t st, const char* op) {
-  // The large-tile kernel needs K % 128 == 0, fp32 scales, N % 4 == 0 and 16-byte
+  // The large-tile kernels need K % 64 == 0 (128 for MXFP8), fp32 scales, N % 4 == 0 and 16-byte
   // aligned output rows (its epilogue stores 16-byte chunks); anything else runs the
   // general kernel.
   if constexpr (MODE != MODE_BLOCK) {
   const int64_t out_bytes = g.out_dtype == AYK_F32 ? 4 : 2;
-  const bool big_ok = g.K % BK == 0 && g.M >= 256 && g.N >= 256 && g.N % 4 == 0 &&
+  const bool big_ok = g.K % (MODE == MODE_MX ? BK : kBigK) == 0 && g.M >= 256 && g.N >= 256 && g.N % 4 == 0 &&
                       (g.ldo * out_bytes) % 16 == 0 && aligned16(g.out) &&
                       (MODE == MODE_MX || (g.sa_dtype == AYK_F32 && g.sb_dtype == AYK_F32 &&
                                            (!g.sb_vec || aligned16(g.sb)))) &&

@@ -115,8 +115,10 @@ def _time_dominant(layers, launches_per_graph=24, replays=5):
     return n, k, sum(per_launch) / len(per_launch), per_launch[len(per_launch) // 2]
 
 
-def _bench_gemm(device, reps=10):
-    """Prefill GEMMs at M = 4096 on the config shapes (supplemental M for MXFP8)."""
+def _bench_gemm(device, reps=20, warmup=5):
+    """Prefill GEMMs at M = 4096 on the config shapes (supplemental M for MXFP8). Each is
+    timed over `reps` launches after `warmup` untimed ones (the clocks settle over the
+    first few milliseconds of matrix-core load)."""
     from ayaka.kernel.hip import fp8_blockwise_mm, fp8_scaled_mm, mxfp8_scaled_mm
 
     g = torch.Generator(device=device).manual_seed(0)
@@ -124,7 +126,8 @@ def _bench_gemm(device, reps=10):
     results = {}
 
     def run(label, n, k, fn):
-        fn()
+        for _ in range(warmup):
+            fn()
         torch.cuda.synchronize()
         start, end = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
         start.record()

@@ -86,7 +86,9 @@ def test_blockwise_gemv(gpu, n, k):
 
 # ------------------------------------------------------------------ W8A8 GEMMs
 MNK = [(8, 3072, 1024), (17, 300, 256), (64, 256, 384), (200, 1000, 1024), (256, 512, 2048), (129, 130, 528),
-       (300, 520, 1024), (513, 772, 2048), (1024, 1024, 3584)]  # the last three take the 256x256 kernel
+       (300, 520, 1024), (513, 772, 2048), (1024, 1024, 3584),
+       # 256x256 kernel with 1, 5 and 19 K stages of 64: steps padded to a multiple of four
+       (256, 256, 64), (400, 300, 320), (260, 1028, 1216)]  # from (300, 520, 1024) on: the 256x256 kernel
 
 
 @pytest.mark.parametrize("m,n,k", MNK)
