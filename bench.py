@@ -18,7 +18,7 @@ GEMMs at M = 4096 (TFLOP/s against the 5.0 PFLOP/s dense fp8 peak) and
 ``cpu_baseline`` times the reference's CPU path (the oracle restatement) on a
 bounded sample on this host's cores.
 
-Usage: python bench.py [--gpus 1] [--steps K] [--warmup W] [--no-gemm] [--no-cpu]
+Usage: python bench.py [--gpus 1] [--steps K] [--warmup W] [--no-gemm] [--no-cpu] [--copy-probe]
 """
 
 import argparse
@@ -232,6 +232,33 @@ def _cpu_baseline():
             f"{sec:.2f} s per pass; oracle/fp8_oracle.fp8_linear('w8a16') on torch CPU"}
 
 
+TRAFFIC_PROFILE = os.path.join(ROOT, "profiles", "gemv_gate_up_traffic.md")
+
+
+def _measured_traffic():
+    """HBM bytes per gate_up GEMV launch from the committed counter summary (FETCH_SIZE +
+    WRITE_SIZE, scaled by the copy-kernel calibration it records), or None."""
+    try:
+        with open(TRAFFIC_PROFILE) as f:
+            for line in f:
+                if line.strip().startswith("traffic_bytes_per_launch:"):
+                    return int(line.split(":", 1)[1].strip())
+    except (OSError, ValueError):
+        return None
+    return None
+
+
+def _copy_probe(device, mib=256, reps=5):
+    """A plain device copy of a known size (counter calibration for the traffic figure)."""
+    src = torch.ones(mib << 18, dtype=torch.float32, device=device)
+    dst = torch.empty_like(src)
+    for _ in range(reps):
+        dst.copy_(src)
+    torch.cuda.synchronize()
+    print(json.dumps({"copy_probe_bytes_read": src.numel() * 4, "copy_probe_bytes_written": dst.numel() * 4,
+                      "launches": reps}), flush=True)
+
+
 def main() -> int:
     ap = argparse.ArgumentParser()
     ap.add_argument("--gpus", type=int, default=1)
@@ -239,6 +266,7 @@ def main() -> int:
     ap.add_argument("--warmup", type=int, default=10)
     ap.add_argument("--no-gemm", action="store_true")
     ap.add_argument("--no-cpu", action="store_true")
+    ap.add_argument("--copy-probe", action="store_true", help="only run a 256 MiB device copy (counter calibration)")
     args = ap.parse_args()
     if args.gpus != 1:
         print(f"bench.py measures one GPU only (got --gpus {args.gpus}); the FP8 linear path is "
@@ -249,6 +277,9 @@ def main() -> int:
 
     device = torch.device("cuda:0")
     torch.cuda.set_device(device)
+    if args.copy_probe:
+        _copy_probe(device)
+        return 0
     layers = _make_cfg2(device)
     outs = [torch.empty(n, dtype=torch.bfloat16, device=device) for _, n, _, _, _ in layers]
     step_bytes = sum(_gemv_bytes(n, k) for _, n, k, _, _ in layers)
@@ -299,7 +330,7 @@ def main() -> int:
         "roofline": {"bound": "hbm", "kernel": "gemv_kernel (gate_up 28672x4096)", "achieved": round(achieved, 1),
                      "peak": HBM_PEAK_GBS, "unit": "GB/s", "frac": round(achieved / HBM_PEAK_GBS, 4),
                      "avg_launch_us": round(avg_ms * 1e3, 2), "median_launch_us": round(med_ms * 1e3, 2),
-                     "bytes_per_launch": _gemv_bytes(n, k), "traffic": None},
+                     "bytes_per_launch": _gemv_bytes(n, k), "traffic": _measured_traffic()},
     }
     result["decode_w8a16"] = _bench_decode_m(layers)
     if not args.no_gemm:
