@@ -303,8 +303,8 @@ __global__ __launch_bounds__(kThreads) void fp8_gemm_kernel(GemmArgs g) {
 //    matrix cores idle.
 //  * Workgroup b runs on XCD b % 8. Tiles are numbered so that each XCD owns a
 //    contiguous range of an M-grouped order (8 M tiles per group): the ~32 tiles an
-//    XCD runs at once share 8 activation and 4 weight panels through its L2, and each
-//    starts its K walk at a different stage.
+//    XCD runs at once share 8 activation and 4 weight panels through its L2; their K
+//    walks start a few stages apart.
 //  * Every wait on the vector-memory counter is written out with its exact count
 //    (it retires in issue order); buffer windows end at the operand's last row, so
 //    rows past M / N read zero and are never stored.
@@ -488,12 +488,13 @@ __global__ __launch_bounds__(kThreads, 1) void fp8_gemm_big_kernel(GemmArgs g) {
   const int64_t n_base = (int64_t)tn * kBigTile, m_base = (int64_t)tm * kBigTile;
   const int nk = (int)(g.K / kBigK);           // real stages
   const int nsteps = (nk + 3) & ~3;            // padded to the unroll (padding computes zeros)
-  // K stagger: workgroup b starts its K walk at stage (b / 8) mod nk. The 32 tiles an
-  // XCD runs together then read different K offsets of their shared panels at any
-  // moment, which spreads the load over the L2 and the memory behind it (measured
-  // +10-14% on long-K shapes). The accumulation order changes, not the result's
-  // tolerance.
-  const int stag = __builtin_amdgcn_readfirstlane((int)((blockIdx.x >> 3) % (unsigned)nk));
+  // K stagger: the tile starts its K walk at stage 2 (tm mod 8) + (tn mod 2) (mod nk).
+  // The 32 tiles an XCD runs together are then a few stages apart: their requests no
+  // longer arrive in lockstep, while the panel slices they share are still in the L2
+  // when the later tiles reach them. Measured against no stagger and against larger
+  // offsets on the config shapes: +5-15%. The accumulation order changes, not the
+  // result's tolerance.
+  const int stag = __builtin_amdgcn_readfirstlane((int)((unsigned)((tm & 7) * 2 + (tn & 1)) % (unsigned)nk));
 
   // Direct loads: wavefronts 0-1 fetch the 256 weight rows, 2-3 the 256 activation rows
   // (128 each), 64 K bytes per stage. Load jj of a wavefront fills LDS rows
