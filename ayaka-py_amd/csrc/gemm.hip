@@ -601,6 +601,270 @@ __global__ __launch_bounds__(kThreads, 1) void fp8_gemm_big_kernel(GemmArgs g) {
   else big_epilogue<MODE, AYK_F32>(g, acc, m_base, n_base, L0);
 }
 
+// ---------------------------------------------------------------------------------
+// Block-scaled kernel (fp8_blockwise_mm; K % 128 == 0, M and N >= 128): a 128 x 128
+// output tile per workgroup of four wavefronts, each owning a 64 (n) x 64 (m) tile
+// (2 x 2 MFMA tiles).
+//
+// The reference scales every 128-K partial product by sa[m, kb] * sb[n / 128, kb]
+// before summing. Each wavefront keeps its partials in AGPRs (the MFMA accumulator,
+// restarted from zero at each 128-K block) and the running sum in VGPRs: at the end of
+// a block, one fma per element moves partial * (sa * sb) into the sum (VALU cannot read
+// AGPRs, so the sum cannot live there). Larger tiles need more registers for the sums
+// than a wavefront has beside its fragments. The partials of m-fragment 0 are folded
+// at the end of the block's second step, those of m-fragment 1 at the start of the
+// next block's first step, so the VALU work runs beside MFMAs. The loads follow the
+// 256 x 256 kernel (64-K stages in a four-buffer LDS ring, direct-to-LDS, one mid-step
+// barrier); each block's three scales (two sa rows per lane, one sb per wavefront: its
+// 64 weight rows lie in one 128-row block) are loaded one block ahead.
+constexpr int kBlkThreads = 256;
+constexpr int kBlkTile = 128;
+constexpr int kBlkStage = 2 * kBlkTile * kBigK;             // 16 KB
+constexpr int kBlkEpilogueLds = 32 * (kBlkTile * 4 + 16);   // 32 staged rows of fp32
+
+template <int OUT>
+__device__ inline void block_epilogue(const GemmArgs& g, const float (&acc)[2][2][16], int64_t m_tile, int64_t n_tile,
+                                      uint8_t* ep) {
+  constexpr int EB = OutBytes<OUT>::v;
+  constexpr int kRowBytes = kBlkTile * EB + 16;
+  constexpr int kChunksPerRow = kBlkTile * EB / 16;
+  constexpr int kRowsPerStep = kBlkThreads / kChunksPerRow;
+  const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+  const int wn = wave >> 1, wm = wave & 1, h = lane >> 5, frow = lane & 31;
+#pragma unroll
+  for (int wmh = 0; wmh < 2; ++wmh) {
+#pragma unroll
+    for (int j = 0; j < 2; ++j) {
+      if (wm == wmh) {  // the two wavefronts of this m half write its 32 rows j
+        uint8_t* srow = ep + frow * kRowBytes;
+#pragma unroll
+        for (int i = 0; i < 2; ++i) {
+#pragma unroll
+          for (int grp = 0; grp < 4; ++grp) {
+            const int nl = wn * 64 + i * 32 + grp * 8 + h * 4;
+            const int64_t n = n_tile + nl;
+            float bias[4] = {0.0f, 0.0f, 0.0f, 0.0f};
+            if (g.bias && n < g.N) load_bias4(g, n, bias);
+            float v[4];
+#pragma unroll
+            for (int q = 0; q < 4; ++q) v[q] = acc[i][j][grp * 4 + q] + bias[q];
+            if constexpr (OUT == AYK_F32) {
+              *reinterpret_cast<float4*>(srow + nl * 4) = make_float4(v[0], v[1], v[2], v[3]);
+            } else {
+              uint16_t b[4];
+#pragma unroll
+              for (int q = 0; q < 4; ++q) b[q] = OUT == AYK_BF16 ? f32_to_bf16_bits(v[q]) : f32_to_f16_bits(v[q]);
+              *reinterpret_cast<uint2*>(srow + nl * 2) =
+                  make_uint2((uint32_t)b[0] | ((uint32_t)b[1] << 16), (uint32_t)b[2] | ((uint32_t)b[3] << 16));
+            }
+          }
+        }
+      }
+      lds_barrier();
+#pragma unroll
+      for (int r0 = 0; r0 < 32; r0 += kRowsPerStep) {
+        const int r = r0 + tid / kChunksPerRow, c = tid % kChunksPerRow;
+        const int64_t gm = m_tile + wmh * 64 + j * 32 + r;
+        const int64_t gn = n_tile + (int64_t)c * (16 / EB);
+        if (gm < g.M && gn < g.N) {
+          const uint4 val = *reinterpret_cast<const uint4*>(ep + r * kRowBytes + c * 16);
+          uint8_t* dst = reinterpret_cast<uint8_t*>(g.out) + (gm * g.ldo + gn) * EB;
+          if (gn + 16 / EB <= g.N) *reinterpret_cast<uint4*>(dst) = val;
+          else *reinterpret_cast<uint2*>(dst) = make_uint2(val.x, val.y);  // N % 4 == 0
+        }
+      }
+      lds_barrier();
+    }
+  }
+}
+
+__global__ __launch_bounds__(kBlkThreads, 1) void fp8_gemm_block_kernel(GemmArgs g) {
+  constexpr int FN = 2, FM = 2;
+  constexpr int kWDma = 2, kADma = 2;           // direct loads per wavefront per step
+  constexpr int kDma = kWDma + kADma;
+  constexpr int kScaleOps = 3;                  // per block, issued one block ahead
+  // Ops issued per step alternate kDma + kScaleOps (a block's first step: the refill and
+  // the next block's scales) and kDma, so any two consecutive steps issue this many:
+  constexpr int kAfterNext = 2 * kDma + kScaleOps;
+  __shared__ __attribute__((aligned(1024))) uint8_t L0[kBlkEpilogueLds > kBlkStage ? kBlkEpilogueLds : kBlkStage];
+  __shared__ __attribute__((aligned(1024))) uint8_t L1[kBlkStage];
+  __shared__ __attribute__((aligned(1024))) uint8_t L2[kBlkStage];
+  __shared__ __attribute__((aligned(1024))) uint8_t L3[kBlkStage];
+
+  const int tid = threadIdx.x, lane = tid & 63;
+  const int wave_u = __builtin_amdgcn_readfirstlane(tid >> 6);
+  const int wn = wave_u >> 1, wm = wave_u & 1;  // 64-row n half, 64-row m half
+  const int h = lane >> 5, frow = lane & 31;
+  int tm, tn;
+  big_tile_coords(blockIdx.x, g.tiles_m, (int)cdiv(g.N, kBlkTile), tm, tn);
+  const int64_t n_base = (int64_t)tn * kBlkTile, m_base = (int64_t)tm * kBlkTile;
+  const int nk = (int)(g.K / kBigK);     // even: K % 128 == 0
+  const int kblocks = nk / 2;
+  const int nsteps = (nk + 3) & ~3;      // the loop is unrolled by four steps (two blocks)
+  // K stagger (even, so 128-K blocks stay aligned): see the 256 x 256 kernel.
+  const int stag = __builtin_amdgcn_readfirstlane((int)((unsigned)(((tm & 7) + (tn & 1)) * 2) % (unsigned)nk));
+
+  // Direct loads: wavefront w fetches weight rows [32 w, 32 w + 32) and activation rows
+  // [32 w, 32 w + 32) (two loads of 16 rows each), swizzled as in the 256 x 256 kernel
+  // (row r holds logical chunk c at c ^ ((r >> 2) & 3)).
+  const int ldw_u = __builtin_amdgcn_readfirstlane((int)g.ldw), lda_u = __builtin_amdgcn_readfirstlane((int)g.lda);
+  const OperandWindow wwin = operand_window(n_base + wave_u * 32, g.N, g.ldw);
+  const OperandWindow awin = operand_window(m_base + wave_u * 32, g.M, g.lda);
+  const __amdgpu_buffer_rsrc_t w_rsrc = uniform_rsrc(g.w + wwin.base_offset, wwin.records);
+  const __amdgpu_buffer_rsrc_t a_rsrc = uniform_rsrc(g.a + awin.base_offset, awin.records);
+  const int sw_chunk = ((lane & 3) ^ ((lane >> 4) & 3)) << 4;
+  const int wvoff = (lane >> 2) * ldw_u + sw_chunk, avoff = (lane >> 2) * lda_u + sw_chunk;
+
+  // Block scales. sa is [M, KB] row-major (element m * KB + kb) or, with sa_vec,
+  // [KB, M] (kb * M + m), fp32; lane (frow, h) needs its two m rows. sb is [NB, KB] in
+  // fp32 / fp16 / bf16, one value per wavefront, kept as the dword that holds it (its
+  // position in the dword is wave-uniform and recomputed at use).
+  int64_t sa_row[FM];
+#pragma unroll
+  for (int j = 0; j < FM; ++j) {
+    const int64_t m = m_base + wm * 64 + j * 32 + frow;
+    sa_row[j] = (m < g.M ? m : g.M - 1) * (g.sa_vec ? 1 : kblocks);
+  }
+  const int64_t nbs = cdiv(g.N, 128);
+  const int64_t nb = (n_base + wn * 64) / 128 < nbs ? (n_base + wn * 64) / 128 : nbs - 1;
+  const int sb_size = g.sb_dtype == AYK_F32 ? 4 : 2;
+  const int64_t sb_base = nb * kblocks;
+  // Two blocks' scales in flight (slot = block % 2). Slot 1 starts as zeros: the first
+  // step folds "the previous block" from it, with zero partials: it adds 0.
+  uint32_t sa_w[2][FM], sb_w[2];
+  sa_w[1][0] = sa_w[1][1] = sb_w[1] = 0u;
+  int kb_of[2] = {0, 0};  // the 128-K block each slot holds (uniform)
+
+  // K stage of step s (padded steps: the last real stage; their loads read zeros).
+  auto stage_of = [&](int s) {
+    const int ks = (s < nk ? s : nk - 1) + stag;
+    return __builtin_amdgcn_readfirstlane(ks >= nk ? ks - nk : ks);
+  };
+  auto issue = [&](int s, uint8_t* dst) {
+    const int ks = stage_of(s);
+    const int pad_off = __builtin_amdgcn_readfirstlane(s < nk ? 0 : 0x40000000);
+#pragma unroll
+    for (int jj = 0; jj < kWDma; ++jj) {
+      const int soff = __builtin_amdgcn_readfirstlane(jj * 16 * ldw_u + ks * kBigK + pad_off);
+      __builtin_amdgcn_raw_ptr_buffer_load_lds(w_rsrc, (__attribute__((address_space(3))) void*)(dst + (wave_u * kWDma + jj) * 1024),
+                                               16, wvoff, soff, 0, 0);
+    }
+#pragma unroll
+    for (int jj = 0; jj < kADma; ++jj) {
+      const int soff = __builtin_amdgcn_readfirstlane(jj * 16 * lda_u + ks * kBigK + pad_off);
+      __builtin_amdgcn_raw_ptr_buffer_load_lds(a_rsrc, (__attribute__((address_space(3))) void*)(dst + kBlkTile * kBigK + (wave_u * kADma + jj) * 1024),
+                                               16, avoff, soff, 0, 0);
+    }
+  };
+  // Scales of the block whose first step is s (block kb = stage / 2) into `slot`.
+  auto issue_scales = [&](int s, int slot) {
+    const int kb = stage_of(s) >> 1;
+    kb_of[slot] = kb;
+    const float* sa_p = reinterpret_cast<const float*>(g.sa);
+#pragma unroll
+    for (int j = 0; j < FM; ++j) sa_w[slot][j] = __float_as_uint(sa_p[g.sa_vec ? (int64_t)kb * g.M + sa_row[j] : sa_row[j] + kb]);
+    const uint8_t* sbp = reinterpret_cast<const uint8_t*>(g.sb) + (sb_base + kb) * sb_size;
+    sb_w[slot] = *reinterpret_cast<const uint32_t*>(sbp - (reinterpret_cast<uintptr_t>(sbp) & 3));
+  };
+
+  const int fsw = (frow >> 2) & 3;
+  const int c0 = (h ^ fsw) << 4, c1 = ((2 + h) ^ fsw) << 4;
+  auto frag = [&](const uint8_t* buf, int row0) -> v8i {
+    const uint8_t* base = buf + (row0 + frow) * kBigK;
+    const uint4 lo = *reinterpret_cast<const uint4*>(base + c0);
+    const uint4 hi = *reinterpret_cast<const uint4*>(base + c1);
+    v8i r;
+    r[0] = (int)lo.x; r[1] = (int)lo.y; r[2] = (int)lo.z; r[3] = (int)lo.w;
+    r[4] = (int)hi.x; r[5] = (int)hi.y; r[6] = (int)hi.z; r[7] = (int)hi.w;
+    return r;
+  };
+  v8i wf[2][FN], af[2][FM];  // fragments of the current and the next step
+  auto read_frags = [&](int set, const uint8_t* buf) {
+#pragma unroll
+    for (int i = 0; i < FN; ++i) wf[set][i] = frag(buf, wn * 64 + i * 32);
+#pragma unroll
+    for (int j = 0; j < FM; ++j) af[set][j] = frag(buf + kBlkTile * kBigK, wm * 64 + j * 32);
+  };
+
+  // The MFMA accumulators (the partials, 64 registers) in AGPRs; the clobber names the
+  // last of them. The sums and fragments take the VGPRs.
+  asm volatile("" ::: "a63");
+  const v16f zero = {};
+  v16f part[FN][FM];
+  float acc[FN][FM][16];
+#pragma unroll
+  for (int i = 0; i < FN; ++i)
+#pragma unroll
+    for (int j = 0; j < FM; ++j) {
+      part[i][j] = zero;
+#pragma unroll
+      for (int r = 0; r < 16; ++r) acc[i][j][r] = 0.0f;
+    }
+  // m-fragment j of a step: fresh partials at a block's first step, accumulate at its second.
+  auto mfmas = [&](int set, int j, bool fresh) {
+#pragma unroll
+    for (int i = 0; i < FN; ++i) part[i][j] = mfma(wf[set][i], af[set][j], fresh ? zero : part[i][j], kScaleOne, kScaleOne);
+  };
+  const uintptr_t sb_addr0 = reinterpret_cast<uintptr_t>(g.sb) + (uintptr_t)(sb_base * sb_size);
+  const bool sb_f32 = g.sb_dtype == AYK_F32, sb_bf16 = g.sb_dtype == AYK_BF16;
+  // Fold m-fragment j's partials of the block in `slot` into the sums. The scale words
+  // pass through an empty asm first, so nothing that reads them is hoisted to where it
+  // would wait for later loads.
+  auto fold = [&](int slot, int j) {
+    uint32_t a = sa_w[slot][j], b = sb_w[slot];
+    asm volatile("" : "+v"(a), "+v"(b));
+    const uint32_t sh = (uint32_t)((sb_addr0 + (uintptr_t)kb_of[slot] * sb_size) & 3) * 8;
+    const uint32_t hb = (b >> sh) & 0xFFFFu;
+    const float f16v = f16_bits_to_f32((uint16_t)hb);
+    const float sbv = sb_f32 ? __uint_as_float(b) : (sb_bf16 ? __uint_as_float(hb << 16) : f16v);
+    const float s = __uint_as_float(a) * sbv;
+#pragma unroll
+    for (int i = 0; i < FN; ++i)
+#pragma unroll
+      for (int r = 0; r < 16; ++r) acc[i][j][r] = fmaf(part[i][j][r], s, acc[i][j][r]);
+  };
+
+  // Prologue: steps 0-3 in flight and block 0's scales, in the order that keeps every
+  // step's wait at kAfterNext (two steps' ops after the one waited for).
+  issue(0, L0);
+  issue(1, L1);
+  issue_scales(0, 0);
+  issue(2, L2);
+  issue(3, L3);
+  wait_vmcnt<kAfterNext + kDma>();  // step 0 landed
+  lds_barrier();
+  read_frags(0, L0);
+
+  // Step s of block s / 2 (slot = block % 2, static under the unroll by four). A
+  // block's first step folds the previous block's m-fragment 1, then refills that slot
+  // with the next block's scales.
+  auto step = [&](int s, int set, bool first, int slot, uint8_t* cur, uint8_t* nxt) {
+    mfmas(set, 0, first);
+    if (first) fold(slot ^ 1, 1);   // the previous block's m-fragment 1 (adds 0 at s == 0)
+    __builtin_amdgcn_sched_barrier(0);
+    wait_vmcnt<kAfterNext>();
+    lds_barrier();
+    __builtin_amdgcn_sched_barrier(0);
+    issue(s + 4 < nsteps ? s + 4 : nsteps - 1, cur);
+    if (first) issue_scales(s + 2 < nsteps ? s + 2 : nsteps - 2, slot ^ 1);
+    read_frags(set ^ 1, nxt);
+    mfmas(set, 1, first);
+    if (!first) fold(slot, 0);
+  };
+  for (int s = 0; s < nsteps; s += 4) {
+    step(s, 0, true, 0, L0, L1);
+    step(s + 1, 1, false, 0, L1, L2);
+    step(s + 2, 0, true, 1, L2, L3);
+    step(s + 3, 1, false, 1, L3, L0);
+  }
+  fold(1, 1);  // the last block's m-fragment 1 (its block index is odd)
+  wait_vmcnt<0>();
+  lds_barrier();
+  if (g.out_dtype == AYK_BF16) block_epilogue<AYK_BF16>(g, acc, m_base, n_base, L0);
+  else if (g.out_dtype == AYK_F16) block_epilogue<AYK_F16>(g, acc, m_base, n_base, L0);
+  else block_epilogue<AYK_F32>(g, acc, m_base, n_base, L0);
+}
+
 // MXFP8 large-tile kernel with 128-K stages: two 64 KB LDS stages, one code dword (four
 // UE8M0 codes) per fragment row and stage. The 64-K-stage kernel above would need one
 // code load per row and stage, which doubles its L2 request count; until its codes
@@ -770,6 +1034,14 @@ int launch_big(GemmArgs g, hipStream_t st, const char* op) {
   return check_launch(op);
 }
 
+int launch_block_big(GemmArgs g, hipStream_t st, const char* op) {
+  g.tiles_m = (int)cdiv(g.M, kBlkTile);
+  const int64_t tiles = (int64_t)g.tiles_m * cdiv(g.N, kBlkTile);
+  if (tiles > 0x7FFFFFFF) return fail(AYK_EINVAL, "%s: problem too large", op);
+  hipLaunchKernelGGL(fp8_gemm_block_kernel, dim3((unsigned)tiles), dim3(kBlkThreads), 0, st, g);
+  return check_launch(op);
+}
+
 template <int MODE, int BN, int BM, int WN, int WM>
 int launch_cfg(GemmArgs g, hipStream_t st, const char* op) {
   g.tiles_m = (int)cdiv(g.M, BM);
@@ -792,6 +1064,14 @@ int launch_gemm(const GemmArgs& g, hipStream_t st, const char* op) {
                                            (!g.sb_vec || aligned16(g.sb)))) &&
                       (g.bias == nullptr || (reinterpret_cast<uintptr_t>(g.bias) & 15) == 0);
   if (big_ok) return launch_big<MODE>(g, st, op);
+  } else {
+    // The block-scaled large-tile kernel: K % 128 == 0, fp32 activation scales, any float
+    // weight-scale dtype, and the same output / bias alignment as above.
+    const int64_t out_bytes = g.out_dtype == AYK_F32 ? 4 : 2;
+    const bool big_ok = g.K % 128 == 0 && g.M >= kBlkTile && g.N >= kBlkTile && g.N % 4 == 0 && g.sa_dtype == AYK_F32 &&
+                        (g.ldo * out_bytes) % 16 == 0 && aligned16(g.out) &&
+                        (g.bias == nullptr || (reinterpret_cast<uintptr_t>(g.bias) & 15) == 0);
+    if (big_ok) return launch_block_big(g, st, op);
   }
   if (g.M <= 32) return launch_cfg<MODE, 128, 32, 4, 1>(g, st, op);
   if (g.M <= 64) return launch_cfg<MODE, 128, 64, 2, 2>(g, st, op);
