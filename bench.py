@@ -327,7 +327,7 @@ def main() -> int:
                    "launch": "one HIP graph per step (4 projections)"},
         "eager": {"ms_per_step": round(eager_ms, 5), "value": round(step_bytes / (eager_ms * 1e-3) / 1e9, 1),
                   "note": "one Python op dispatch per projection, no graph"},
-        "roofline": {"bound": "hbm", "kernel": "gemv_kernel (gate_up 28672x4096)", "achieved": round(achieved, 1),
+        "roofline": {"bound": "hbm", "kernel": "gemv_stream_kernel (gate_up 28672x4096)", "achieved": round(achieved, 1),
                      "peak": HBM_PEAK_GBS, "unit": "GB/s", "frac": round(achieved / HBM_PEAK_GBS, 4),
                      "avg_launch_us": round(avg_ms * 1e3, 2), "median_launch_us": round(med_ms * 1e3, 2),
                      "bytes_per_launch": _gemv_bytes(n, k), "traffic": _measured_traffic()},
