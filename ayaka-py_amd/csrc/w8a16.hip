@@ -234,7 +234,16 @@ __global__ __launch_bounds__(kThreads) void w8a16_gemm_kernel(W16Args g) {
 // M - 1 and their D columns are never stored). K-split partials [split, M, N] are
 // summed in a fixed order by the reduce kernel.
 
-constexpr int kSkRows = 128;          // weight rows per workgroup (4 wavefronts x 32)
+// s_waitcnt with only the vector-memory count constrained (gfx9 encoding: vmcnt in
+// bits [3:0] and [15:14], expcnt [6:4] and lgkmcnt [11:8] left at their maxima).
+template <int N>
+__device__ inline void wait_vmcnt() {
+  static_assert(N >= 0 && N < 64, "vmcnt range");
+  __builtin_amdgcn_s_waitcnt((N & 15) | ((N >> 4) << 14) | (7 << 4) | (15 << 8));
+}
+
+constexpr int kSkRows = 128;          // weight rows per workgroup (32 per wavefront)
+constexpr int kSkThreads = kSkRows * 2;  // 64 lanes per 32 rows
 constexpr int kSkLdsBudget = 80 * 1024;  // two workgroups per CU
 
 // LDS bytes of the staged activation slice (`pitch` elements per row): whole
@@ -278,7 +287,7 @@ __device__ inline v8s convert8(uint32_t lo, uint32_t hi, float s) {
 }
 
 template <bool BF16, bool ROW_SCALE, int D>
-__global__ __launch_bounds__(256) void w8a16_skinny_kernel(SkinnyArgs a) {
+__global__ __launch_bounds__(kSkThreads) void w8a16_skinny_kernel(SkinnyArgs a) {
   extern __shared__ __attribute__((aligned(16))) uint8_t sk_lds[];
   uint16_t* xs = reinterpret_cast<uint16_t*>(sk_lds);
   float* ss = reinterpret_cast<float*>(sk_lds + x_lds_bytes(a.M, a.x_pitch));
@@ -297,20 +306,23 @@ __global__ __launch_bounds__(256) void w8a16_skinny_kernel(SkinnyArgs a) {
 #pragma unroll
     for (int c = 0; c < 4; ++c) ring[d][c] = *reinterpret_cast<const uint4*>(wrow + k + c * 32);
   };
-  // The first D weight steps go out before the staging below, so that their HBM
-  // latency overlaps it.
-#pragma unroll
-  for (int d = 0; d < D; ++d) load(d, kbeg + d * 128);
 
-  // Stage the activation slice with direct-to-LDS loads (no staging registers): one
-  // wavefront instruction fills 64 consecutive 16-byte LDS vectors; vector p of the
-  // padded layout holds x[p / pv][kbeg + 8 * (p % pv) ..] (pv = klen / 8 + 1 vectors
-  // per row, the last one padding, which - like vectors past the last row - is
-  // filled from a clamped, valid address).
+  // Start-up order. The vector-memory counter retires in issue order, so a wait on any
+  // load issued behind the weight ring would wait for the whole ring (and a wait the
+  // compiler cannot place exactly lands inside the K loop, draining the ring on every
+  // iteration). So: (1) the activation slice goes to LDS with direct-to-LDS loads;
+  // (2) the scales: a per-row scale as the raw dword that holds it (converted after the
+  // barrier), or the block-scale table, staged in LDS before any weight load is in
+  // flight; (3) the first D weight steps; (4) one wait for "all but the ring" and a
+  // workgroup barrier.
+  //
+  // (1) Vector p of the padded layout holds x[p / pv][kbeg + 8 * (p % pv) ..] (pv =
+  // klen / 8 + 1 vectors per row, the last one padding, which - like vectors past the
+  // last row - is filled from a clamped, valid address).
   {
     const int pv = a.x_pitch / 8, vpr = klen / 8;
     const int total = (int)a.M * pv;
-    for (int p0 = wave * 64; p0 < total; p0 += 256) {
+    for (int p0 = wave * 64; p0 < total; p0 += kSkThreads) {
       const int p = min(p0 + lane, total - 1);
       const int m = p / pv, c = min(p - m * pv, vpr - 1);
       __builtin_amdgcn_global_load_lds(
@@ -318,18 +330,28 @@ __global__ __launch_bounds__(256) void w8a16_skinny_kernel(SkinnyArgs a) {
           (__attribute__((address_space(3))) void*)(sk_lds + (size_t)__builtin_amdgcn_readfirstlane(p0) * 16), 16, 0, 0);
     }
   }
-  if constexpr (!ROW_SCALE) {
+  // (2)
+  RawBits row_bits{0, 0};
+  if constexpr (ROW_SCALE) {
+    row_bits = load_bits(a.scale, a.scale_dtype, (int64_t)((uint64_t)nrow / (uint64_t)a.by) * a.srs);
+  } else {
     const int64_t c0 = kbeg / a.bx, cmax = (a.K - 1) / a.bx;
-    for (int i = tid; i < kSkRows * a.s_cols; i += 256) {
+    for (int i = tid; i < kSkRows * a.s_cols; i += kSkThreads) {
       const int r = i / a.s_cols, c = i - r * a.s_cols;
       const int64_t n = min(nwg + r, a.N - 1);
       ss[i] = load_f32(a.scale, a.scale_dtype, (n / a.by) * a.srs + min(c0 + c, cmax));
     }
   }
-  __syncthreads();
+  // (3)
+#pragma unroll
+  for (int d = 0; d < D; ++d) load(d, kbeg + d * 128);
+  // (4)
+  wait_vmcnt<4 * D>();
+  __builtin_amdgcn_s_waitcnt(0xC07F);  // lgkmcnt(0): this wavefront's LDS writes are done
+  __builtin_amdgcn_s_barrier();
   if (n0 >= a.N) return;  // whole wavefront past N (uniform; no barrier follows)
 
-  const float row_s = ROW_SCALE ? load_f32(a.scale, a.scale_dtype, (nrow / a.by) * a.srs) : 1.0f;
+  const float row_s = ROW_SCALE ? bits_to_f32(row_bits, a.scale_dtype) : 1.0f;
   const uint16_t* xrow = xs + min(lr, (int)a.M - 1) * a.x_pitch + h * 16;
   const float* srow = ss + (wave * 32 + lr) * a.s_cols;
   const uint32_t bx = (uint32_t)a.bx;
@@ -455,9 +477,9 @@ void launch_skinny_kernel(const SkinnyPlan& p, const SkinnyArgs& a, hipStream_t 
   const dim3 grid((unsigned)cdiv(a.N, kSkRows), (unsigned)p.split);
   const unsigned lds = (unsigned)p.lds;
   switch (p.depth) {
-    case 4: hipLaunchKernelGGL((w8a16_skinny_kernel<BF16, ROW_SCALE, 4>), grid, dim3(256), lds, st, a); break;
-    case 2: hipLaunchKernelGGL((w8a16_skinny_kernel<BF16, ROW_SCALE, 2>), grid, dim3(256), lds, st, a); break;
-    default: hipLaunchKernelGGL((w8a16_skinny_kernel<BF16, ROW_SCALE, 1>), grid, dim3(256), lds, st, a); break;
+    case 4: hipLaunchKernelGGL((w8a16_skinny_kernel<BF16, ROW_SCALE, 4>), grid, dim3(kSkThreads), lds, st, a); break;
+    case 2: hipLaunchKernelGGL((w8a16_skinny_kernel<BF16, ROW_SCALE, 2>), grid, dim3(kSkThreads), lds, st, a); break;
+    default: hipLaunchKernelGGL((w8a16_skinny_kernel<BF16, ROW_SCALE, 1>), grid, dim3(kSkThreads), lds, st, a); break;
   }
 }
 
