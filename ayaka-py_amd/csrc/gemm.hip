@@ -379,9 +379,69 @@ __device__ inline __amdgpu_buffer_rsrc_t uniform_rsrc(const void* base, int32_t 
                                            __builtin_amdgcn_readfirstlane(records), kBufferFlags);
 }
 
-template <int MODE, int OUT>
-__device__ inline void big_epilogue(const GemmArgs& g, const v16f (&acc)[4][4], int64_t m_tile, int64_t n_tile,
-                                    uint8_t* stage_lds) {
+// Output scales of one lane of the 256 x 256 kernels: the activation scale of each of
+// its four m-fragment rows and the weight scales of its 64 output columns. They are
+// loaded before the K loop (and before its first direct load, so the loop's exact
+// vector-memory waits are unaffected) and stay in registers until the epilogue: loaded
+// at the epilogue, their latency stalled every tile while the whole chip was storing.
+struct BigScales {
+  float sa[4];
+  float sb[4][4][4];  // [n-fragment i][column group][column]
+};
+template <int MODE>
+__device__ inline BigScales load_big_scales(const GemmArgs& g, int64_t m_tile, int64_t n_tile) {
+  const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+  const int wn = wave >> 1, wm = wave & 1, h = lane >> 5, frow = lane & 31;
+  BigScales sc;
+#pragma unroll
+  for (int j = 0; j < 4; ++j) sc.sa[j] = 1.0f;
+#pragma unroll
+  for (int i = 0; i < 4; ++i)
+#pragma unroll
+    for (int grp = 0; grp < 4; ++grp)
+#pragma unroll
+      for (int q = 0; q < 4; ++q) sc.sb[i][grp][q] = 1.0f;
+  if constexpr (MODE == MODE_SCALED) {
+    const float* sa_p = reinterpret_cast<const float*>(g.sa);
+    const float* sb_p = reinterpret_cast<const float*>(g.sb);
+#pragma unroll
+    for (int j = 0; j < 4; ++j) {
+      const int64_t m = m_tile + wm * 128 + j * 32 + frow;
+      sc.sa[j] = sa_p[g.sa_vec ? (m < g.M ? m : 0) : 0];
+    }
+    if (g.sb_vec) {
+#pragma unroll
+      for (int i = 0; i < 4; ++i)
+#pragma unroll
+        for (int grp = 0; grp < 4; ++grp) {
+          const int64_t n = n_tile + wn * 128 + i * 32 + grp * 8 + h * 4;
+          const float4 t = *reinterpret_cast<const float4*>(sb_p + (n < g.N ? n : 0));
+          sc.sb[i][grp][0] = t.x; sc.sb[i][grp][1] = t.y; sc.sb[i][grp][2] = t.z; sc.sb[i][grp][3] = t.w;
+        }
+    } else {
+      const float t = sb_p[0];
+#pragma unroll
+      for (int i = 0; i < 4; ++i)
+#pragma unroll
+        for (int grp = 0; grp < 4; ++grp)
+#pragma unroll
+          for (int q = 0; q < 4; ++q) sc.sb[i][grp][q] = t;
+    }
+  }
+  return sc;
+}
+
+// Two floats -> two bf16 (round to nearest even) in one dword, with the gfx950
+// packed converter.
+__device__ inline uint32_t pack_bf16x2(float a, float b) {
+  typedef float f2 __attribute__((ext_vector_type(2)));
+  typedef __bf16 bf2 __attribute__((ext_vector_type(2)));
+  return __builtin_bit_cast(uint32_t, __builtin_convertvector((f2{a, b}), bf2));
+}
+
+template <int MODE, int OUT, bool BIAS>
+__device__ inline void big_epilogue_impl(const GemmArgs& g, const v16f (&acc)[4][4], const BigScales& sc,
+                                         int64_t m_tile, int64_t n_tile, uint8_t* stage_lds) {
   constexpr int EB = OutBytes<OUT>::v;
   constexpr int kRowBytes = 256 * EB + 16;        // padded staging row
   constexpr int kStageRows = EB == 4 ? 32 : 64;   // rows staged at once (fits 64 KB)
@@ -389,13 +449,8 @@ __device__ inline void big_epilogue(const GemmArgs& g, const v16f (&acc)[4][4], 
   static_assert(kStageRows * kRowBytes <= kEpilogueLds, "staging tile must fit the first stage object");
   const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
   const int wn = wave >> 1, wm = wave & 1, h = lane >> 5, frow = lane & 31;
-  const float* sa_p = reinterpret_cast<const float*>(g.sa);
-  const float* sb_p = reinterpret_cast<const float*>(g.sb);
 #pragma unroll
   for (int j = 0; j < 4; ++j) {
-    const int64_t m = m_tile + wm * 128 + j * 32 + frow;
-    float sa = 1.0f;
-    if constexpr (MODE == MODE_SCALED) sa = sa_p[g.sa_vec ? (m < g.M ? m : 0) : 0];
 #pragma unroll
     for (int pass = 0; pass < kPasses; ++pass) {
       if (kPasses == 1 || wm == pass) {
@@ -405,40 +460,34 @@ __device__ inline void big_epilogue(const GemmArgs& g, const v16f (&acc)[4][4], 
 #pragma unroll
           for (int grp = 0; grp < 4; ++grp) {
             const int nl = wn * 128 + i * 32 + grp * 8 + h * 4;  // column within the tile
-            const int64_t n = n_tile + nl;
-            float sb[4] = {1.0f, 1.0f, 1.0f, 1.0f};
             float bias[4] = {0.0f, 0.0f, 0.0f, 0.0f};
-            if (n < g.N) {
-              if constexpr (MODE == MODE_SCALED) {
-                if (g.sb_vec) {
-                  const float4 t = *reinterpret_cast<const float4*>(sb_p + n);
-                  sb[0] = t.x; sb[1] = t.y; sb[2] = t.z; sb[3] = t.w;
-                } else {
-                  sb[0] = sb[1] = sb[2] = sb[3] = sb_p[0];
-                }
-              }
-              if (g.bias) load_bias4(g, n, bias);
+            if constexpr (BIAS) {
+              if (n_tile + nl < g.N) load_bias4(g, n_tile + nl, bias);
             }
             float v[4];
 #pragma unroll
             for (int qq = 0; qq < 4; ++qq) {
               float y = acc[i][j][grp * 4 + qq];
-              if constexpr (MODE == MODE_SCALED) y = (y * sa) * sb[qq];
-              v[qq] = y + bias[qq];
+              if constexpr (MODE == MODE_SCALED) y = (y * sc.sa[j]) * sc.sb[i][grp][qq];
+              v[qq] = BIAS ? y + bias[qq] : y;
             }
             if constexpr (OUT == AYK_F32) {
               *reinterpret_cast<float4*>(srow + nl * 4) = make_float4(v[0], v[1], v[2], v[3]);
+            } else if constexpr (OUT == AYK_BF16) {
+              *reinterpret_cast<uint2*>(srow + nl * 2) = make_uint2(pack_bf16x2(v[0], v[1]), pack_bf16x2(v[2], v[3]));
             } else {
               uint16_t b[4];
 #pragma unroll
-              for (int qq = 0; qq < 4; ++qq) b[qq] = OUT == AYK_BF16 ? f32_to_bf16_bits(v[qq]) : f32_to_f16_bits(v[qq]);
+              for (int qq = 0; qq < 4; ++qq) b[qq] = f32_to_f16_bits(v[qq]);
               *reinterpret_cast<uint2*>(srow + nl * 2) =
                   make_uint2((uint32_t)b[0] | ((uint32_t)b[1] << 16), (uint32_t)b[2] | ((uint32_t)b[3] << 16));
             }
           }
         }
       }
-      __syncthreads();
+      // The staging writes are visible (LDS only: the global stores of the previous pass
+      // need not have completed, they read registers).
+      lds_barrier();
       // Staged row r: with one pass, r < 32 is tile row j*32 + r (wm = 0) and r >= 32
       // is 128 + j*32 + (r - 32) (wm = 1); with two passes, pass*128 + j*32 + r.
       constexpr int kChunksPerRow = 256 * EB / 16;
@@ -460,8 +509,23 @@ __device__ inline void big_epilogue(const GemmArgs& g, const v16f (&acc)[4][4], 
           }
         }
       }
-      __syncthreads();
+      // Every lane has read its chunks of the staging tile before it is rewritten.
+      lds_barrier();
     }
+  }
+}
+
+template <int MODE>
+__device__ inline void big_epilogue(const GemmArgs& g, const v16f (&acc)[4][4], const BigScales& sc, int64_t m_tile,
+                                    int64_t n_tile, uint8_t* stage_lds) {
+  if (g.bias) {
+    if (g.out_dtype == AYK_BF16) big_epilogue_impl<MODE, AYK_BF16, true>(g, acc, sc, m_tile, n_tile, stage_lds);
+    else if (g.out_dtype == AYK_F16) big_epilogue_impl<MODE, AYK_F16, true>(g, acc, sc, m_tile, n_tile, stage_lds);
+    else big_epilogue_impl<MODE, AYK_F32, true>(g, acc, sc, m_tile, n_tile, stage_lds);
+  } else {
+    if (g.out_dtype == AYK_BF16) big_epilogue_impl<MODE, AYK_BF16, false>(g, acc, sc, m_tile, n_tile, stage_lds);
+    else if (g.out_dtype == AYK_F16) big_epilogue_impl<MODE, AYK_F16, false>(g, acc, sc, m_tile, n_tile, stage_lds);
+    else big_epilogue_impl<MODE, AYK_F32, false>(g, acc, sc, m_tile, n_tile, stage_lds);
   }
 }
 
@@ -555,13 +619,17 @@ __global__ __launch_bounds__(kThreads, 1) void fp8_gemm_big_kernel(GemmArgs g) {
     for (int j = 0; j < FM; ++j)
 #pragma unroll
       for (int r = 0; r < 16; ++r) acc[i][j][r] = 0.0f;
-  auto mfmas = [&](int set, int j0) {
+  auto mfmas = [&](int set, int j0, int j1) {
 #pragma unroll
-    for (int j = j0; j < j0 + 2; ++j)
+    for (int j = j0; j < j1; ++j)
 #pragma unroll
       for (int i = 0; i < FN; ++i) acc[i][j] = mfma(wf[set][i], af[set][j], acc[i][j], kScaleOne, kScaleOne);
   };
 
+  constexpr int kHead = 1;  // m-fragments multiplied before the step's barrier
+  // The output scales are loaded first: older than every direct load, they never
+  // count against the loop's vector-memory waits.
+  const BigScales scales = load_big_scales<MODE>(g, m_base, n_base);
   // Prologue: steps 0-3 in flight, step 0 visible, its fragments in set 0.
   issue(0, L0);
   issue(1, L1);
@@ -571,21 +639,22 @@ __global__ __launch_bounds__(kThreads, 1) void fp8_gemm_big_kernel(GemmArgs g) {
   lds_barrier();
   read_frags(0, L0);
 
-  // Step s: the first half of its MFMAs; then "step s + 1 has landed" (the wavefront's
-  // own loads: steps s + 2 and s + 3 may still be in flight) and a barrier, which also
-  // certifies that every wavefront has its step-s fragments in registers, so step s's
-  // buffer is refilled with step s + 4; then step s + 1's fragments are read while the
-  // second half of step s's MFMAs runs. Everything a wait depends on is issued in a
+  // Step s: the MFMAs of its first m-fragment; then "step s + 1 has landed" (the
+  // wavefront's own loads: steps s + 2 and s + 3 may still be in flight) and a barrier,
+  // which also certifies that every wavefront has its step-s fragments in registers, so
+  // step s's buffer is refilled with step s + 4; then step s + 1's fragments are read
+  // while the remaining three quarters of step s's MFMAs run (a longer window than an
+  // even split: +4%). Everything a wait depends on is issued in a
   // fixed order, so the counts are exact; the body has no branches.
   auto step = [&](int s, int set, uint8_t* cur, uint8_t* nxt) {
-    mfmas(set, 0);
+    mfmas(set, 0, kHead);
     __builtin_amdgcn_sched_barrier(0);
     wait_vmcnt<2 * kOps>();
     lds_barrier();
     __builtin_amdgcn_sched_barrier(0);
     issue(s + 4 < nsteps ? s + 4 : nsteps - 1, cur);
     read_frags(set ^ 1, nxt);
-    mfmas(set, 2);
+    mfmas(set, kHead, FM);
   };
   for (int s = 0; s < nsteps; s += 4) {
     step(s, 0, L0, L1);
@@ -596,9 +665,7 @@ __global__ __launch_bounds__(kThreads, 1) void fp8_gemm_big_kernel(GemmArgs g) {
   // Every issued load has landed and no wavefront still reads a stage buffer.
   wait_vmcnt<0>();
   lds_barrier();
-  if (g.out_dtype == AYK_BF16) big_epilogue<MODE, AYK_BF16>(g, acc, m_base, n_base, L0);
-  else if (g.out_dtype == AYK_F16) big_epilogue<MODE, AYK_F16>(g, acc, m_base, n_base, L0);
-  else big_epilogue<MODE, AYK_F32>(g, acc, m_base, n_base, L0);
+  big_epilogue<MODE>(g, acc, scales, m_base, n_base, L0);
 }
 
 // ---------------------------------------------------------------------------------
@@ -1018,9 +1085,7 @@ __global__ __launch_bounds__(kThreads, 1) void fp8_gemm_mx128_kernel(GemmArgs g)
 
   // The last step's barrier guarantees no wavefront still reads lds0 / lds1 and every
   // direct load has landed (the last issue re-loaded a step into the idle buffer).
-  if (g.out_dtype == AYK_BF16) big_epilogue<MODE, AYK_BF16>(g, acc, m_base, n_base, lds0);
-  else if (g.out_dtype == AYK_F16) big_epilogue<MODE, AYK_F16>(g, acc, m_base, n_base, lds0);
-  else big_epilogue<MODE, AYK_F32>(g, acc, m_base, n_base, lds0);
+  big_epilogue<MODE>(g, acc, BigScales{}, m_base, n_base, lds0);
 }
 
 template <int MODE>

@@ -132,6 +132,30 @@ def test_fp8_scaled_mm_big_tile_strided_out(gpu, out_dtype):
     assert torch.all(buf[:, n:].float() == 7.0), "wrote past the output columns"
 
 
+@pytest.mark.parametrize("k", [192, 320, 1088])
+@pytest.mark.parametrize("rowwise,with_bias", [(True, False), (False, True), (True, True)])
+def test_fp8_scaled_mm_many_tiles(gpu, k, rowwise, with_bias):
+    """More 256x256 tiles (9 x 32 = 288) than compute units, so compute units run several
+    tiles; K of 3, 5 and 17 stages (padded steps)."""
+    from ayaka.kernel.hip import fp8_scaled_mm
+
+    m, n = 2304, 8192
+    _say(f"fp8_scaled_mm many tiles m={m} n={n} k={k} rowwise={rowwise} bias={with_bias}")
+    a = _fp8((m, k), seed=31, scale=40)
+    w = _fp8((n, k), seed=32, scale=40)
+    sa = (torch.rand(m, generator=_gen(1)) * 0.01 + 1e-3) if rowwise else torch.tensor(0.004)
+    sb = (torch.rand(n, generator=_gen(2)) * 0.01 + 1e-3) if rowwise else torch.tensor(0.002)
+    bias = torch.randn(n, generator=_gen(3)).to(torch.bfloat16) if with_bias else None
+    ref = ora.fp8_scaled_mm(a, w, sa, sb, bias)
+    out = torch.empty(m, n, dtype=torch.bfloat16, device=gpu)
+    fp8_scaled_mm(a.to(gpu), w.to(gpu).t(), sa.to(gpu), sb.to(gpu), None if bias is None else bias.to(gpu), out=out)
+    assert_linear_close(out, ref, "many tiles bf16")
+    # A second call into the same buffer (every tile is rewritten).
+    out.fill_(float("nan"))
+    fp8_scaled_mm(a.to(gpu), w.to(gpu).t(), sa.to(gpu), sb.to(gpu), None if bias is None else bias.to(gpu), out=out)
+    assert_linear_close(out, ref, "many tiles bf16 (second call)")
+
+
 def test_fp8_scaled_mm_row_major_b_and_odd_k(gpu):
     from ayaka.kernel.hip import fp8_scaled_mm
 
