@@ -35,6 +35,7 @@ namespace {
 
 typedef int v8i __attribute__((ext_vector_type(8)));
 typedef float v16f __attribute__((ext_vector_type(16)));
+typedef int v4i __attribute__((ext_vector_type(4)));
 
 constexpr int kThreads = 256;
 constexpr int BK = 128;
@@ -389,7 +390,7 @@ struct BigScales {
   float sb[4][4][4];  // [n-fragment i][column group][column]
 };
 template <int MODE>
-__device__ inline BigScales load_big_scales(const GemmArgs& g, int64_t m_tile, int64_t n_tile) {
+__device__ __attribute__((always_inline)) inline BigScales load_big_scales(const GemmArgs& g, int64_t m_tile, int64_t n_tile) {
   const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
   const int wn = wave >> 1, wm = wave & 1, h = lane >> 5, frow = lane & 31;
   BigScales sc;
@@ -440,7 +441,7 @@ __device__ inline uint32_t pack_bf16x2(float a, float b) {
 }
 
 template <int MODE, int OUT, bool BIAS>
-__device__ inline void big_epilogue_impl(const GemmArgs& g, const v16f (&acc)[4][4], const BigScales& sc,
+__device__ __attribute__((always_inline)) inline void big_epilogue_impl(const GemmArgs& g, const v16f (&acc)[4][4], const BigScales& sc,
                                          int64_t m_tile, int64_t n_tile, uint8_t* stage_lds) {
   constexpr int EB = OutBytes<OUT>::v;
   constexpr int kRowBytes = 256 * EB + 16;        // padded staging row
@@ -516,7 +517,7 @@ __device__ inline void big_epilogue_impl(const GemmArgs& g, const v16f (&acc)[4]
 }
 
 template <int MODE>
-__device__ inline void big_epilogue(const GemmArgs& g, const v16f (&acc)[4][4], const BigScales& sc, int64_t m_tile,
+__device__ __attribute__((always_inline)) inline void big_epilogue(const GemmArgs& g, const v16f (&acc)[4][4], const BigScales& sc, int64_t m_tile,
                                     int64_t n_tile, uint8_t* stage_lds) {
   if (g.bias) {
     if (g.out_dtype == AYK_BF16) big_epilogue_impl<MODE, AYK_BF16, true>(g, acc, sc, m_tile, n_tile, stage_lds);
@@ -668,6 +669,148 @@ __global__ __launch_bounds__(kThreads, 1) void fp8_gemm_big_kernel(GemmArgs g) {
   big_epilogue<MODE>(g, acc, scales, m_base, n_base, L0);
 }
 
+// The 256 x 256 kernel with 128-byte row loads (K % 128 == 0): a load instruction
+// covers 8 rows x 128 K bytes (two 64-K steps) instead of 16 rows x 64 bytes, which
+// halves the L2 requests per byte (an L2-resident probe reads 57 B/cycle per compute
+// unit with the wide shape against 29 with the narrow one). Stage buffers therefore
+// hold a pair of steps: two 64 KB pair buffers, the second pair's loads in flight while
+// the first is multiplied. The fragment reads, the MFMA order and the epilogue are the
+// narrow kernel's.
+template <int MODE>
+__global__ __launch_bounds__(kThreads, 1) void fp8_gemm_pair_kernel(GemmArgs g) {
+  static_assert(MODE == MODE_SCALED, "per-row / per-tensor scales only");
+  constexpr int FN = 4, FM = 4;        // 32x32 MFMA tiles per wavefront (n, m)
+  constexpr int kPairK = 2 * kBigK;    // 128 K bytes per pair
+  constexpr int kPairBytes = 2 * kBigTile * kPairK;  // 64 KB
+  constexpr int kDma = kPairBytes / 1024 / 4;        // direct loads per wavefront per pair (16)
+  static_assert(kPairBytes == kEpilogueLds, "the first pair buffer holds the epilogue's staging tile");
+  // Two pair buffers in two distinct LDS objects (the compiler tells that reads of one
+  // never alias the in-flight direct loads into the other).
+  __shared__ __attribute__((aligned(1024))) uint8_t P0[kPairBytes];
+  __shared__ __attribute__((aligned(1024))) uint8_t P1[kPairBytes];
+
+  const int tid = threadIdx.x, lane = tid & 63;
+  const int wave_u = __builtin_amdgcn_readfirstlane(tid >> 6);  // keep descriptors in SGPRs
+  const int wn = wave_u >> 1, wm = wave_u & 1;
+  const int h = lane >> 5, frow = lane & 31;
+  int tm, tn;
+  big_tile_coords(blockIdx.x, g.tiles_m, (int)cdiv(g.N, kBigTile), tm, tn);
+  const int64_t n_base = (int64_t)tn * kBigTile, m_base = (int64_t)tm * kBigTile;
+  const int np = (int)(g.K / kPairK);    // real pairs
+  const int npairs = (np + 1) & ~1;      // padded to the unroll (a padded pair computes zeros)
+  // K stagger in pairs: (tm mod 8) + (tn mod 2) (mod np), the narrow kernel's stagger
+  // of 2 (tm mod 8) + (tn mod 2) steps rounded to whole pairs.
+  const int stag = __builtin_amdgcn_readfirstlane((int)((unsigned)((tm & 7) + (tn & 1)) % (unsigned)np));
+
+  // Direct loads: wavefronts 0-1 fetch the 256 weight rows, 2-3 the 256 activation rows
+  // (128 each). Load jj (0-15) of wavefront w reads operand rows 128 (w & 1) + 8 jj +
+  // L/8 (lane L), 128 K bytes; the hardware writes lane L's 16 bytes at physical chunk
+  // L & 7 of LDS row 64 w + 8 (jj & 7) + L/8 of half jj / 8 (32 KB) of the pair buffer.
+  // Row r holds logical chunk c at c ^ ((r >> 1) & 7), so lane L fetches logical chunk
+  // (L & 7) ^ ((4 (jj & 1) + (L >> 4)) & 7). Operand row R (0-255) of wavefront pair
+  // side s (0: weight, 1: activation) is LDS row 64 (2 s + R / 128) + R % 64 of half
+  // (R % 128) / 64.
+  const bool w_wave = wave_u < 2;
+  const int64_t ld = w_wave ? g.ldw : g.lda;
+  const int ld_u = __builtin_amdgcn_readfirstlane((int)ld);
+  const OperandWindow win = operand_window((w_wave ? n_base : m_base) + (wave_u & 1) * 128, w_wave ? g.N : g.M, ld);
+  const __amdgpu_buffer_rsrc_t op_rsrc = uniform_rsrc((w_wave ? g.w : g.a) + win.base_offset, win.records);
+  const int voff_e = (lane >> 3) * ld_u + (((lane & 7) ^ ((lane >> 4) & 7)) << 4);
+  const int voff_o = (lane >> 3) * ld_u + (((lane & 7) ^ ((4 + (lane >> 4)) & 7)) << 4);
+  // Issue pair p (< npairs) into pair buffer `dst`. A padded pair (p >= np) reads past
+  // every buffer window, which returns zeros.
+  auto issue = [&](int p, uint8_t* dst) {
+    int kp = (p < np ? p : np - 1) + stag;
+    kp = __builtin_amdgcn_readfirstlane(kp >= np ? kp - np : kp);
+    const int pad_off = __builtin_amdgcn_readfirstlane(p < np ? 0 : 0x40000000);
+#pragma unroll
+    for (int jj = 0; jj < kDma; ++jj) {
+      const int soff = __builtin_amdgcn_readfirstlane(jj * 8 * ld_u + kp * kPairK + pad_off);
+      __builtin_amdgcn_raw_ptr_buffer_load_lds(
+          op_rsrc, (__attribute__((address_space(3))) void*)(dst + ((jj >> 3) * (kPairBytes / 2) + (wave_u * 8 + (jj & 7)) * 1024)),
+          16, (jj & 1) ? voff_o : voff_e, soff, 0, 0);
+    }
+  };
+
+  // Fragment reads: a fragment's LDS row is frow plus a multiple of 32, so its swizzle
+  // (row >> 1) & 7 is (frow >> 1) & 7 for all of them; step half t of the pair reads
+  // logical chunks 4 t + h and 4 t + 2 + h. One 16-byte load at a single integer offset
+  // from the pair buffer each (see the narrow kernel).
+  const int fsw = (frow >> 1) & 7;
+  const int off_t[2][2] = {{frow * kPairK + ((h ^ fsw) << 4), frow * kPairK + (((2 + h) ^ fsw) << 4)},
+                           {frow * kPairK + (((4 + h) ^ fsw) << 4), frow * kPairK + (((6 + h) ^ fsw) << 4)}};
+  auto frag = [&](const uint8_t* buf, int row0_bytes, int t) -> v8i {
+    const v4i lo = *reinterpret_cast<const v4i*>(buf + (row0_bytes + off_t[t][0]));
+    const v4i hi = *reinterpret_cast<const v4i*>(buf + (row0_bytes + off_t[t][1]));
+    return __builtin_shufflevector(lo, hi, 0, 1, 2, 3, 4, 5, 6, 7);
+  };
+  // Byte offset of the first row of operand rows [R, R + 32) (R % 32 == 0) of side s.
+  auto rows_at = [](int s, int R) { return ((R & 127) >> 6) * (kPairBytes / 2) + (64 * (2 * s + (R >> 7)) + (R & 63)) * kPairK; };
+  v8i wf[2][FN], af[2][FM];  // fragments of the current and the next step
+  auto read_frags = [&](int set, const uint8_t* buf, int t) {
+#pragma unroll
+    for (int i = 0; i < FN; ++i) wf[set][i] = frag(buf, rows_at(0, wn * 128 + i * 32), t);
+#pragma unroll
+    for (int j = 0; j < FM; ++j) af[set][j] = frag(buf, rows_at(1, wm * 128 + j * 32), t);
+  };
+
+  // Declaring an AGPR clobber makes the compiler select the AGPR form of the MFMAs.
+  asm volatile("" ::: "a255");
+  v16f acc[FN][FM];
+#pragma unroll
+  for (int i = 0; i < FN; ++i)
+#pragma unroll
+    for (int j = 0; j < FM; ++j)
+#pragma unroll
+      for (int r = 0; r < 16; ++r) acc[i][j][r] = 0.0f;
+  auto mfmas = [&](int set, int j0, int j1) {
+#pragma unroll
+    for (int j = j0; j < j1; ++j)
+#pragma unroll
+      for (int i = 0; i < FN; ++i) acc[i][j] = mfma(wf[set][i], af[set][j], acc[i][j], kScaleOne, kScaleOne);
+  };
+  constexpr int kHead = 1;  // m-fragments multiplied before the step's barrier
+
+  const BigScales scales = load_big_scales<MODE>(g, m_base, n_base);
+  // Prologue: pairs 0 and 1 in flight, pair 0 visible, step (0, 0)'s fragments in set 0.
+  issue(0, P0);
+  issue(1, P1);
+  wait_vmcnt<kDma>();
+  lds_barrier();
+  read_frags(0, P0, 0);
+
+  // Pair p in `cur`, pair p + 1 in flight into `nxt`. Its first step: the barrier (the
+  // whole pair has landed) certifies every wavefront has its step fragments, then the
+  // second step's fragments are read from the same buffer. Its second step: "pair p + 1
+  // has landed" (nothing else is in flight) and a barrier, after which no wavefront reads
+  // `cur` any more: pair p + 2 is issued into it and the next pair's first fragments are
+  // read from `nxt`.
+  auto pair = [&](int p, uint8_t* cur, uint8_t* nxt) {
+    mfmas(0, 0, kHead);
+    __builtin_amdgcn_sched_barrier(0);
+    lds_barrier();
+    __builtin_amdgcn_sched_barrier(0);
+    read_frags(1, cur, 1);
+    mfmas(0, kHead, FM);
+    mfmas(1, 0, kHead);
+    __builtin_amdgcn_sched_barrier(0);
+    wait_vmcnt<0>();
+    lds_barrier();
+    __builtin_amdgcn_sched_barrier(0);
+    issue(p + 2 < npairs ? p + 2 : npairs - 1, cur);
+    read_frags(0, nxt, 0);
+    mfmas(1, kHead, FM);
+  };
+  for (int p = 0; p < npairs; p += 2) {
+    pair(p, P0, P1);
+    pair(p + 1, P1, P0);
+  }
+  // Every issued load has landed and no wavefront still reads a pair buffer.
+  wait_vmcnt<0>();
+  lds_barrier();
+  big_epilogue<MODE>(g, acc, scales, m_base, n_base, P0);
+}
+
 // ---------------------------------------------------------------------------------
 // Block-scaled kernel (fp8_blockwise_mm; K % 128 == 0, M and N >= 128): a 128 x 128
 // output tile per workgroup of four wavefronts, each owning a 64 (n) x 64 (m) tile
@@ -690,7 +833,7 @@ constexpr int kBlkStage = 2 * kBlkTile * kBigK;             // 16 KB
 constexpr int kBlkEpilogueLds = 32 * (kBlkTile * 4 + 16);   // 32 staged rows of fp32
 
 template <int OUT>
-__device__ inline void block_epilogue(const GemmArgs& g, const float (&acc)[2][2][16], int64_t m_tile, int64_t n_tile,
+__device__ __attribute__((always_inline)) inline void block_epilogue(const GemmArgs& g, const float (&acc)[2][2][16], int64_t m_tile, int64_t n_tile,
                                       uint8_t* ep) {
   constexpr int EB = OutBytes<OUT>::v;
   constexpr int kRowBytes = kBlkTile * EB + 16;
@@ -1095,6 +1238,7 @@ int launch_big(GemmArgs g, hipStream_t st, const char* op) {
   const int64_t tiles = (int64_t)g.tiles_m * cdiv(g.N, kBigTile);
   if (tiles > 0x7FFFFFFF) return fail(AYK_EINVAL, "%s: problem too large", op);
   if constexpr (MODE == MODE_MX) hipLaunchKernelGGL((fp8_gemm_mx128_kernel<MODE_MX>), dim3((unsigned)tiles), dim3(kThreads), 0, st, g);
+  else if (g.K % (2 * kBigK) == 0) hipLaunchKernelGGL((fp8_gemm_pair_kernel<MODE>), dim3((unsigned)tiles), dim3(kThreads), 0, st, g);
   else hipLaunchKernelGGL((fp8_gemm_big_kernel<MODE>), dim3((unsigned)tiles), dim3(kThreads), 0, st, g);
   return check_launch(op);
 }

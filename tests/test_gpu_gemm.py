@@ -88,7 +88,9 @@ def test_blockwise_gemv(gpu, n, k):
 MNK = [(8, 3072, 1024), (17, 300, 256), (64, 256, 384), (200, 1000, 1024), (256, 512, 2048), (129, 130, 528),
        (300, 520, 1024), (513, 772, 2048), (1024, 1024, 3584),
        # 256x256 kernel with 1, 5 and 19 K stages of 64: steps padded to a multiple of four
-       (256, 256, 64), (400, 300, 320), (260, 1028, 1216)]  # from (300, 520, 1024) on: the 256x256 kernel
+       (256, 256, 64), (400, 300, 320), (260, 1028, 1216),
+       # its 128-byte-row variant (K % 128 == 0) with 1 and 3 pairs of stages: pairs padded to even
+       (256, 260, 128), (512, 512, 384)]  # from (300, 520, 1024) on: the 256x256 kernels
 
 
 @pytest.mark.parametrize("m,n,k", MNK)
@@ -132,11 +134,11 @@ def test_fp8_scaled_mm_big_tile_strided_out(gpu, out_dtype):
     assert torch.all(buf[:, n:].float() == 7.0), "wrote past the output columns"
 
 
-@pytest.mark.parametrize("k", [192, 320, 1088])
+@pytest.mark.parametrize("k", [192, 320, 1088, 640])
 @pytest.mark.parametrize("rowwise,with_bias", [(True, False), (False, True), (True, True)])
 def test_fp8_scaled_mm_many_tiles(gpu, k, rowwise, with_bias):
     """More 256x256 tiles (9 x 32 = 288) than compute units, so compute units run several
-    tiles; K of 3, 5 and 17 stages (padded steps)."""
+    tiles; K of 3, 5 and 17 stages (padded steps) and of 5 pairs of stages."""
     from ayaka.kernel.hip import fp8_scaled_mm
 
     m, n = 2304, 8192
