@@ -678,7 +678,7 @@ __global__ __launch_bounds__(kThreads, 1) void fp8_gemm_big_kernel(GemmArgs g) {
 // narrow kernel's.
 template <int MODE>
 __global__ __launch_bounds__(kThreads, 1) void fp8_gemm_pair_kernel(GemmArgs g) {
-  static_assert(MODE == MODE_SCALED, "per-row / per-tensor scales only");
+  static_assert(MODE == MODE_SCALED || MODE == MODE_MX, "per-row / per-tensor scales or MX codes");
   constexpr int FN = 4, FM = 4;        // 32x32 MFMA tiles per wavefront (n, m)
   constexpr int kPairK = 2 * kBigK;    // 128 K bytes per pair
   constexpr int kPairBytes = 2 * kBigTile * kPairK;  // 64 KB
@@ -688,6 +688,10 @@ __global__ __launch_bounds__(kThreads, 1) void fp8_gemm_pair_kernel(GemmArgs g) 
   // never alias the in-flight direct loads into the other).
   __shared__ __attribute__((aligned(1024))) uint8_t P0[kPairBytes];
   __shared__ __attribute__((aligned(1024))) uint8_t P1[kPairBytes];
+  // MXFP8: the UE8M0 codes of the tile's 512 rows for a chunk of four pairs (16 bytes a
+  // row), in two 8 KB halves (chunk c in half c mod 2).
+  constexpr int kChunkBytes = 2 * kBigTile * 16;
+  __shared__ __attribute__((aligned(1024))) uint8_t C[MODE == MODE_MX ? 2 * kChunkBytes : 16];
 
   const int tid = threadIdx.x, lane = tid & 63;
   const int wave_u = __builtin_amdgcn_readfirstlane(tid >> 6);  // keep descriptors in SGPRs
@@ -700,7 +704,10 @@ __global__ __launch_bounds__(kThreads, 1) void fp8_gemm_pair_kernel(GemmArgs g) 
   const int npairs = (np + 1) & ~1;      // padded to the unroll (a padded pair computes zeros)
   // K stagger in pairs: (tm mod 8) + (tn mod 2) (mod np), the narrow kernel's stagger
   // of 2 (tm mod 8) + (tn mod 2) steps rounded to whole pairs.
-  const int stag = __builtin_amdgcn_readfirstlane((int)((unsigned)((tm & 7) + (tn & 1)) % (unsigned)np));
+  // MXFP8 (np % 4 == 0): whole chunks of four pairs, 4 ((tm mod 8) + (tn mod 2)) (mod np).
+  const int stag = __builtin_amdgcn_readfirstlane(
+      MODE == MODE_MX ? 4 * (int)((unsigned)((tm & 7) + (tn & 1)) % (unsigned)(np / 4))
+                      : (int)((unsigned)((tm & 7) + (tn & 1)) % (unsigned)np));
 
   // Direct loads: wavefronts 0-1 fetch the 256 weight rows, 2-3 the 256 activation rows
   // (128 each). Load jj (0-15) of wavefront w reads operand rows 128 (w & 1) + 8 jj +
@@ -763,21 +770,75 @@ __global__ __launch_bounds__(kThreads, 1) void fp8_gemm_pair_kernel(GemmArgs g) 
     for (int j = 0; j < FM; ++j)
 #pragma unroll
       for (int r = 0; r < 16; ++r) acc[i][j][r] = 0.0f;
+  // MXFP8: the codes of a fragment row for one pair are one dword (four 32-K blocks)
+  // of its chunk row in C. Those of pair p + 1 are read during pair p into the second
+  // set and moved to the first at the pair's end. Step half t of the pair uses block
+  // 2 t + h in lane half h: the dword shifted right by 8 (2 t + h) (the MFMA reads the
+  // low byte of its scale operands).
+  uint32_t wc[2][FN], ac[2][FM];
+  // Code chunk loads mirror the operand loads: wavefronts 0-1 the weight rows, 2-3 the
+  // activation rows, 128 each, as two 16-byte direct loads of 64 rows; chunk row r
+  // (0-255 weight, 256-511 activation) at byte 16 r of its half. Rows past M / N read
+  // zero codes (never stored).
+  const int64_t ld_c = w_wave ? g.ld_sb : g.ld_sa;
+  const OperandWindow cwin = MODE == MODE_MX ? operand_window((w_wave ? n_base : m_base) + (wave_u & 1) * 128, w_wave ? g.N : g.M, ld_c)
+                                             : OperandWindow{0, 0};
+  const __amdgpu_buffer_rsrc_t code_rsrc =
+      uniform_rsrc(reinterpret_cast<const uint8_t*>(w_wave ? g.sb : g.sa) + cwin.base_offset, cwin.records);
+  const int ldc_u = __builtin_amdgcn_readfirstlane((int)ld_c);
+  auto issue_codes = [&](int c) {
+    if constexpr (MODE == MODE_MX) {
+      int kc = c + stag / 4;
+      kc = __builtin_amdgcn_readfirstlane(kc >= np / 4 ? kc - np / 4 : kc);
+#pragma unroll
+      for (int q = 0; q < 2; ++q)
+        __builtin_amdgcn_raw_ptr_buffer_load_lds(
+            code_rsrc, (__attribute__((address_space(3))) void*)(C + ((c & 1) * kChunkBytes + (wave_u * 128 + q * 64) * 16)), 16,
+            lane * ldc_u, __builtin_amdgcn_readfirstlane(q * 64 * ldc_u + kc * 16), 0, 0);
+    }
+  };
+  auto read_codes = [&](int p, int set) {
+    if constexpr (MODE == MODE_MX) {
+      const int base = ((p >> 2) & 1) * kChunkBytes + (p & 3) * 4;
+#pragma unroll
+      for (int i = 0; i < FN; ++i) wc[set][i] = *reinterpret_cast<const uint32_t*>(C + (base + (wn * 128 + i * 32 + frow) * 16));
+#pragma unroll
+      for (int j = 0; j < FM; ++j) ac[set][j] = *reinterpret_cast<const uint32_t*>(C + (base + (256 + wm * 128 + j * 32 + frow) * 16));
+    }
+  };
+  auto next_codes = [&] {
+    if constexpr (MODE == MODE_MX) {
+#pragma unroll
+      for (int i = 0; i < FN; ++i) wc[0][i] = wc[1][i];
+#pragma unroll
+      for (int j = 0; j < FM; ++j) ac[0][j] = ac[1][j];
+    }
+  };
   auto mfmas = [&](int set, int j0, int j1) {
 #pragma unroll
     for (int j = j0; j < j1; ++j)
 #pragma unroll
-      for (int i = 0; i < FN; ++i) acc[i][j] = mfma(wf[set][i], af[set][j], acc[i][j], kScaleOne, kScaleOne);
+      for (int i = 0; i < FN; ++i) {
+        if constexpr (MODE == MODE_MX) {
+          const int sh = 8 * (2 * set + h);  // fragment set `set` holds step half t = set
+          acc[i][j] = mfma(wf[set][i], af[set][j], acc[i][j], (int)(wc[0][i] >> sh), (int)(ac[0][j] >> sh));
+        } else {
+          acc[i][j] = mfma(wf[set][i], af[set][j], acc[i][j], kScaleOne, kScaleOne);
+        }
+      }
   };
   constexpr int kHead = 1;  // m-fragments multiplied before the step's barrier
 
   const BigScales scales = load_big_scales<MODE>(g, m_base, n_base);
-  // Prologue: pairs 0 and 1 in flight, pair 0 visible, step (0, 0)'s fragments in set 0.
+  // Prologue: pairs 0 and 1 in flight (pair 0's codes between them), pair 0 visible,
+  // step (0, 0)'s fragments in set 0.
   issue(0, P0);
+  issue_codes(0);
   issue(1, P1);
   wait_vmcnt<kDma>();
   lds_barrier();
   read_frags(0, P0, 0);
+  read_codes(0, 0);
 
   // Pair p in `cur`, pair p + 1 in flight into `nxt`. Its first step: the barrier (the
   // whole pair has landed) certifies every wavefront has its step fragments, then the
@@ -797,9 +858,14 @@ __global__ __launch_bounds__(kThreads, 1) void fp8_gemm_pair_kernel(GemmArgs g) 
     wait_vmcnt<0>();
     lds_barrier();
     __builtin_amdgcn_sched_barrier(0);
+    // The next pair's codes are read before any new code load is in flight (the
+    // compiler cannot tell the two halves of C apart and would wait for it).
+    read_codes(p + 1 < npairs ? p + 1 : npairs - 1, 1);
     issue(p + 2 < npairs ? p + 2 : npairs - 1, cur);
+    if (MODE == MODE_MX && ((p + 2) & 3) == 0 && p + 2 < npairs) issue_codes((p + 2) >> 2);
     read_frags(0, nxt, 0);
     mfmas(1, kHead, FM);
+    next_codes();
   };
   for (int p = 0; p < npairs; p += 2) {
     pair(p, P0, P1);
@@ -1237,9 +1303,16 @@ int launch_big(GemmArgs g, hipStream_t st, const char* op) {
   g.tiles_m = (int)cdiv(g.M, kBigTile);
   const int64_t tiles = (int64_t)g.tiles_m * cdiv(g.N, kBigTile);
   if (tiles > 0x7FFFFFFF) return fail(AYK_EINVAL, "%s: problem too large", op);
-  if constexpr (MODE == MODE_MX) hipLaunchKernelGGL((fp8_gemm_mx128_kernel<MODE_MX>), dim3((unsigned)tiles), dim3(kThreads), 0, st, g);
-  else if (g.K % (2 * kBigK) == 0) hipLaunchKernelGGL((fp8_gemm_pair_kernel<MODE>), dim3((unsigned)tiles), dim3(kThreads), 0, st, g);
-  else hipLaunchKernelGGL((fp8_gemm_big_kernel<MODE>), dim3((unsigned)tiles), dim3(kThreads), 0, st, g);
+  if constexpr (MODE == MODE_MX) {
+    if (g.K % 512 == 0 && g.ld_sa % 16 == 0 && g.ld_sb % 16 == 0 && aligned16(g.sa) && aligned16(g.sb))
+      hipLaunchKernelGGL((fp8_gemm_pair_kernel<MODE>), dim3((unsigned)tiles), dim3(kThreads), 0, st, g);
+    else
+      hipLaunchKernelGGL((fp8_gemm_mx128_kernel<MODE>), dim3((unsigned)tiles), dim3(kThreads), 0, st, g);
+  } else if (g.K % (2 * kBigK) == 0) {
+    hipLaunchKernelGGL((fp8_gemm_pair_kernel<MODE>), dim3((unsigned)tiles), dim3(kThreads), 0, st, g);
+  } else {
+    hipLaunchKernelGGL((fp8_gemm_big_kernel<MODE>), dim3((unsigned)tiles), dim3(kThreads), 0, st, g);
+  }
   return check_launch(op);
 }
 

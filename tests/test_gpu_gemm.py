@@ -190,7 +190,11 @@ def test_fp8_blockwise_mm(gpu, m, n, k, sdt, col_major):
 
 
 @pytest.mark.parametrize("m,n,k", [(1, 512, 1024), (1, 1000, 8192), (64, 256, 512), (100, 300, 1024), (512, 512, 2048), (33, 96, 96),
-                                   (300, 520, 1024), (777, 1028, 2048)])
+                                   (300, 520, 1024), (777, 1028, 2048),
+                                   # 256x256 kernels: codes staged in chunks of four 128-K pairs
+                                   # (K % 512 == 0; three chunks, M / N tails, 288 tiles) and the
+                                   # 128-K-stage kernel for other K % 128 == 0
+                                   (520, 1040, 1536), (2304, 8192, 1024), (512, 512, 640)])
 def test_mxfp8_scaled_mm(gpu, m, n, k):
     from ayaka.kernel.hip import mxfp8_scaled_mm
 
