@@ -704,9 +704,10 @@ __global__ __launch_bounds__(kThreads, 1) void fp8_gemm_pair_kernel(GemmArgs g) 
   const int npairs = (np + 1) & ~1;      // padded to the unroll (a padded pair computes zeros)
   // K stagger in pairs: (tm mod 8) + (tn mod 2) (mod np), the narrow kernel's stagger
   // of 2 (tm mod 8) + (tn mod 2) steps rounded to whole pairs.
-  // MXFP8 (np % 4 == 0): whole chunks of four pairs, 4 ((tm mod 8) + (tn mod 2)) (mod np).
+  // MXFP8 (np % 4 == 0) staggers in whole chunks of four pairs, which is coarse: only
+  // 4 ((tm mod 2) + (tn mod 2)) (mod np), the best of none, this and 4 (tm mod 8 ...).
   const int stag = __builtin_amdgcn_readfirstlane(
-      MODE == MODE_MX ? 4 * (int)((unsigned)((tm & 7) + (tn & 1)) % (unsigned)(np / 4))
+      MODE == MODE_MX ? 4 * (int)((unsigned)((tm & 1) + (tn & 1)) % (unsigned)(np / 4))
                       : (int)((unsigned)((tm & 7) + (tn & 1)) % (unsigned)np));
 
   // Direct loads: wavefronts 0-1 fetch the 256 weight rows, 2-3 the 256 activation rows
