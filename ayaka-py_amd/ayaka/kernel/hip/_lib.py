@@ -57,6 +57,7 @@ SIGNATURES: dict[str, list[Any]] = {
     "ayk_static_quant_fp8": [_p, _i, _l, _p, _i, _p, _p],
     "ayk_fp8_scaled_mm": [_p, _l, _p, _l, _l, _l, _l, _p, _i, _i, _p, _i, _i, _p, _i, _p, _i, _l, _p],
     "ayk_fp8_blockwise_mm": [_p, _l, _p, _l, _l, _l, _l, _p, _i, _i, _p, _i, _p, _i, _p, _i, _l, _p],
+    "ayk_int8_scaled_mm": [_p, _l, _p, _l, _l, _l, _l, _p, _p, _p, _i, _p, _i, _l, _p],
     "ayk_mxfp8_scaled_mm": [_p, _l, _p, _l, _p, _l, _p, _l, _l, _l, _l, _p, _i, _p, _i, _l, _p],
     "ayk_fp8_weight_only_gemv": [_p, _i, _p, _l, _l, _l, _p, _i, _l, _l, _l, _p, _p, _z, _p],
     "ayk_fp8_weight_only_gemv_workspace_bytes": [_l, _l],

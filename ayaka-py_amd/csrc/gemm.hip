@@ -42,7 +42,9 @@ constexpr int BK = 128;
 constexpr int kLdsRow = BK + 16;  // padded LDS row stride in bytes
 constexpr int kScaleOne = 127;    // UE8M0 code of 1.0
 
-enum Mode { MODE_SCALED = 0, MODE_BLOCK = 1, MODE_MX = 2 };
+enum Mode { MODE_SCALED = 0, MODE_BLOCK = 1, MODE_MX = 2, MODE_INT8 = 3 };
+// Modes whose epilogue applies per-row / per-tensor output scales.
+constexpr bool row_scaled(int mode) { return mode == MODE_SCALED || mode == MODE_INT8; }
 
 struct GemmArgs {
   const uint8_t* a;  // [M, K] e4m3
@@ -68,6 +70,32 @@ struct GemmArgs {
 
 __device__ inline v16f mfma(const v8i& wa, const v8i& ab, const v16f& c, int sw, int sa) {
   return __builtin_amdgcn_mfma_scale_f32_32x32x64_f8f6f4(wa, ab, c, 0, 0, 0, sw, 0, sa);
+}
+typedef int v16i __attribute__((ext_vector_type(16)));
+typedef int v4i __attribute__((ext_vector_type(4)));
+// One 64-K step of a 32x32 tile in the mode's arithmetic. INT8: two
+// v_mfma_i32_32x32x32_i8 on the fragment's halves (its K order only has to match
+// between the operands for a plain dot product); the int32 sums travel in the fp32
+// accumulator registers bit for bit and are converted in the epilogue (acc_value).
+template <int MODE>
+__device__ inline v16f mma(const v8i& wa, const v8i& ab, const v16f& c, int sw, int sa) {
+  if constexpr (MODE == MODE_INT8) {
+    v16i acc = __builtin_bit_cast(v16i, c);
+    acc = __builtin_amdgcn_mfma_i32_32x32x32_i8(__builtin_shufflevector(wa, wa, 0, 1, 2, 3), __builtin_shufflevector(ab, ab, 0, 1, 2, 3),
+                                                acc, 0, 0, 0);
+    acc = __builtin_amdgcn_mfma_i32_32x32x32_i8(__builtin_shufflevector(wa, wa, 4, 5, 6, 7), __builtin_shufflevector(ab, ab, 4, 5, 6, 7),
+                                                acc, 0, 0, 0);
+    return __builtin_bit_cast(v16f, acc);
+  } else {
+    return mfma(wa, ab, c, sw, sa);
+  }
+}
+// Accumulator register value as a float (INT8: the exact int32 sum, converted with
+// round to nearest even as torch's int32 -> float32).
+template <int MODE>
+__device__ inline float acc_value(float r) {
+  if constexpr (MODE == MODE_INT8) return (float)__builtin_bit_cast(int, r);
+  else return r;
 }
 
 // 32 operand bytes of one lane: K [16h, 16h+16) and [32+16h, 48+16h) of the step.
@@ -227,7 +255,7 @@ __global__ __launch_bounds__(kThreads) void fp8_gemm_kernel(GemmArgs g) {
 #pragma unroll
         for (int j = 0; j < FM; ++j) {
           if constexpr (MODE == MODE_BLOCK) part[i][j] = mfma(wf[i], af[j], part[i][j], wsc[i], asc[j]);
-          else acc[i][j] = mfma(wf[i], af[j], acc[i][j], wsc[i], asc[j]);
+          else acc[i][j] = mma<MODE>(wf[i], af[j], acc[i][j], wsc[i], asc[j]);
         }
     }
 
@@ -258,7 +286,7 @@ __global__ __launch_bounds__(kThreads) void fp8_gemm_kernel(GemmArgs g) {
   for (int j = 0; j < FM; ++j) {
     const int64_t m = m_base + wm * TM + j * 32 + frag_row;
     float sa = 1.0f;
-    if constexpr (MODE == MODE_SCALED) {
+    if constexpr (row_scaled(MODE)) {
       const int64_t mi = m < g.M ? m : g.M - 1;
       sa = load_f32(g.sa, g.sa_dtype, g.sa_vec ? mi : 0);
     }
@@ -272,8 +300,8 @@ __global__ __launch_bounds__(kThreads) void fp8_gemm_kernel(GemmArgs g) {
         for (int q = 0; q < 4; ++q) {
           const int64_t n = n0 + q;
           const int64_t ni = n < g.N ? n : g.N - 1;
-          float y = acc[i][j][grp * 4 + q];
-          if constexpr (MODE == MODE_SCALED) {
+          float y = acc_value<MODE>(acc[i][j][grp * 4 + q]);
+          if constexpr (row_scaled(MODE)) {
             y = y * sa;
             y = y * load_f32(g.sb, g.sb_dtype, g.sb_vec ? ni : 0);
           }
@@ -402,7 +430,7 @@ __device__ __attribute__((always_inline)) inline BigScales load_big_scales(const
     for (int grp = 0; grp < 4; ++grp)
 #pragma unroll
       for (int q = 0; q < 4; ++q) sc.sb[i][grp][q] = 1.0f;
-  if constexpr (MODE == MODE_SCALED) {
+  if constexpr (row_scaled(MODE)) {
     const float* sa_p = reinterpret_cast<const float*>(g.sa);
     const float* sb_p = reinterpret_cast<const float*>(g.sb);
 #pragma unroll
@@ -468,8 +496,8 @@ __device__ __attribute__((always_inline)) inline void big_epilogue_impl(const Ge
             float v[4];
 #pragma unroll
             for (int qq = 0; qq < 4; ++qq) {
-              float y = acc[i][j][grp * 4 + qq];
-              if constexpr (MODE == MODE_SCALED) y = (y * sc.sa[j]) * sc.sb[i][grp][qq];
+              float y = acc_value<MODE>(acc[i][j][grp * 4 + qq]);
+              if constexpr (row_scaled(MODE)) y = (y * sc.sa[j]) * sc.sb[i][grp][qq];
               v[qq] = BIAS ? y + bias[qq] : y;
             }
             if constexpr (OUT == AYK_F32) {
@@ -532,7 +560,7 @@ __device__ __attribute__((always_inline)) inline void big_epilogue(const GemmArg
 
 template <int MODE>
 __global__ __launch_bounds__(kThreads, 1) void fp8_gemm_big_kernel(GemmArgs g) {
-  static_assert(MODE == MODE_SCALED, "per-row / per-tensor scales only");
+  static_assert(row_scaled(MODE), "per-row / per-tensor scales only");
   constexpr int FN = 4, FM = 4;                        // 32x32 MFMA tiles per wavefront (n, m)
   constexpr int kDma = kBigStage / 1024 / 4;           // direct loads per wavefront per stage (8)
   constexpr int kOps = kDma;                           // vector-memory ops per wavefront per stage
@@ -624,7 +652,7 @@ __global__ __launch_bounds__(kThreads, 1) void fp8_gemm_big_kernel(GemmArgs g) {
 #pragma unroll
     for (int j = j0; j < j1; ++j)
 #pragma unroll
-      for (int i = 0; i < FN; ++i) acc[i][j] = mfma(wf[set][i], af[set][j], acc[i][j], kScaleOne, kScaleOne);
+      for (int i = 0; i < FN; ++i) acc[i][j] = mma<MODE>(wf[set][i], af[set][j], acc[i][j], kScaleOne, kScaleOne);
   };
 
   constexpr int kHead = 1;  // m-fragments multiplied before the step's barrier
@@ -678,7 +706,7 @@ __global__ __launch_bounds__(kThreads, 1) void fp8_gemm_big_kernel(GemmArgs g) {
 // narrow kernel's.
 template <int MODE>
 __global__ __launch_bounds__(kThreads, 1) void fp8_gemm_pair_kernel(GemmArgs g) {
-  static_assert(MODE == MODE_SCALED || MODE == MODE_MX, "per-row / per-tensor scales or MX codes");
+  static_assert(row_scaled(MODE) || MODE == MODE_MX, "per-row / per-tensor scales or MX codes");
   constexpr int FN = 4, FM = 4;        // 32x32 MFMA tiles per wavefront (n, m)
   constexpr int kPairK = 2 * kBigK;    // 128 K bytes per pair
   constexpr int kPairBytes = 2 * kBigTile * kPairK;  // 64 KB
@@ -824,7 +852,7 @@ __global__ __launch_bounds__(kThreads, 1) void fp8_gemm_pair_kernel(GemmArgs g) 
           const int sh = 8 * (2 * set + h);  // fragment set `set` holds step half t = set
           acc[i][j] = mfma(wf[set][i], af[set][j], acc[i][j], (int)(wc[0][i] >> sh), (int)(ac[0][j] >> sh));
         } else {
-          acc[i][j] = mfma(wf[set][i], af[set][j], acc[i][j], kScaleOne, kScaleOne);
+          acc[i][j] = mma<MODE>(wf[set][i], af[set][j], acc[i][j], kScaleOne, kScaleOne);
         }
       }
   };
@@ -1402,6 +1430,27 @@ int ayk_fp8_scaled_mm(const void* a, int64_t lda, const void* b, int64_t ldb, in
   g.bias = bias; g.bias_dtype = bias_dtype;
   g.out = out; g.out_dtype = out_dtype; g.ldo = ldo;
   return launch_gemm<MODE_SCALED>(g, static_cast<hipStream_t>(stream), op);
+}
+
+int ayk_int8_scaled_mm(const void* a, int64_t lda, const void* b, int64_t ldb, int64_t M, int64_t N,
+                       int64_t K, const float* scale_a, const float* scale_b, const void* bias,
+                       int bias_dtype, void* out, int out_dtype, int64_t ldo, ayk_stream_t stream) {
+  const char* op = "int8_scaled_mm";
+  if (int rc = check_common(op, a, lda, b, ldb, M, N, K, bias, bias_dtype, out_dtype, ldo)) return rc;
+  if ((M > 0 && scale_a == nullptr) || (N > 0 && scale_b == nullptr)) return fail(AYK_EINVAL, "%s: scale_a / scale_b are required", op);
+  if (M == 0 || N == 0) return AYK_OK;
+  if (int rc = check_device()) return rc;
+  GemmArgs g{};
+  g.a = static_cast<const uint8_t*>(a);
+  g.lda = lda;
+  g.w = static_cast<const uint8_t*>(b);
+  g.ldw = ldb;
+  g.M = M; g.N = N; g.K = K;
+  g.sa = scale_a; g.sa_dtype = AYK_F32; g.sa_vec = 1;
+  g.sb = scale_b; g.sb_dtype = AYK_F32; g.sb_vec = 1;
+  g.bias = bias; g.bias_dtype = bias_dtype;
+  g.out = out; g.out_dtype = out_dtype; g.ldo = ldo;
+  return launch_gemm<MODE_INT8>(g, static_cast<hipStream_t>(stream), op);
 }
 
 int ayk_fp8_blockwise_mm(const void* a, int64_t lda, const void* b, int64_t ldb, int64_t M,

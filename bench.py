@@ -169,6 +169,17 @@ def _bench_gemm(device, reps=20, warmup=5):
     out = torch.empty(m, n, dtype=torch.bfloat16, device=device)
     run("mxfp8_llama70b_gate_up", n, k, lambda: mxfp8_scaled_mm(a, ca, w, cw, out=out))
     del a, w, out
+    # INT8 rowwise (the §8(f) INT8 scaled GEMM), on the Qwen2 gate_up shape
+    from ayaka.kernel.hip import int8_scaled_mm
+
+    n, k = 37888, 3584
+    a = torch.randint(-128, 128, (m, k), generator=g, device=device, dtype=torch.int8)
+    w = torch.randint(-128, 128, (n, k), generator=g, device=device, dtype=torch.int8)
+    sa = torch.rand(m, generator=g, device=device) * 1e-4
+    sb = torch.rand(n, generator=g, device=device) * 1e-4
+    out = torch.empty(m, n, dtype=torch.bfloat16, device=device)
+    run("int8_rowwise_qwen2_gate_up", n, k, lambda: int8_scaled_mm(a, w.t(), sa, sb, out=out))
+    del a, w, out
     torch.cuda.empty_cache()
     return results
 

@@ -100,6 +100,16 @@ int ayk_fp8_scaled_mm(const void* a, int64_t lda, const void* b, int64_t ldb,
                       const void* bias, int bias_dtype,
                       void* out, int out_dtype, int64_t ldo, ayk_stream_t stream);
 
+/* Replaces ayaka::int8_scaled_mm (gemm/int8_gemm.py:134; oracle reference/gemm.py:192-211).
+ * out = float(a @ b^T, int32 accumulation) * scale_a[m] * scale_b[n] + bias, with a the
+ * [M, K] int8 activation and b the [N, K] int8 weight; scale_a [M] and scale_b [N] fp32.
+ * Requires K % 16 == 0, lda/ldb multiples of 16 and 16-byte aligned a/b. */
+int ayk_int8_scaled_mm(const void* a, int64_t lda, const void* b, int64_t ldb,
+                       int64_t M, int64_t N, int64_t K,
+                       const float* scale_a, const float* scale_b,
+                       const void* bias, int bias_dtype,
+                       void* out, int out_dtype, int64_t ldo, ayk_stream_t stream);
+
 /* Replaces ayaka::fp8_blockwise_mm (gemm/fp8_gemm.py:370; oracle reference/gemm.py:40-70).
  * out = sum_kb (a[:, kb] @ b[:, kb]^T) * scale_a[m, kb] * scale_b[n / 128, kb] + bias.
  * scale_a: [M, ceil(K/128)] (or [ceil(K/128), M] when sa_col_major), scale_b:

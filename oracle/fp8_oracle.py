@@ -97,6 +97,33 @@ def fp8_scaled_mm(a, b_nk, scale_a, scale_b, bias=None) -> torch.Tensor:
     return y
 
 
+def int8_matmul_exact(a, b_nk) -> torch.Tensor:
+    """``a @ b_nk^T`` of int8 operands as the exact integer sum (int64).
+
+    The reference's int8 kernel accumulates in int32 (gemm/int8_gemm.py:70-81,
+    ``tl.dot(..., out_dtype=tl.int32)``), which is exact for any K below 2^17 at int8
+    magnitudes. fp64 represents every such sum exactly, so a fp64 product rounded back
+    to int64 is that sum.
+    """
+    return (a.double() @ b_nk.double().t()).round().to(torch.int64)
+
+
+def int8_scaled_mm(a, b_nk, scale_a, scale_b, bias=None) -> torch.Tensor:
+    """``float(a @ b) * sa * sb + bias`` in fp32 (reference gemm.py:192-211).
+
+    The accumulator is the exact int32 sum (as the reference kernel, int8_gemm.py:81;
+    the reference's own fp32 restatement rounds sums above 2^24, the kernel does not),
+    converted to fp32 once; then the reference's operation order: times ``scale_a``
+    per row, times ``scale_b`` per column, plus ``bias``.
+    """
+    y = int8_matmul_exact(a, b_nk).to(torch.float32)
+    y = y * scale_a.float().reshape(-1, 1)
+    y = y * scale_b.float().reshape(1, -1)
+    if bias is not None:
+        y = y + bias.float()
+    return y
+
+
 def fp8_blockwise_mm(a, b, scale_a, scale_b, bias=None, a_scale_col_major: bool = False) -> torch.Tensor:
     """Per-128-K partials rescaled then summed, fp32 (reference gemm.py:40-70)."""
     m, k = a.shape

@@ -298,3 +298,72 @@ def test_weight_only_gemm_decode_shapes(gpu, m, n, k, case, xdt):
     ref = ora.fp8_weight_only_gemm(x, w, scale, -(-k // bx), by, bx, sdt)
     assert y.dtype == xdt and y.shape == (m, n)
     assert_linear_close(y, ref, "weight_only_gemm")
+
+
+# ------------------------------------------------------------------ INT8 GEMM
+def _i8(shape, seed):
+    return torch.randint(-128, 128, shape, generator=_gen(seed), dtype=torch.int8)
+
+
+INT8_MNK = [(8, 3072, 1024), (17, 300, 256), (200, 1000, 1040),  # general kernel (K % 64 != 0 included)
+            (300, 520, 1024), (400, 300, 320), (260, 1028, 1216), (2304, 8192, 640)]  # 256x256 kernels
+
+
+@pytest.mark.parametrize("m,n,k", INT8_MNK)
+@pytest.mark.parametrize("with_bias", [False, True])
+def test_int8_scaled_mm(gpu, m, n, k, with_bias):
+    from ayaka.kernel.hip import int8_scaled_mm
+
+    _say(f"int8_scaled_mm m={m} n={n} k={k} bias={with_bias}")
+    a, w = _i8((m, k), m), _i8((n, k), n)
+    sa = torch.rand(m, generator=_gen(1)) * 1e-3 + 1e-4
+    sb = torch.rand(n, generator=_gen(2)) * 1e-3 + 1e-4
+    bias = torch.randn(n, generator=_gen(3)).to(torch.bfloat16) if with_bias else None
+    ref = ora.int8_scaled_mm(a, w, sa, sb, bias)
+    args = (a.to(gpu), w.to(gpu).t(), sa.to(gpu), sb.to(gpu), None if bias is None else bias.to(gpu))
+    y = int8_scaled_mm(*args)
+    assert y.dtype == torch.bfloat16  # the reference's default out_dtype
+    assert_linear_close(y, ref, "int8_scaled_mm bf16")
+    out = torch.full((m, n), float("nan"), dtype=torch.float32, device=gpu)
+    r = int8_scaled_mm(*args, out=out)
+    assert r is out
+    # fp32 output: the same fp32 epilogue as the oracle up to the compiler's fused
+    # multiply-add of the bias.
+    torch.testing.assert_close(out.cpu(), ref, rtol=2e-6, atol=1e-6 * ref.abs().max().item())
+
+
+@pytest.mark.parametrize("m,n,k", [(64, 256, 512), (512, 512, 1024), (520, 1040, 2048)])
+def test_int8_scaled_mm_integer_sum_is_exact(gpu, m, n, k):
+    """Unit scales, fp32 output: every int32 sum below 2^24 comes out exactly."""
+    from ayaka.kernel.hip import int8_scaled_mm
+
+    _say(f"int8_scaled_mm exact m={m} n={n} k={k}")
+    a, w = _i8((m, k), 5), _i8((n, k), 6)
+    exact = ora.int8_matmul_exact(a, w)
+    assert exact.abs().max().item() < 2**24
+    out = int8_scaled_mm(a.to(gpu), w.to(gpu).t(), torch.ones(m, device=gpu), torch.ones(n, device=gpu), out_dtype=torch.float32)
+    assert torch.equal(out.cpu().to(torch.int64), exact)
+
+
+def test_int8_scaled_mm_row_major_b_and_contract(gpu):
+    from ayaka.kernel.hip import int8_scaled_mm
+
+    _say("int8_scaled_mm row-major b and errors")
+    m, n, k = 96, 200, 256
+    a, w = _i8((m, k), 8), _i8((n, k), 9)
+    sa, sb = (torch.rand(m, generator=_gen(1)) + 0.5) * 1e-3, (torch.rand(n, generator=_gen(2)) + 0.5) * 1e-3
+    ref = ora.int8_scaled_mm(a, w, sa, sb)  # |ref| well inside the fp16 range
+    b_kn = w.t().contiguous().to(gpu)  # [K, N] row-major
+    y = int8_scaled_mm(a.to(gpu), b_kn, sa.to(gpu), sb.to(gpu), out_dtype=torch.float16)
+    assert y.dtype == torch.float16
+    assert_linear_close(y, ref, "int8 row-major b")
+    with pytest.raises(TypeError):
+        int8_scaled_mm(a.to(gpu).to(torch.float8_e4m3fn), b_kn, sa.to(gpu), sb.to(gpu))
+    with pytest.raises(TypeError):
+        int8_scaled_mm(a.to(gpu), b_kn, sa.to(gpu).half(), sb.to(gpu))
+    with pytest.raises(ValueError):
+        int8_scaled_mm(a.to(gpu), b_kn, torch.tensor(1.0, device=gpu), sb.to(gpu))  # scalar scale
+    with pytest.raises(ValueError):
+        int8_scaled_mm(a[:, :250].contiguous().to(gpu), b_kn[:250], sa.to(gpu), sb.to(gpu))  # K % 16
+    with pytest.raises(ValueError):
+        int8_scaled_mm(a.to(gpu), b_kn, sa.to(gpu), sb.to(gpu), out_dtype=torch.int32)

@@ -204,6 +204,40 @@ def test_scaled_mm_brute_force_and_invariants():
     assert torch.equal(ora.fp8_scaled_mm(a, zero, sa, sb, bias), bias.expand(3, 4))
 
 
+def test_int8_matmul_exact_brute_force_and_past_fp32():
+    g = torch.Generator().manual_seed(7)
+    a = torch.randint(-128, 128, (3, 37), generator=g, dtype=torch.int8)
+    w = torch.randint(-128, 128, (4, 37), generator=g, dtype=torch.int8)
+    y = ora.int8_matmul_exact(a, w)
+    for i in range(3):
+        for j in range(4):
+            assert y[i, j].item() == sum(int(a[i, k]) * int(w[j, k]) for k in range(37))
+    # Sums above 2^24 stay exact (an fp32 accumulation would round them): 2048 products
+    # of -128 * -127 plus one of 1 * 1 -> 33292289, odd and above 2^25.
+    a2 = torch.full((1, 2049), -128, dtype=torch.int8)
+    w2 = torch.full((1, 2049), -127, dtype=torch.int8)
+    a2[0, -1], w2[0, -1] = 1, 1
+    assert ora.int8_matmul_exact(a2, w2).item() == 2048 * 128 * 127 + 1
+    assert (a2.float() @ w2.float().t()).item() != 2048 * 128 * 127 + 1  # what fp32 would give
+
+
+def test_int8_scaled_mm_known_answers_and_invariants():
+    a = torch.tensor([[1, -2, 3, 4], [127, -128, 0, 5]], dtype=torch.int8)
+    w = torch.tensor([[1, 1, 1, 1], [2, 0, -1, 3], [-128, 127, 64, -64]], dtype=torch.int8)
+    sa, sb = torch.tensor([0.5, 0.25]), torch.tensor([2.0, 1.0, 0.125])
+    bias = torch.tensor([1.0, -1.0, 0.5])
+    y = ora.int8_scaled_mm(a, w, sa, sb, bias)
+    acc = [[6, 11, -128 - 254 + 192 - 256], [4, 254 + 15, -16256 - 16256 - 320]]
+    for i in range(2):
+        for j in range(3):
+            assert y[i, j].item() == acc[i][j] * sa[i].item() * sb[j].item() + bias[j].item()
+    # Row scale moves one row only; a zero weight leaves the bias.
+    sa2 = sa.clone()
+    sa2[0] *= 4
+    assert torch.equal(ora.int8_scaled_mm(a, w, sa2, sb)[0], 4 * ora.int8_scaled_mm(a, w, sa, sb)[0])
+    assert torch.equal(ora.int8_scaled_mm(a, torch.zeros_like(w), sa, sb, bias), bias.expand(2, 3))
+
+
 def test_blockwise_mm_reduces_to_plain_and_brute_force():
     a, w = _rand_fp8((3, 300), 3), _rand_fp8((130, 300), 4)
     ones_a, ones_b = torch.ones(3, 3), torch.ones(2, 3)
