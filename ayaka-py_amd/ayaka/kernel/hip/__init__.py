@@ -4,6 +4,7 @@ Importing this package loads ``libayaka_fp8.so`` lazily (first call) and registe
 every operator under the reference's names and schemas.
 """
 
+from ayaka.kernel.hip.cache.cache_ops import gather_cache, scatter_cache, write_kv
 from ayaka.kernel.hip.gemm.fp8_gemm import fp8_blockwise_mm, fp8_scaled_mm
 from ayaka.kernel.hip.gemm.fp8_gemv import fp8_blockwise_gemv, fp8_weight_only_gemv
 from ayaka.kernel.hip.gemm.fp8_linear import fp8_block_linear, fp8_pertensor_linear, fp8_rowwise_linear
@@ -27,10 +28,13 @@ __all__ = [
     "fp8_scaled_mm",
     "fp8_weight_only_gemm",
     "fp8_weight_only_gemv",
+    "gather_cache",
     "int8_scaled_mm",
     "mxfp8_scaled_mm",
     "per_token_group_quant_fp8",
     "per_token_group_quant_mxfp8",
     "per_token_quant_fp8",
+    "scatter_cache",
     "static_quant_fp8",
+    "write_kv",
 ]

@@ -25,6 +25,7 @@ AYK_F16 = 1
 AYK_BF16 = 2
 AYK_E4M3 = 3
 AYK_U8 = 4
+AYK_E5M2 = 5
 
 # ayk_status values
 AYK_OK = 0
@@ -39,12 +40,14 @@ _DTYPE_CODES: dict[torch.dtype, int] = {
     torch.bfloat16: AYK_BF16,
     torch.float8_e4m3fn: AYK_E4M3,
     torch.uint8: AYK_U8,
+    torch.float8_e5m2: AYK_E5M2,
 }
 
 _p = ctypes.c_void_p
 _i = ctypes.c_int
 _l = ctypes.c_int64
 _z = ctypes.c_size_t
+_f = ctypes.c_float
 
 #: name -> argtypes (restype int unless listed in _RESTYPES)
 SIGNATURES: dict[str, list[Any]] = {
@@ -58,6 +61,8 @@ SIGNATURES: dict[str, list[Any]] = {
     "ayk_fp8_scaled_mm": [_p, _l, _p, _l, _l, _l, _l, _p, _i, _i, _p, _i, _i, _p, _i, _p, _i, _l, _p],
     "ayk_fp8_blockwise_mm": [_p, _l, _p, _l, _l, _l, _l, _p, _i, _i, _p, _i, _p, _i, _p, _i, _l, _p],
     "ayk_int8_scaled_mm": [_p, _l, _p, _l, _l, _l, _l, _p, _p, _p, _i, _p, _i, _l, _p],
+    "ayk_kv_cache_write": [_p, _p, _i, _l, _l, _l, _p, _p, _i, _l, _p, _f, _f, _p],
+    "ayk_kv_cache_gather": [_p, _i, _l, _l, _p, _l, _p, _i, _f, _i, _p],
     "ayk_mxfp8_scaled_mm": [_p, _l, _p, _l, _p, _l, _p, _l, _l, _l, _l, _p, _i, _p, _i, _l, _p],
     "ayk_fp8_weight_only_gemv": [_p, _i, _p, _l, _l, _l, _p, _i, _l, _l, _l, _p, _p, _z, _p],
     "ayk_fp8_weight_only_gemv_workspace_bytes": [_l, _l],

@@ -60,6 +60,34 @@ __host__ __device__ inline uint8_t e4m3_encode(float v) {
   return sign | (uint8_t)(rounded - ((127u - 7u) << 3));
 }
 
+// OCP e5m2 (1 sign, 5 exponent bits with bias 15, 2 mantissa bits; infinities; largest
+// finite 57344): IEEE round to nearest even, so magnitudes from 61440 (the midpoint to
+// the next binade) become infinity and NaN stays NaN (0x7F with the sign), as torch's
+// float -> float8_e5m2 cast.
+__host__ __device__ inline uint8_t e5m2_encode(float v) {
+  const uint32_t bits = f2u(v);
+  const uint8_t sign = (uint8_t)((bits >> 24) & 0x80u);
+  const uint32_t mag = bits & 0x7FFFFFFFu;
+  if (mag > 0x7F800000u) return sign | 0x7F;   // NaN
+  if (mag >= 0x47700000u) return sign | 0x7C;  // >= 61440 and infinity
+  if (mag < 0x38800000u) {                     // below 2^-14: subnormal range
+    // mag * 2^16 is exact; rounding it to an integer in [0, 4] is the code (4 == 2^-14).
+    return sign | (uint8_t)rintf(u2f(mag) * 65536.0f);
+  }
+  const uint32_t lsb = (mag >> 21) & 1u;
+  const uint32_t rounded = (mag + 0xFFFFFu + lsb) >> 21;
+  return sign | (uint8_t)(rounded - ((127u - 15u) << 2));
+}
+__host__ __device__ inline float e5m2_decode(uint8_t c) {
+  // e5m2 is the top byte of an IEEE half.
+  const uint16_t h = (uint16_t)c << 8;
+  const uint32_t sign = (uint32_t)(h & 0x8000u) << 16;
+  const uint32_t e = (h >> 10) & 0x1F, m = (h >> 8) & 3;
+  if (e == 0x1F) return u2f(sign | 0x7F800000u | (m ? 0x400000u : 0u));
+  if (e == 0) return u2f(sign | f2u((float)m * (1.0f / 65536.0f)));
+  return u2f(sign | ((e + 112u) << 23) | (m << 21));
+}
+
 // Exact decode of one e4m3fn byte (host and device; the device hot loops use the
 // gfx950 hardware converter instead, see e4m3x4_to_f32).
 __host__ __device__ inline float e4m3_decode(uint8_t c) {

@@ -34,7 +34,8 @@ typedef enum ayk_dtype {
   AYK_F16 = 1,
   AYK_BF16 = 2,
   AYK_E4M3 = 3, /* OCP float8 e4m3fn */
-  AYK_U8 = 4    /* raw bytes; as a scale: UE8M0 exponent codes */
+  AYK_U8 = 4,   /* raw bytes; as a scale: UE8M0 exponent codes */
+  AYK_E5M2 = 5  /* OCP float8 e5m2 (KV caches) */
 } ayk_dtype;
 
 typedef enum ayk_status {
@@ -169,6 +170,30 @@ int ayk_fp8_blockwise_gemv(const void* a, const void* b, int64_t ldb, int64_t N,
                            void* out, int out_dtype,
                            void* workspace, size_t workspace_bytes, ayk_stream_t stream);
 size_t ayk_fp8_blockwise_gemv_workspace_bytes(int64_t N, int64_t K);
+
+/* ------------------------------------------------------------------ KV cache
+ * Paged caches are [pages, page_size, heads, head_dim], flattened to `num_slots` rows of
+ * `width` = heads * head_dim elements; a slot is page * page_size + offset. */
+
+/* Replaces ayaka::cache_write_kv (kernel/triton/cache/cache_ops.py:160; oracle
+ * _write_kv_reference :97 with _write_reference :40) and, with `value` == NULL,
+ * ayaka::cache_scatter (cache_ops.py:65). Row t of key (and value), `src_row_stride`
+ * elements apart, is written to slot slots[t] of key_cache (value_cache). An fp8 cache
+ * (AYK_E4M3 / AYK_E5M2) stores round-to-nearest-even(clamp(x * inverse, +-max)); a float
+ * cache stores x cast to its dtype. Negative slots are skipped; slots >= num_slots are
+ * skipped too (the caller validates them, as the reference requires). */
+int ayk_kv_cache_write(const void* key, const void* value, int src_dtype, int64_t num_tokens,
+                       int64_t width, int64_t src_row_stride, void* key_cache, void* value_cache,
+                       int cache_dtype, int64_t num_slots, const int64_t* slots,
+                       float k_inverse, float v_inverse, ayk_stream_t stream);
+
+/* Replaces ayaka::cache_gather (cache_ops.py:230; oracle _gather_reference :206).
+ * dest[i] = cache[slots[i]] (repeats allowed), dequantized as float(value) * scale when
+ * `dequantize`, else copied / cast to `dest_dtype`. A slot outside [0, num_slots) gives
+ * a zero row. */
+int ayk_kv_cache_gather(const void* cache, int cache_dtype, int64_t num_slots, int64_t width,
+                        const int64_t* slots, int64_t n, void* dest, int dest_dtype, float scale,
+                        int dequantize, ayk_stream_t stream);
 
 #ifdef __cplusplus
 }

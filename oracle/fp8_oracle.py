@@ -249,3 +249,38 @@ def fp8_linear(recipe: str, x: torch.Tensor, weight: torch.Tensor, weight_scale:
     if bias is not None and not (fused is not None and m > 1 and recipe != "w8a16"):
         y = y + bias
     return y.reshape(*lead, n)
+
+
+# ------------------------------------------------------------------ KV cache (§8 f3)
+def kv_write(source, cache, slots, inverse_scale: float) -> None:
+    """Write rows of ``source`` [n, heads, head_dim] to ``cache`` [pages, page_size, heads,
+    head_dim] at flattened slots (reference cache_ops.py:40-62 ``_write_reference``, with
+    the negative-slot filter of ``_write_kv_reference`` :109-111): fp8 caches take
+    ``x.float() * inverse_scale`` clamped to the dtype's finite range, then torch's
+    round-to-nearest-even cast; float caches a plain cast.
+    """
+    valid = slots >= 0
+    source, slots = source[valid], slots[valid]
+    payload = source
+    if cache.dtype in (torch.float8_e4m3fn, torch.float8_e5m2):
+        limit = torch.finfo(cache.dtype).max
+        payload = payload.float().mul(inverse_scale).clamp(-limit, limit)
+    payload = payload.to(cache.dtype)
+    target = cache.flatten(0, 1)
+    if cache.dtype in (torch.float8_e4m3fn, torch.float8_e5m2):
+        target.view(torch.uint8).index_copy_(0, slots, payload.contiguous().view(torch.uint8))
+    else:
+        target.index_copy_(0, slots, payload)
+
+
+def kv_gather(cache, slots, dtype, scale: float, dequantize: bool) -> torch.Tensor:
+    """Rows of ``cache`` at ``slots`` (reference cache_ops.py:206-227 ``_gather_reference``):
+    ``float(x) * scale`` when dequantizing, then cast to ``dtype``."""
+    flat = cache.flatten(0, 1)
+    if cache.dtype in (torch.float8_e4m3fn, torch.float8_e5m2):
+        result = flat.view(torch.uint8).index_select(0, slots).view(cache.dtype)
+    else:
+        result = flat.index_select(0, slots)
+    if dequantize:
+        result = result.float().mul(scale)
+    return result.to(dtype)

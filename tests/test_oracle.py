@@ -326,3 +326,60 @@ def test_linear_dispatch_m1_equals_gemv_and_prefill_quantizes():
     x8 = torch.randn(8, k, generator=torch.Generator().manual_seed(18)).to(torch.bfloat16)
     q, s = ora.per_token_quant(x8)
     assert torch.equal(ora.fp8_linear("w8a8_rowwise", x8, w, scale), ora.fp8_scaled_mm(q, w, s, scale).to(torch.bfloat16))
+
+
+def _e5m2_table() -> torch.Tensor:
+    """All 256 e5m2 values from the bit layout (1 sign, 5 exponent bias 15, 2 mantissa)."""
+    vals = []
+    for c in range(256):
+        s = -1.0 if c & 0x80 else 1.0
+        e, m = (c >> 2) & 0x1F, c & 3
+        if e == 0x1F:
+            vals.append(float("nan") if m else s * float("inf"))
+        elif e == 0:
+            vals.append(s * m * 2.0**-16)
+        else:
+            vals.append(s * (1 + m / 4) * 2.0 ** (e - 15))
+    return torch.tensor(vals, dtype=torch.float64)
+
+
+def test_kv_write_e5m2_is_clamped_round_nearest_even():
+    """The oracle's e5m2 path (torch's cast after the clamp) against a brute-force nearest
+    search on the e5m2 grid built from its bit layout: every finite value, every midpoint,
+    values past the clamp and NaN."""
+    table = _e5m2_table()
+    finite = torch.isfinite(table)
+    grid = table[finite].unique()
+    mids = (grid[1:] + grid[:-1]) / 2
+    v = torch.cat([grid, mids, torch.tensor([6.0e4, -7.0e4, 1e9, 2.0**-18, -(2.0**-17)])]).float()
+    cache = torch.zeros(1, v.numel(), 1, 1, dtype=torch.float8_e5m2)
+    ora.kv_write(v.reshape(-1, 1, 1), cache, torch.arange(v.numel()), 1.0)
+    got = cache.flatten().view(torch.uint8).long()
+    vc = v.double().clamp(-57344, 57344)
+    codes = torch.arange(256)
+    fin_codes = codes[finite]
+    d = (vc[:, None] - table[finite][None, :]).abs()
+    best = d.min(dim=1, keepdim=True).values
+    cand = d == best
+    even = (fin_codes % 2 == 0)[None, :]
+    sign_ok = (fin_codes >= 128)[None, :] == torch.signbit(vc)[:, None]
+    pick = (cand & even).int() * 4 + cand.int() * 2 + sign_ok.int()
+    want = fin_codes[pick.argmax(dim=1)]
+    assert torch.equal(got, want)
+    nan_cache = torch.zeros(1, 2, 1, 1, dtype=torch.float8_e5m2)
+    ora.kv_write(torch.tensor([float("nan"), -float("nan")]).reshape(2, 1, 1), nan_cache, torch.arange(2), 1.0)
+    assert torch.isnan(nan_cache.float()).all()
+
+
+def test_kv_write_scales_skips_negative_slots_and_gathers_back():
+    x = torch.tensor([[[1.0, -2.0]], [[300.0, 0.5]], [[7.0, 8.0]]])
+    cache = torch.zeros(2, 2, 1, 2, dtype=torch.float8_e4m3fn)
+    ora.kv_write(x, cache, torch.tensor([3, -1, 0]), 2.0)  # token 1 masked
+    flat = cache.float().reshape(4, 2)
+    assert flat[3].tolist() == [2.0, -4.0] and flat[0].tolist() == [14.0, 16.0]
+    assert flat[1].abs().sum() == 0 and flat[2].abs().sum() == 0
+    big = torch.zeros(1, 1, 1, 2, dtype=torch.float8_e4m3fn)
+    ora.kv_write(torch.tensor([[[1000.0, -1000.0]]]), big, torch.tensor([0]), 1.0)
+    assert big.flatten().float().tolist() == [448.0, -448.0]  # clamped, not NaN
+    back = ora.kv_gather(cache, torch.tensor([3, 3, 0]), torch.float32, 0.5, True)
+    assert back.reshape(3, 2).tolist() == [[1.0, -2.0], [1.0, -2.0], [7.0, 8.0]]
