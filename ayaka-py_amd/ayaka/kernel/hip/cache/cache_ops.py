@@ -57,14 +57,12 @@ def _check_plane(source: torch.Tensor, cache: torch.Tensor, slots: torch.Tensor)
 
 
 def _source_rows(source: torch.Tensor, width: int) -> tuple[torch.Tensor, int]:
-    """``source`` as rows of ``width`` contiguous elements and the row stride."""
+    """``source`` as rows of ``width`` contiguous elements and the row stride. Any
+    alignment is accepted: the library takes 8-element vector kernels when rows are
+    16-byte aligned, per-element kernels otherwise."""
     rows = source.reshape(source.shape[0], width)
     if rows.stride(-1) != 1 or (rows.shape[0] > 1 and rows.stride(0) < width):
         rows = rows.contiguous()
-    if rows.dtype != torch.float32 and (rows.data_ptr() % 16 or (rows.shape[0] > 1 and rows.stride(0) % 8)):
-        rows = rows.contiguous()
-        if rows.data_ptr() % 16:
-            rows = rows.clone()
     stride = int(rows.stride(0)) if rows.shape[0] > 1 else width
     return rows, stride
 

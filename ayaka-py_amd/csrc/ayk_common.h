@@ -193,6 +193,41 @@ __device__ inline void e4m3x4_to_f32(uint32_t w, float* out) {
   out[3] = hi.y;
 }
 
+// Four fp32 values -> four fp8 codes in one dword (byte i holds value i), with the
+// hardware round-to-nearest-even converters v_cvt_pk_fp8_f32 (e4m3) and
+// v_cvt_pk_bf8_f32 (e5m2). For every non-NaN fp32 input they give exactly
+// e4m3_encode / e5m2_encode (compared over all 2^32 bit patterns on gfx950); a NaN
+// comes out as 0xFF / 0xFE whatever its sign, so NaN inputs are re-encoded as
+// sign | 0x7F, torch's NaN code, on a branch that finite data never takes.
+__device__ inline uint32_t fp8_nan_patch(uint32_t w, const float* v) {
+#pragma unroll
+  for (int i = 0; i < 4; ++i) {
+    if (v[i] != v[i]) {
+      const uint32_t code = ((f2u(v[i]) >> 24) & 0x80u) | 0x7Fu;
+      w = (w & ~(0xFFu << (8 * i))) | (code << (8 * i));
+    }
+  }
+  return w;
+}
+__device__ inline uint32_t e4m3x4_encode(float a, float b, float c, float d) {
+  uint32_t w = (uint32_t)__builtin_amdgcn_cvt_pk_fp8_f32(a, b, 0, false);
+  w = (uint32_t)__builtin_amdgcn_cvt_pk_fp8_f32(c, d, (int)w, true);
+  if (__builtin_expect((a != a) | (b != b) | (c != c) | (d != d), 0)) {
+    const float v[4] = {a, b, c, d};
+    w = fp8_nan_patch(w, v);
+  }
+  return w;
+}
+__device__ inline uint32_t e5m2x4_encode(float a, float b, float c, float d) {
+  uint32_t w = (uint32_t)__builtin_amdgcn_cvt_pk_bf8_f32(a, b, 0, false);
+  w = (uint32_t)__builtin_amdgcn_cvt_pk_bf8_f32(c, d, (int)w, true);
+  if (__builtin_expect((a != a) | (b != b) | (c != c) | (d != d), 0)) {
+    const float v[4] = {a, b, c, d};
+    w = fp8_nan_patch(w, v);
+  }
+  return w;
+}
+
 // NaN-propagating max of magnitudes, the semantics of torch's amax.
 __device__ inline float nanmax(float a, float b) { return (a > b || a != a) ? a : b; }
 

@@ -58,11 +58,13 @@ __device__ inline float absmax_n(const float* f, float m) {
 // Quantize N floats with scale s (q = e4m3(clamp(f / s))) and store N bytes.
 template <int N>
 __device__ inline void store_quant(uint8_t* dst, const float* f, float s) {
-  uint32_t w[(N + 3) / 4] = {};
+  static_assert(N % 4 == 0, "16-byte vectors hold 4 or 8 elements");
+  float q[N];
 #pragma unroll
-  for (int i = 0; i < N; ++i) {
-    w[i / 4] |= (uint32_t)e4m3_encode(clamp_e4m3(f[i] / s)) << (8 * (i % 4));
-  }
+  for (int i = 0; i < N; ++i) q[i] = clamp_e4m3(f[i] / s);
+  uint32_t w[N / 4];
+#pragma unroll
+  for (int i = 0; i < N / 4; ++i) w[i] = e4m3x4_encode(q[4 * i], q[4 * i + 1], q[4 * i + 2], q[4 * i + 3]);
   if constexpr (N == 8) {
     *reinterpret_cast<uint2*>(dst) = make_uint2(w[0], w[1]);
   } else {
@@ -219,10 +221,11 @@ __global__ __launch_bounds__(kQuantThreads) void group_quant_vec_kernel(
       unpack16<T>(cache[j], f);
       uint32_t w[V / 4] = {};
       if (!ms.zero) {
+        float q[V];
 #pragma unroll
-        for (int i = 0; i < V; ++i) {
-          w[i / 4] |= (uint32_t)e4m3_encode(clamp_e4m3(f[i] * ms.inv)) << (8 * (i % 4));
-        }
+        for (int i = 0; i < V; ++i) q[i] = clamp_e4m3(f[i] * ms.inv);
+#pragma unroll
+        for (int i = 0; i < V / 4; ++i) w[i] = e4m3x4_encode(q[4 * i], q[4 * i + 1], q[4 * i + 2], q[4 * i + 3]);
       }
       uint8_t* dst = qg + (int64_t)(lig + j * GL) * V;
       if constexpr (V == 8) {

@@ -184,6 +184,97 @@ def _bench_gemm(device, reps=20, warmup=5):
     return results
 
 
+def _time_rotated(fns, reps: int, warmup: int) -> float:
+    """Average ms per call over `reps` calls cycling through `fns` (input copies whose
+    total exceeds the 256 MB Infinity Cache, so each call streams from HBM)."""
+    for i in range(warmup):
+        fns[i % len(fns)]()
+    torch.cuda.synchronize()
+    start, end = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+    start.record()
+    for i in range(reps):
+        fns[i % len(fns)]()
+    end.record()
+    torch.cuda.synchronize()
+    return start.elapsed_time(end) / reps
+
+
+def _hbm_entry(ms: float, nbytes: int, **extra) -> dict:
+    gbs = nbytes / (ms * 1e-3) / 1e9
+    return {**extra, "us": round(ms * 1e3, 2), "bytes": nbytes, "GB/s": round(gbs, 1),
+            "frac": round(gbs / HBM_PEAK_GBS, 4)}
+
+
+def _bench_kv_cache(device, reps=40, warmup=8, copies=4):
+    """FP8 KV-cache write (bf16 K/V -> e4m3 pages) and dequantizing gather (e4m3 -> bf16)
+    for a 16384-token prefill chunk of Llama-3-8B (8 KV heads x 128) into a 65536-slot
+    cache at shuffled slots, rotating over `copies` sources and caches. Algorithmic bytes:
+    write 2 planes x (2 B read + 1 B written) per element + 8 B per slot; gather 1 B read
+    + 2 B written per element + 8 B per slot."""
+    from ayaka.kernel.hip import gather_cache, write_kv
+
+    g = torch.Generator(device=device).manual_seed(0)
+    n, heads, dim, pages, page_size = 16384, 8, 128, 4096, 16
+    width = heads * dim
+    sets = []
+    for _ in range(copies):
+        key = torch.randn(n, heads, dim, generator=g, device=device).to(torch.bfloat16)
+        value = torch.randn(n, heads, dim, generator=g, device=device).to(torch.bfloat16)
+        k_cache = torch.zeros(pages, page_size, heads, dim, device=device, dtype=torch.float8_e4m3fn)
+        v_cache = torch.zeros_like(k_cache)
+        slots = torch.randperm(pages * page_size, generator=g, device=device)[:n]
+        dest = torch.empty(n, heads, dim, device=device, dtype=torch.bfloat16)
+        sets.append((key, value, k_cache, v_cache, slots, dest))
+    writes = [lambda s=s: write_kv(s[0], s[1], s[2], s[3], s[4], 0.5, 0.5) for s in sets]
+    gathers = [lambda s=s: gather_cache(s[2], s[4], s[5], 2.0, True) for s in sets]
+    results = {
+        "write_kv_bf16_to_e4m3": _hbm_entry(_time_rotated(writes, reps, warmup), 2 * n * width * 3 + 8 * n,
+                                            tokens=n, width=width),
+        "gather_e4m3_to_bf16": _hbm_entry(_time_rotated(gathers, reps, warmup), n * width * 3 + 8 * n,
+                                          tokens=n, width=width),
+    }
+    del sets, writes, gathers
+    torch.cuda.empty_cache()
+    return results
+
+
+def _bench_quant(device, reps=40, warmup=8, copies=6):
+    """Activation quantizers on bf16 prefill activations (M = 4096) at the config hidden
+    sizes, rotating over `copies` inputs. Algorithmic bytes: 2 B read + 1 B written per
+    element, plus the scales written."""
+    from ayaka.kernel.hip import (per_token_group_quant_fp8, per_token_group_quant_mxfp8, per_token_quant_fp8,
+                                  static_quant_fp8)
+
+    g = torch.Generator(device=device).manual_seed(0)
+    m = 4096
+    results = {}
+
+    def inputs(k):
+        return [torch.randn(m, k, generator=g, device=device).to(torch.bfloat16) for _ in range(copies)]
+
+    xs = inputs(3584)
+    results["per_token_qwen2_k3584"] = _hbm_entry(
+        _time_rotated([lambda x=x: per_token_quant_fp8(x) for x in xs], reps, warmup), m * 3584 * 3 + m * 4, M=m, K=3584)
+    scale = torch.full((), 0.05, device=device)
+    outs = [torch.empty(m, 3584, dtype=torch.float8_e4m3fn, device=device) for _ in xs]
+    results["static_qwen2_k3584"] = _hbm_entry(
+        _time_rotated([lambda x=x, o=o: static_quant_fp8(x, scale, out=o) for x, o in zip(xs, outs)], reps, warmup),
+        m * 3584 * 3, M=m, K=3584)
+    del xs, outs
+    xs = inputs(7168)
+    results["group128_dsv3_k7168"] = _hbm_entry(
+        _time_rotated([lambda x=x: per_token_group_quant_fp8(x, 128) for x in xs], reps, warmup),
+        m * 7168 * 3 + m * 56 * 4, M=m, K=7168)
+    del xs
+    xs = inputs(8192)
+    results["mxfp8_llama70b_k8192"] = _hbm_entry(
+        _time_rotated([lambda x=x: per_token_group_quant_mxfp8(x, 32) for x in xs], reps, warmup),
+        m * 8192 * 3 + m * 256, M=m, K=8192)
+    del xs
+    torch.cuda.empty_cache()
+    return results
+
+
 def _bench_decode_m(layers, reps=20):
     """W8A16 at the other Cfg2 decode batch sizes (M = 4, 16, 32): GB/s per projection
     (algorithmic bytes: fp8 weights + scales + bf16 x and out), each launch timed in a
@@ -346,6 +437,8 @@ def main() -> int:
     result["decode_w8a16"] = _bench_decode_m(layers)
     if not args.no_gemm:
         result["gemm"] = _bench_gemm(device)
+    result["quant"] = _bench_quant(device)
+    result["kv_cache"] = _bench_kv_cache(device)
     if not args.no_cpu:
         result["cpu_baseline"] = _cpu_baseline()
     print(json.dumps(result), flush=True)

@@ -34,6 +34,17 @@ def _bytes(t):
     return t.contiguous().view(torch.uint8) if t.dtype.itemsize == 1 else t.contiguous().view(torch.int16 if t.dtype.itemsize == 2 else torch.int32)
 
 
+def _same(got, ref) -> bool:
+    """Bit-identical, except that a NaN in a 16/32-bit float tensor may carry any payload
+    (torch's own fp32 -> bf16 cast gives 0xFFFF on CPU, 0x7FC0 in its scalar code). fp8
+    NaN encodings are fixed by the format and compared as bytes."""
+    got, ref = got.cpu(), ref.cpu()
+    if got.dtype.itemsize == 1:
+        return torch.equal(_bytes(got), _bytes(ref))
+    nan = torch.isnan(ref)
+    return torch.equal(torch.isnan(got), nan) and torch.equal(_bytes(got)[~nan], _bytes(ref)[~nan])
+
+
 @pytest.mark.parametrize("cache_dtype", CACHE_DTYPES)
 @pytest.mark.parametrize("src_dtype", [torch.bfloat16, torch.float16, torch.float32])
 def test_write_kv_bit_exact(gpu, src_dtype, cache_dtype):
@@ -44,7 +55,7 @@ def test_write_kv_bit_exact(gpu, src_dtype, cache_dtype):
     key, value = _source(n, heads, dim, src_dtype, 1), _source(n, heads, dim, src_dtype, 2)
     g = torch.Generator().manual_seed(3)
     slots = torch.randperm(pages * page_size, generator=g)[:n]
-    slots[::9] = -1  # masked padding tokens
+    slots[4::9] = -1  # masked padding tokens (token 0, holding the NaN/inf cases, is written)
     k_cache = torch.full((pages, page_size, heads, dim), 0.25).to(cache_dtype)
     v_cache = torch.full((pages, page_size, heads, dim), -0.5).to(cache_dtype)
     k_ref, v_ref = k_cache.clone(), v_cache.clone()
@@ -52,8 +63,8 @@ def test_write_kv_bit_exact(gpu, src_dtype, cache_dtype):
     ora.kv_write(value, v_ref, slots, 3.0)
     kg, vg = k_cache.to(gpu), v_cache.to(gpu)
     write_kv(key.to(gpu), value.to(gpu), kg, vg, slots.to(gpu), 0.5, 3.0)
-    assert torch.equal(_bytes(kg.cpu()), _bytes(k_ref)), "key cache differs"
-    assert torch.equal(_bytes(vg.cpu()), _bytes(v_ref)), "value cache differs"
+    assert _same(kg, k_ref), "key cache differs"
+    assert _same(vg, v_ref), "value cache differs"
 
 
 @pytest.mark.parametrize("cache_dtype", [torch.float8_e4m3fn, torch.float8_e5m2])
@@ -70,7 +81,7 @@ def test_scatter_cache_one_plane_with_strided_source(gpu, cache_dtype):
     ora.kv_write(src.contiguous(), ref, slots, 0.125)
     cg = cache.to(gpu)
     scatter_cache(src.to(gpu), cg, slots.to(gpu), 0.125)
-    assert torch.equal(_bytes(cg.cpu()), _bytes(ref))
+    assert _same(cg, ref)
 
 
 @pytest.mark.parametrize("cache_dtype", [torch.float8_e4m3fn, torch.float8_e5m2])
@@ -86,10 +97,10 @@ def test_gather_cache_dequantize(gpu, cache_dtype, dest_dtype):
     ref = ora.kv_gather(cache, slots, dest_dtype, 0.75, True)
     dest = torch.empty(50, heads, dim, dtype=dest_dtype, device=gpu)
     gather_cache(cache.to(gpu), slots.to(gpu), dest, 0.75, True)
-    assert torch.equal(_bytes(dest.cpu()), _bytes(ref.reshape(50, heads, dim)))
+    assert _same(dest, ref.reshape(50, heads, dim))
     raw = torch.empty(50, heads, dim, dtype=cache_dtype, device=gpu)
     gather_cache(cache.to(gpu), slots.to(gpu), raw, 1.0, False)
-    assert torch.equal(_bytes(raw.cpu()), _bytes(ora.kv_gather(cache, slots, cache_dtype, 1.0, False).reshape(50, heads, dim)))
+    assert _same(raw, ora.kv_gather(cache, slots, cache_dtype, 1.0, False).reshape(50, heads, dim))
 
 
 def test_kv_cache_contract(gpu):
@@ -109,3 +120,113 @@ def test_kv_cache_contract(gpu):
         write_kv(key.cpu(), key.cpu(), cache.cpu(), cache.cpu(), slots.cpu(), 1.0, 1.0)
     with pytest.raises(ValueError, match="dequantize"):
         gather_cache(cache.to(torch.bfloat16), slots, torch.empty(4, 2, 8, device=gpu), 1.0, True)
+
+
+# (heads, head_dim, source storage offset): width 15 and a source one element off a
+# 16-byte boundary take the per-element kernels; width 16 the 8-element vector kernels.
+LAYOUTS = [(3, 5, 0), (2, 8, 1), (2, 8, 0)]
+
+
+@pytest.mark.parametrize("layout", LAYOUTS)
+@pytest.mark.parametrize("cache_dtype", CACHE_DTYPES + [torch.float32])
+@pytest.mark.parametrize("src_dtype", [torch.bfloat16, torch.float32])
+def test_write_kv_ragged_and_unaligned_rows(gpu, src_dtype, cache_dtype, layout):
+    from ayaka.kernel.hip import write_kv
+
+    heads, dim, offset = layout
+    _say(f"write_kv layout={layout} src={src_dtype} cache={cache_dtype}")
+    pages, page_size, n = 6, 8, 33
+    key, value = _source(n, heads, dim, src_dtype, 11), _source(n, heads, dim, src_dtype, 12)
+    slots = torch.randperm(pages * page_size, generator=torch.Generator().manual_seed(13))[:n]
+    slots[5] = -3
+    k_cache = torch.zeros(pages, page_size, heads, dim).to(cache_dtype)
+    v_cache = torch.ones(pages, page_size, heads, dim).to(cache_dtype)
+    k_ref, v_ref = k_cache.clone(), v_cache.clone()
+    ora.kv_write(key, k_ref, slots, 2.0)
+    ora.kv_write(value, v_ref, slots, 0.03125)
+
+    def shifted(x):  # same values, data pointer `offset` elements past an aligned base
+        base = torch.empty(x.numel() + 8, dtype=x.dtype, device=gpu)
+        view = base[offset: offset + x.numel()].view(x.shape)
+        view.copy_(x.to(gpu))
+        return view
+
+    kg, vg = k_cache.to(gpu), v_cache.to(gpu)
+    write_kv(shifted(key), shifted(value), kg, vg, slots.to(gpu), 2.0, 0.03125)
+    assert _same(kg, k_ref), "key cache differs"
+    assert _same(vg, v_ref), "value cache differs"
+
+
+@pytest.mark.parametrize("layout", [(3, 5), (2, 8)])
+@pytest.mark.parametrize("cache_dtype", CACHE_DTYPES)
+def test_gather_cache_ragged_rows_and_same_dtype_copy(gpu, cache_dtype, layout):
+    from ayaka.kernel.hip import gather_cache
+
+    heads, dim = layout
+    _say(f"gather_cache layout={layout} cache={cache_dtype}")
+    pages, page_size = 4, 8
+    g = torch.Generator().manual_seed(14)
+    cache = _source(pages * page_size, heads, dim, torch.float32, 15).view(pages, page_size, heads, dim).to(cache_dtype)
+    slots = torch.randint(0, pages * page_size, (21,), generator=g)
+    cg, sg = cache.to(gpu), slots.to(gpu)
+    same = torch.empty(21, heads, dim, dtype=cache_dtype, device=gpu)
+    gather_cache(cg, sg, same, 1.0, False)
+    ref = ora.kv_gather(cache, slots, cache_dtype, 1.0, False).reshape(21, heads, dim)
+    assert _same(same, ref)
+    if cache_dtype in (torch.float8_e4m3fn, torch.float8_e5m2):
+        deq = torch.empty(21, heads, dim, dtype=torch.bfloat16, device=gpu)
+        gather_cache(cg, sg, deq, 0.375, True)
+        ref = ora.kv_gather(cache, slots, torch.bfloat16, 0.375, True).reshape(21, heads, dim)
+        assert _same(deq, ref)
+    else:
+        widened = torch.empty(21, heads, dim, dtype=torch.float32, device=gpu)
+        gather_cache(cg, sg, widened, 1.0, False)
+        ref = ora.kv_gather(cache, slots, torch.float32, 1.0, False).reshape(21, heads, dim)
+        assert _same(widened, ref)
+
+
+def _fp32_patterns(chunk: int, count: int, device) -> torch.Tensor:
+    """fp32 values whose bit patterns are chunk * count .. (chunk + 1) * count - 1."""
+    start = chunk * count
+    start = start - (1 << 32) if start >= (1 << 31) else start  # int32 two's complement
+    return (torch.arange(count, dtype=torch.int32, device=device) + start).view(torch.float32)
+
+
+@pytest.mark.parametrize("cache_dtype", [torch.float8_e4m3fn, torch.float8_e5m2])
+def test_write_every_fp32_pattern(gpu, cache_dtype):
+    """All 2^32 fp32 bit patterns through the vector write (inverse scale 1), against
+    torch's clamp + round-to-nearest-even cast on the same device, in 2^28-element chunks."""
+    from ayaka.kernel.hip import scatter_cache
+
+    limit = torch.finfo(cache_dtype).max
+    count, heads, dim = 1 << 28, 8, 128
+    n = count // (heads * dim)
+    slots = torch.arange(n, device=gpu)
+    cache = torch.empty(n // 16, 16, heads, dim, dtype=cache_dtype, device=gpu)
+    for chunk in range(1 << 4):
+        _say(f"write_kv fp32 sweep {cache_dtype} chunk {chunk}")
+        x = _fp32_patterns(chunk, count, gpu)
+        scatter_cache(x.view(n, heads, dim), cache, slots, 1.0)
+        ref = x.clamp(-limit, limit).to(cache_dtype)
+        bad = int((cache.view(-1).view(torch.uint8) != ref.view(torch.uint8)).sum())
+        assert bad == 0, f"{bad} codes differ in chunk {chunk}"
+        del x, ref
+
+
+@pytest.mark.parametrize("src_dtype", [torch.bfloat16, torch.float16])
+@pytest.mark.parametrize("cache_dtype", [torch.float8_e4m3fn, torch.float8_e5m2])
+def test_write_every_16bit_pattern(gpu, src_dtype, cache_dtype):
+    """All 2^16 bf16 / fp16 patterns at two inverse scales, against the oracle."""
+    from ayaka.kernel.hip import write_kv
+
+    _say(f"write_kv 16-bit sweep {src_dtype} -> {cache_dtype}")
+    x = torch.arange(1 << 16, dtype=torch.int32).to(torch.int16).view(src_dtype).view(64, 8, 128)
+    slots = torch.arange(64)
+    k_ref = torch.zeros(4, 16, 8, 128).to(cache_dtype)
+    v_ref = k_ref.clone()
+    ora.kv_write(x, k_ref, slots, 1.0)
+    ora.kv_write(x, v_ref, slots, 0.3)
+    kg, vg = k_ref.clone().zero_().to(gpu), v_ref.clone().zero_().to(gpu)
+    write_kv(x.to(gpu), x.to(gpu), kg, vg, slots.to(gpu), 1.0, 0.3)
+    assert torch.equal(_bytes(kg.cpu()), _bytes(k_ref))
+    assert torch.equal(_bytes(vg.cpu()), _bytes(v_ref))

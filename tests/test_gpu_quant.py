@@ -160,3 +160,24 @@ def test_encode_every_fp32_neighbourhood(gpu):
     nan_r = torch.isnan(ref.float())
     assert torch.equal(torch.isnan(q.cpu().float()), nan_r)
     assert torch.equal(qb[~nan_r], rb[~nan_r])
+
+
+def test_static_quant_every_fp32_pattern(gpu):
+    """All 2^32 fp32 bit patterns through static quant with scale 1 (x / 1 is x), against
+    torch's clamp + round-to-nearest-even e4m3 cast on the same device, in 2^28 chunks:
+    pins the hardware conversion in the vector store against the cast for every input."""
+    from ayaka.kernel.hip import static_quant_fp8
+
+    count = 1 << 28
+    one = torch.ones((), dtype=torch.float32, device=gpu)
+    out = torch.empty(count, dtype=torch.float8_e4m3fn, device=gpu)
+    for chunk in range(1 << 4):
+        _say(f"static_quant_fp8 fp32 sweep chunk {chunk}")
+        start = chunk * count
+        start = start - (1 << 32) if start >= (1 << 31) else start
+        x = (torch.arange(count, dtype=torch.int32, device=gpu) + start).view(torch.float32)
+        static_quant_fp8(x.view(1 << 14, 1 << 14), one, out=out.view(1 << 14, 1 << 14))
+        ref = x.clamp(-448.0, 448.0).to(torch.float8_e4m3fn)
+        bad = int((out.view(torch.uint8) != ref.view(torch.uint8)).sum())
+        assert bad == 0, f"{bad} codes differ in chunk {chunk}"
+        del x, ref
