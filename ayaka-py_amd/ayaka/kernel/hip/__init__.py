@@ -11,6 +11,7 @@ from ayaka.kernel.hip.gemm.fp8_linear import fp8_block_linear, fp8_pertensor_lin
 from ayaka.kernel.hip.gemm.fp8_mxfp8_gemm import mxfp8_scaled_mm
 from ayaka.kernel.hip.gemm.fp8_w8a16_gemm import fp8_matmul_channelwise, fp8_weight_only_gemm
 from ayaka.kernel.hip.gemm.int8_gemm import int8_scaled_mm
+from ayaka.kernel.hip.moe.moe_grouped_gemm import fp8_blockwise_scaled_grouped_mm
 from ayaka.kernel.hip.quant.fp8_quant import (
     per_token_group_quant_fp8,
     per_token_group_quant_mxfp8,
@@ -22,6 +23,7 @@ __all__ = [
     "fp8_block_linear",
     "fp8_blockwise_gemv",
     "fp8_blockwise_mm",
+    "fp8_blockwise_scaled_grouped_mm",
     "fp8_matmul_channelwise",
     "fp8_pertensor_linear",
     "fp8_rowwise_linear",

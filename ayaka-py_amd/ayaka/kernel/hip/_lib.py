@@ -60,6 +60,7 @@ SIGNATURES: dict[str, list[Any]] = {
     "ayk_static_quant_fp8": [_p, _i, _l, _p, _i, _p, _p],
     "ayk_fp8_scaled_mm": [_p, _l, _p, _l, _l, _l, _l, _p, _i, _i, _p, _i, _i, _p, _i, _p, _i, _l, _p],
     "ayk_fp8_blockwise_mm": [_p, _l, _p, _l, _l, _l, _l, _p, _i, _i, _p, _i, _p, _i, _p, _i, _l, _p],
+    "ayk_fp8_grouped_blockwise_mm": [_p, _p, _p, _p, _p, _p, _l, _l, _l, _l, _p, _i, _p],
     "ayk_int8_scaled_mm": [_p, _l, _p, _l, _l, _l, _l, _p, _p, _p, _i, _p, _i, _l, _p],
     "ayk_kv_cache_write": [_p, _p, _i, _l, _l, _l, _p, _p, _i, _l, _p, _f, _f, _p],
     "ayk_kv_cache_gather": [_p, _i, _l, _l, _p, _l, _p, _i, _f, _i, _p],

@@ -983,7 +983,10 @@ __device__ __attribute__((always_inline)) inline void block_epilogue(const GemmA
   }
 }
 
-__global__ __launch_bounds__(kBlkThreads, 1) void fp8_gemm_block_kernel(GemmArgs g) {
+// One 128 x 128 output tile (tile coordinates tm, tn) of a block-scaled GEMM, staged
+// through the four LDS buffers the calling kernel declares (L0 also stages the epilogue).
+__device__ __attribute__((always_inline)) inline void block_gemm_tile(const GemmArgs& g, int tm, int tn, uint8_t* L0,
+                                                                      uint8_t* L1, uint8_t* L2, uint8_t* L3) {
   constexpr int FN = 2, FM = 2;
   constexpr int kWDma = 2, kADma = 2;           // direct loads per wavefront per step
   constexpr int kDma = kWDma + kADma;
@@ -991,17 +994,11 @@ __global__ __launch_bounds__(kBlkThreads, 1) void fp8_gemm_block_kernel(GemmArgs
   // Ops issued per step alternate kDma + kScaleOps (a block's first step: the refill and
   // the next block's scales) and kDma, so any two consecutive steps issue this many:
   constexpr int kAfterNext = 2 * kDma + kScaleOps;
-  __shared__ __attribute__((aligned(1024))) uint8_t L0[kBlkEpilogueLds > kBlkStage ? kBlkEpilogueLds : kBlkStage];
-  __shared__ __attribute__((aligned(1024))) uint8_t L1[kBlkStage];
-  __shared__ __attribute__((aligned(1024))) uint8_t L2[kBlkStage];
-  __shared__ __attribute__((aligned(1024))) uint8_t L3[kBlkStage];
 
   const int tid = threadIdx.x, lane = tid & 63;
   const int wave_u = __builtin_amdgcn_readfirstlane(tid >> 6);
   const int wn = wave_u >> 1, wm = wave_u & 1;  // 64-row n half, 64-row m half
   const int h = lane >> 5, frow = lane & 31;
-  int tm, tn;
-  big_tile_coords(blockIdx.x, g.tiles_m, (int)cdiv(g.N, kBlkTile), tm, tn);
   const int64_t n_base = (int64_t)tn * kBlkTile, m_base = (int64_t)tm * kBlkTile;
   const int nk = (int)(g.K / kBigK);     // even: K % 128 == 0
   const int kblocks = nk / 2;
@@ -1168,6 +1165,115 @@ __global__ __launch_bounds__(kBlkThreads, 1) void fp8_gemm_block_kernel(GemmArgs
   if (g.out_dtype == AYK_BF16) block_epilogue<AYK_BF16>(g, acc, m_base, n_base, L0);
   else if (g.out_dtype == AYK_F16) block_epilogue<AYK_F16>(g, acc, m_base, n_base, L0);
   else block_epilogue<AYK_F32>(g, acc, m_base, n_base, L0);
+}
+
+#define AYK_BLOCK_LDS                                                                                        \
+  __shared__ __attribute__((aligned(1024))) uint8_t L0[kBlkEpilogueLds > kBlkStage ? kBlkEpilogueLds : kBlkStage]; \
+  __shared__ __attribute__((aligned(1024))) uint8_t L1[kBlkStage];                                         \
+  __shared__ __attribute__((aligned(1024))) uint8_t L2[kBlkStage];                                         \
+  __shared__ __attribute__((aligned(1024))) uint8_t L3[kBlkStage]
+
+__global__ __launch_bounds__(kBlkThreads, 1) void fp8_gemm_block_kernel(GemmArgs g) {
+  AYK_BLOCK_LDS;
+  int tm, tn;
+  big_tile_coords(blockIdx.x, g.tiles_m, (int)cdiv(g.N, kBlkTile), tm, tn);
+  block_gemm_tile(g, tm, tn, L0, L1, L2, L3);
+}
+
+// ------------------------------------------------------------ MoE grouped block-128 GEMM
+// Expert e owns activation rows [off_e, off_e + M_e) of a [M_total, K] and weights
+// b[e] = [N, K] (memory [E][N][K]); scales are fp32, [M_total, K/128] per row and
+// 128-K block for the activations, [E][N/128][K/128] for the weights. Each workgroup
+// takes one 128 x 128 tile of one expert: the launch is an upper bound on the tile
+// count (no host synchronisation), workgroups past the real count exit at once.
+struct GroupedBlockArgs {
+  const uint8_t* a;
+  const uint8_t* b;
+  const float* sa;
+  const float* sb;
+  void* out;
+  int out_dtype;
+  const int32_t* problem_sizes;   // [E, 3]: M_e, N_e, K_e
+  const int32_t* expert_offsets;  // [E]: first row of expert e
+  int num_experts;
+  int64_t m_total, n, k;
+};
+
+// Expert e's problem, clamped to what the operands hold (rows past M_total, N_e > n,
+// K_e > k), so device-side metadata can never address outside the tensors.
+struct ExpertProblem {
+  int64_t off, m, n, k;
+};
+__device__ inline ExpertProblem expert_problem(const GroupedBlockArgs& ga, int e) {
+  ExpertProblem p;
+  const int64_t off = ga.expert_offsets[e];
+  p.off = off < 0 ? 0 : (off > ga.m_total ? ga.m_total : off);
+  const int64_t m = ga.problem_sizes[3 * e], n = ga.problem_sizes[3 * e + 1], k = ga.problem_sizes[3 * e + 2];
+  p.m = m < 0 ? 0 : (m > ga.m_total - p.off ? ga.m_total - p.off : m);
+  p.n = n < 0 ? 0 : (n > ga.n ? ga.n : n);
+  p.k = k < 0 ? 0 : ((k > ga.k ? ga.k : k) / 128) * 128;  // whole 128-K blocks, as the reference's K // 128
+  return p;
+}
+__device__ inline int64_t expert_tiles(const ExpertProblem& p) { return cdiv(p.m, kBlkTile) * cdiv(p.n, kBlkTile); }
+
+__global__ __launch_bounds__(kBlkThreads, 1) void fp8_grouped_block_kernel(GroupedBlockArgs ga) {
+  AYK_BLOCK_LDS;
+  // Locate this workgroup's expert: lane l sums the tiles of experts [l * per, l * per
+  // + per), a wave scan turns the sums into prefixes, the first lane whose inclusive
+  // prefix passes the tile index owns the expert, and that lane's range is walked.
+  const int lane = threadIdx.x & 63;
+  const int E = ga.num_experts, per = (E + 63) / 64;
+  const int64_t pid = blockIdx.x;
+  int64_t mine = 0;
+  for (int i = 0; i < per; ++i) {
+    const int e = lane * per + i;
+    if (e < E) mine += expert_tiles(expert_problem(ga, e));
+  }
+  int64_t incl = mine;
+#pragma unroll
+  for (int d = 1; d < 64; d <<= 1) {
+    const int64_t v = __shfl_up(incl, d, 64);
+    if (lane >= d) incl += v;
+  }
+  const uint64_t owners = __ballot(incl > pid);
+  if (owners == 0) return;  // past the real tile count (uniform: the ballot is)
+  const int owner = __ffsll((unsigned long long)owners) - 1;
+  int64_t start = __shfl(incl - mine, owner, 64);
+  int e = owner * per;
+  ExpertProblem p = expert_problem(ga, e);
+  for (int64_t t = expert_tiles(p); pid >= start + t; t = expert_tiles(p)) {
+    start += t;
+    p = expert_problem(ga, ++e);
+  }
+  const int64_t local = pid - start;
+  const int64_t tiles_m = cdiv(p.m, kBlkTile);
+  const int tm = (int)(local % tiles_m), tn = (int)(local / tiles_m);
+  const int64_t kb_total = ga.k / 128;
+  const int eb = ga.out_dtype == AYK_F32 ? 4 : 2;
+  if (p.k == 0) {  // no whole 128-K block: the sum is empty, the tile is zeros
+    for (int idx = threadIdx.x; idx < kBlkTile * kBlkTile; idx += kBlkThreads) {
+      const int64_t gm = (int64_t)tm * kBlkTile + idx / kBlkTile, gn = (int64_t)tn * kBlkTile + idx % kBlkTile;
+      if (gm < p.m && gn < p.n) store_f32(ga.out, ga.out_dtype, (p.off + gm) * ga.n + gn, 0.0f);
+    }
+    return;
+  }
+  GemmArgs g{};
+  g.a = ga.a + p.off * ga.k;
+  g.lda = ga.k;
+  g.w = ga.b + (int64_t)e * ga.n * ga.k;
+  g.ldw = ga.k;
+  g.M = p.m;
+  g.N = p.n;
+  g.K = p.k;
+  g.sa = ga.sa + p.off * kb_total;
+  g.sa_dtype = AYK_F32;
+  g.sb = ga.sb + (int64_t)e * (ga.n / 128) * kb_total;
+  g.sb_dtype = AYK_F32;
+  g.out = static_cast<uint8_t*>(ga.out) + p.off * ga.n * eb;
+  g.out_dtype = ga.out_dtype;
+  g.ldo = ga.n;
+  g.tiles_m = (int)tiles_m;
+  block_gemm_tile(g, tm, tn, L0, L1, L2, L3);
 }
 
 // MXFP8 large-tile kernel with 128-K stages: two 64 KB LDS stages, one code dword (four
@@ -1473,6 +1579,46 @@ int ayk_fp8_blockwise_mm(const void* a, int64_t lda, const void* b, int64_t ldb,
   g.bias = bias; g.bias_dtype = bias_dtype;
   g.out = out; g.out_dtype = out_dtype; g.ldo = ldo;
   return launch_gemm<MODE_BLOCK>(g, static_cast<hipStream_t>(stream), op);
+}
+
+int ayk_fp8_grouped_blockwise_mm(const void* a, const void* b, const float* scales_a, const float* scales_b,
+                                 const int32_t* problem_sizes, const int32_t* expert_offsets, int64_t num_experts,
+                                 int64_t m_total, int64_t n, int64_t k, void* out, int out_dtype,
+                                 ayk_stream_t stream) {
+  const char* op = "fp8_blockwise_scaled_grouped_mm";
+  if (num_experts < 0 || m_total < 0 || n < 0 || k < 0)
+    return fail(AYK_EINVAL, "%s: bad shape experts=%lld M=%lld N=%lld K=%lld", op, (long long)num_experts,
+                (long long)m_total, (long long)n, (long long)k);
+  if (n % 128 || k % 128) return fail(AYK_EINVAL, "%s: N and K must be multiples of 128", op);
+  if (out_dtype != AYK_BF16 && out_dtype != AYK_F16) return fail(AYK_EINVAL, "%s: output must be bfloat16 or half", op);
+  if (num_experts > (1 << 20)) return fail(AYK_EINVAL, "%s: too many experts", op);
+  if (num_experts == 0 || m_total == 0 || n == 0 || k == 0) return AYK_OK;
+  if (!a || !b || !scales_a || !scales_b || !problem_sizes || !expert_offsets || !out)
+    return fail(AYK_EINVAL, "%s: missing operand", op);
+  if (!aligned16(a) || !aligned16(b) || !aligned16(out) || (reinterpret_cast<uintptr_t>(scales_a) & 3) ||
+      (reinterpret_cast<uintptr_t>(scales_b) & 3))
+    return fail(AYK_EINVAL, "%s: operands must be 16-byte aligned (scales 4-byte)", op);
+  if (k > 0x7FFFFFFF || n * k > ((int64_t)1 << 31)) return fail(AYK_EINVAL, "%s: expert weight too large", op);
+  // Upper bound on the tiles: every expert adds at most one partial M tile.
+  const int64_t bound = (cdiv(m_total, kBlkTile) + num_experts) * cdiv(n, kBlkTile);
+  if (bound > 0x7FFFFFFF) return fail(AYK_EINVAL, "%s: problem too large", op);
+  if (int rc = check_device()) return rc;
+  GroupedBlockArgs ga{};
+  ga.a = static_cast<const uint8_t*>(a);
+  ga.b = static_cast<const uint8_t*>(b);
+  ga.sa = scales_a;
+  ga.sb = scales_b;
+  ga.out = out;
+  ga.out_dtype = out_dtype;
+  ga.problem_sizes = problem_sizes;
+  ga.expert_offsets = expert_offsets;
+  ga.num_experts = (int)num_experts;
+  ga.m_total = m_total;
+  ga.n = n;
+  ga.k = k;
+  hipLaunchKernelGGL(fp8_grouped_block_kernel, dim3((unsigned)bound), dim3(kBlkThreads), 0,
+                     static_cast<hipStream_t>(stream), ga);
+  return check_launch(op);
 }
 
 int ayk_mxfp8_scaled_mm(const void* a, int64_t lda, const uint8_t* a_scale, int64_t ld_as,

@@ -184,6 +184,56 @@ def _bench_gemm(device, reps=20, warmup=5):
     return results
 
 
+def _bench_moe(device, reps=10, warmup=3):
+    """MoE FP8 block-128 grouped GEMM at the DeepSeek-V3 MoE gate_up shape: 256 experts,
+    4096 tokens routed top-8 (32768 rows, per-expert counts from a seeded multinomial),
+    N = 2 x 2048, K = 7168. Useful FLOPs: 2 x rows x N x K."""
+    from ayaka.kernel.hip import fp8_blockwise_scaled_grouped_mm
+
+    g = torch.Generator(device="cpu").manual_seed(0)
+    experts, tokens, topk, n, k = 256, 4096, 8, 4096, 7168
+    counts = torch.bincount(torch.multinomial(torch.ones(experts), tokens * topk, replacement=True, generator=g),
+                            minlength=experts)
+    rows = int(counts.sum())
+    offsets = torch.cat([torch.zeros(1, dtype=torch.int64), counts.cumsum(0)[:-1]]).to(torch.int32)
+    ps = torch.stack([counts, torch.full_like(counts, n), torch.full_like(counts, k)], 1).to(torch.int32)
+    gd = torch.Generator(device=device).manual_seed(1)
+    fp8 = torch.float8_e4m3fn
+    a = (torch.randn(rows, k, generator=gd, device=device) * 50).clamp(-448, 448).to(fp8)
+    b = torch.empty(experts, n, k, dtype=fp8, device=device)
+    for e0 in range(0, experts, 32):  # in slices: a full fp32 staging tensor would be 30 GB
+        b[e0:e0 + 32] = (torch.randn(32, n, k, generator=gd, device=device) * 50).clamp(-448, 448).to(fp8)
+    sa = torch.rand(rows, k // 128, generator=gd, device=device) * 1e-3
+    sb = torch.rand(experts, n // 128, k // 128, generator=gd, device=device) * 1e-3
+    out = torch.empty(rows, n, dtype=torch.bfloat16, device=device)
+    i64 = lambda: torch.empty(experts, dtype=torch.int64, device=device)  # noqa: E731
+    ptrs = [i64() for _ in range(5)]
+    strides = [torch.full((experts,), v, dtype=torch.int64, device=device) for v in (k, k, n)]
+    lay = [torch.empty(experts, 5, dtype=torch.int32, device=device) for _ in range(2)]
+    ps_d, off_d = ps.to(device), offsets.to(device)
+    ws = torch.empty(1, dtype=torch.uint8, device=device)
+
+    def run():
+        fp8_blockwise_scaled_grouped_mm(out, *ptrs, a, b, sa, sb, *strides, *lay, ps_d, off_d, ws)
+
+    for _ in range(warmup):
+        run()
+    torch.cuda.synchronize()
+    start, end = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+    start.record()
+    for _ in range(reps):
+        run()
+    end.record()
+    torch.cuda.synchronize()
+    ms = start.elapsed_time(end) / reps
+    tflops = 2.0 * rows * n * k / (ms * 1e-3) / 1e12
+    result = {"experts": experts, "rows": rows, "N": n, "K": k, "max_rows_per_expert": int(counts.max()),
+              "ms": round(ms, 4), "tflops": round(tflops, 1), "frac": round(tflops / FP8_PEAK_TFLOPS, 4)}
+    del a, b, out
+    torch.cuda.empty_cache()
+    return result
+
+
 def _time_rotated(fns, reps: int, warmup: int) -> float:
     """Average ms per call over `reps` calls cycling through `fns` (input copies whose
     total exceeds the 256 MB Infinity Cache, so each call streams from HBM)."""
@@ -437,6 +487,7 @@ def main() -> int:
     result["decode_w8a16"] = _bench_decode_m(layers)
     if not args.no_gemm:
         result["gemm"] = _bench_gemm(device)
+        result["moe_grouped_block128"] = _bench_moe(device)
     result["quant"] = _bench_quant(device)
     result["kv_cache"] = _bench_kv_cache(device)
     if not args.no_cpu:

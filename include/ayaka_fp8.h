@@ -122,6 +122,20 @@ int ayk_fp8_blockwise_mm(const void* a, int64_t lda, const void* b, int64_t ldb,
                          const void* bias, int bias_dtype,
                          void* out, int out_dtype, int64_t ldo, ayk_stream_t stream);
 
+/* Replaces fp8_blockwise_scaled_grouped_mm (kernel/triton/moe/moe_grouped_gemm.py:599,
+ * kernel :472-585): the MoE grouped block-128 GEMM. Expert e computes rows
+ * [expert_offsets[e], + problem_sizes[e][0]) of out:
+ *   out[m, n] = sum_kb scales_a[m, kb] * scales_b[e][n / 128][kb] * (a[m, kb] . b[e][n, kb])
+ * with a [m_total, k] e4m3, b memory [E][n][k] e4m3, scales_a [m_total, k/128] fp32,
+ * scales_b [E][n/128][k/128] fp32, out [m_total, n] bf16/fp16 (row stride n); rows of no
+ * expert are not written. problem_sizes [E, 3] int32 (M_e, N_e, K_e) and expert_offsets
+ * [E] int32 are read on the device (clamped to the operands). n % 128 == 0,
+ * k % 128 == 0, 16-byte aligned a/b/out. */
+int ayk_fp8_grouped_blockwise_mm(const void* a, const void* b, const float* scales_a, const float* scales_b,
+                                 const int32_t* problem_sizes, const int32_t* expert_offsets, int64_t num_experts,
+                                 int64_t m_total, int64_t n, int64_t k, void* out, int out_dtype,
+                                 ayk_stream_t stream);
+
 /* Replaces ayaka::mxfp8_scaled_mm (gemm/fp8_mxfp8_gemm.py:163; oracle reference/gemm.py:73-92).
  * out = sum_g (a[:, g] @ w[:, g]^T) * 2^(a_scale[m,g]-127) * 2^(w_scale[n,g]-127) + bias
  * over 32-wide K groups g; UE8M0 code 0 decodes to 0 and 0xFF to NaN.

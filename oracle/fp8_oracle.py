@@ -142,6 +142,32 @@ def fp8_blockwise_mm(a, b, scale_a, scale_b, bias=None, a_scale_col_major: bool 
     return y
 
 
+def grouped_blockwise_mm(a, b, scales_a, scales_b, problem_sizes, expert_offsets, out) -> torch.Tensor:
+    """MoE grouped block-128 GEMM (reference kernel/triton/moe/moe_grouped_gemm.py:472-585,
+    the non-swapped operand convention): for expert e with rows [off_e, off_e + M_e),
+    ``out[rows, :N_e] = fp8_blockwise_mm(a[rows, :K_e], b[e, :N_e, :K_e], sa_e, sb_e)``
+    rounded once to ``out``'s dtype, rows of no expert keeping ``out``'s values. ``b`` is
+    [E, N, K]. The scale operands are addressed as the reference's pointer tables do
+    (:85-101, :564-573): ``sa_e`` starts at element ``off_e * (K / 128)`` of ``scales_a``
+    and ``sb_e`` at ``e * (N / 128) * (K / 128)`` of ``scales_b``, both with row stride
+    ``K_e // 128`` (the same as slicing when K_e == K). Returns the updated copy of ``out``."""
+    res = out.clone()
+    k_all, n_all = a.shape[1], b.shape[1]
+    sa_flat, sb_flat = scales_a.reshape(-1), scales_b.reshape(-1)
+    for e in range(expert_offsets.numel()):
+        m_e, n_e, k_e = (int(v) for v in problem_sizes[e])
+        off = int(expert_offsets[e])
+        if m_e <= 0 or n_e <= 0:
+            continue
+        kb, nb = k_e // SCALE_BLOCK, -(-n_e // SCALE_BLOCK)
+        sa0, sb0 = off * (k_all // SCALE_BLOCK), e * (n_all // SCALE_BLOCK) * (k_all // SCALE_BLOCK)
+        sa_e = sa_flat[sa0:sa0 + m_e * kb].reshape(m_e, kb)
+        sb_e = sb_flat[sb0:sb0 + nb * kb].reshape(nb, kb)
+        y = fp8_blockwise_mm(a[off:off + m_e, :k_e], b[e, :n_e, :k_e], sa_e, sb_e)
+        res[off:off + m_e, :n_e] = y.to(res.dtype)
+    return res
+
+
 def mxfp8_scaled_mm(a, a_scale, b, b_scale, bias=None) -> torch.Tensor:
     """e4m3 operands with UE8M0 1x32 scales folded in, fp32 (reference gemm.py:73-92)."""
     k = a.shape[1]

@@ -383,3 +383,38 @@ def test_kv_write_scales_skips_negative_slots_and_gathers_back():
     assert big.flatten().float().tolist() == [448.0, -448.0]  # clamped, not NaN
     back = ora.kv_gather(cache, torch.tensor([3, 3, 0]), torch.float32, 0.5, True)
     assert back.reshape(3, 2).tolist() == [[1.0, -2.0], [1.0, -2.0], [7.0, 8.0]]
+
+
+def test_grouped_blockwise_mm_brute_force_and_expert_order():
+    """The grouped oracle against a scalar fp64 sum written from the operator's formula
+    out[m, n] = sum_kb sa[m, kb] * sb[e][n // 128][kb] * sum_{k in kb} a[m, k] b[e, n, k]
+    on uneven experts (one empty, rows of no expert left alone), and invariance under a
+    reordering of the experts' row ranges."""
+    g = torch.Generator().manual_seed(21)
+    E, n, k = 3, 128, 256
+    counts, offsets = [2, 0, 2], [0, 2, 3]  # rows 2 and 5 belong to no expert
+    m_total = 6
+    a = (torch.randn(m_total, k, generator=g) * 40).clamp(-448, 448).to(ora.E4M3)
+    b = (torch.randn(E, n, k, generator=g) * 40).clamp(-448, 448).to(ora.E4M3)
+    sa = torch.rand(m_total, k // 128, generator=g) + 0.5
+    sb = torch.rand(E, n // 128, k // 128, generator=g) + 0.5
+    ps = torch.tensor([[c, n, k] for c in counts], dtype=torch.int32)
+    off = torch.tensor(offsets, dtype=torch.int32)
+    out = torch.full((m_total, n), 7.0)
+    got = ora.grouped_blockwise_mm(a, b, sa, sb, ps, off, out)
+    af, bf = a.double().tolist(), b.double().tolist()
+    for e, (c, o) in enumerate(zip(counts, offsets)):
+        for m in range(o, o + c):
+            for col in range(0, n, 37):  # a spread of columns keeps the loop short
+                want = 0.0
+                for kb in range(k // 128):
+                    dot = sum(af[m][kk] * bf[e][col][kk] for kk in range(kb * 128, kb * 128 + 128))
+                    want += float(sa[m, kb]) * float(sb[e, col // 128, kb]) * dot
+                assert abs(float(got[m, col]) - want) <= 1e-5 * abs(want) + 1e-3, (e, m, col)
+    assert torch.equal(got[2], out[2]) and torch.equal(got[5], out[5])
+    # experts laid out in the opposite row order give the same rows
+    perm_off = torch.tensor([4, 6, 0], dtype=torch.int32)
+    a2 = torch.cat([a[3:5], a[2:3], a[5:6], a[0:2]])  # rows: e2 at 0..1, e0 at 4..5
+    sa2 = torch.cat([sa[3:5], sa[2:3], sa[5:6], sa[0:2]])
+    got2 = ora.grouped_blockwise_mm(a2, b, sa2, sb, ps, perm_off, torch.zeros(6, n))
+    assert torch.equal(got2[4:6], got[0:2]) and torch.equal(got2[0:2], got[3:5])
