@@ -228,6 +228,35 @@ __device__ inline uint32_t e5m2x4_encode(float a, float b, float c, float d) {
   return w;
 }
 
+// x / s for many x and one s: the correctly rounded quotient from a reciprocal computed
+// once, by Markstein's correction (P. W. Markstein, "Computation of elementary functions
+// on the IBM RISC System/6000 processor", IBM J. Res. Dev. 34(1), 1990; Muller et al.,
+// Handbook of Floating-Point Arithmetic, "Markstein's theorem"): with r = RN(1/s),
+// q0 = RN(x r) is within one ulp of x/s, the residual x - s q0 is exact under an FMA,
+// and RN(q0 + residual r) = RN(x / s) when nothing underflows. Used only when s and r
+// are both normal; q0 itself is returned when it is zero (keeping the sign of a zero x)
+// or not finite (x infinite or NaN). For subnormal x the last bit can differ from the
+// IEEE quotient, whose magnitude is then below 2^-100 and below every fp8 code.
+struct Divisor {
+  float s, r;
+  bool fast;
+};
+__device__ inline Divisor make_divisor(float s) {
+  Divisor d;
+  d.s = s;
+  d.r = 1.0f / s;
+  const float as = fabsf(s), ar = fabsf(d.r);
+  d.fast = as >= 1.17549435e-38f && as <= 3.40282347e38f && ar >= 1.17549435e-38f && ar <= 3.40282347e38f;
+  return d;
+}
+// The quotient of a fast divisor (d.fast), without the IEEE fallback.
+__device__ inline float divide_fast(const Divisor& d, float x) {
+  const float q0 = x * d.r;
+  const float q = fmaf(fmaf(-d.s, q0, x), d.r, q0);
+  return (q0 == 0.0f || !(fabsf(q0) <= 3.40282347e38f)) ? q0 : q;
+}
+__device__ inline float divide(const Divisor& d, float x) { return d.fast ? divide_fast(d, x) : x / d.s; }
+
 // NaN-propagating max of magnitudes, the semantics of torch's amax.
 __device__ inline float nanmax(float a, float b) { return (a > b || a != a) ? a : b; }
 

@@ -55,13 +55,19 @@ __device__ inline float absmax_n(const float* f, float m) {
   return m;
 }
 
-// Quantize N floats with scale s (q = e4m3(clamp(f / s))) and store N bytes.
+// Quantize N floats with scale d.s (q = e4m3(clamp(f / s)), f / s correctly rounded)
+// and store N bytes.
 template <int N>
-__device__ inline void store_quant(uint8_t* dst, const float* f, float s) {
+__device__ inline void store_quant(uint8_t* dst, const float* f, const Divisor& d) {
   static_assert(N % 4 == 0, "16-byte vectors hold 4 or 8 elements");
   float q[N];
+  if (d.fast) {  // per row or group; a wavefront whose lanes agree runs one path
 #pragma unroll
-  for (int i = 0; i < N; ++i) q[i] = clamp_e4m3(f[i] / s);
+    for (int i = 0; i < N; ++i) q[i] = clamp_e4m3(divide_fast(d, f[i]));
+  } else {
+#pragma unroll
+    for (int i = 0; i < N; ++i) q[i] = clamp_e4m3(f[i] / d.s);
+  }
   uint32_t w[N / 4];
 #pragma unroll
   for (int i = 0; i < N / 4; ++i) w[i] = e4m3x4_encode(q[4 * i], q[4 * i + 1], q[4 * i + 2], q[4 * i + 3]);
@@ -119,12 +125,13 @@ __global__ __launch_bounds__(kQuantThreads) void per_token_quant_vec_kernel(
     amax = floor_amax(block_max256(amax, red));
     const float s = amax / kE4M3Max;
     if (threadIdx.x == 0) scale[row] = s;
+    const Divisor dv = make_divisor(s);
 #pragma unroll
     for (int i = 0; i < VPT; ++i) {
       const int64_t v = threadIdx.x + (int64_t)i * kQuantThreads;
       if (v < nvec) {
         unpack16<T>(cache[i], f);
-        store_quant<V>(qr + v * V, f, s);
+        store_quant<V>(qr + v * V, f, dv);
       }
     }
   } else {
@@ -135,9 +142,53 @@ __global__ __launch_bounds__(kQuantThreads) void per_token_quant_vec_kernel(
     amax = floor_amax(block_max256(amax, red));
     const float s = amax / kE4M3Max;
     if (threadIdx.x == 0) scale[row] = s;
+    const Divisor dv = make_divisor(s);
     for (int64_t v = threadIdx.x; v < nvec; v += kQuantThreads) {
       unpack16<T>(xr[v], f);
-      store_quant<V>(qr + v * V, f, s);
+      store_quant<V>(qr + v * V, f, dv);
+    }
+  }
+}
+
+// One wavefront per row (kQuantThreads / 64 rows per workgroup) for rows of at most
+// 64 VPT vectors: lane l keeps vectors l, l + 64, ... in registers, the amax is a wave
+// reduction, and no workgroup barrier separates a row's read from its store.
+template <typename T, int VPT>
+__global__ __launch_bounds__(kQuantThreads) void per_token_quant_wave_kernel(
+    const typename T::storage* __restrict__ x, int64_t rows, int64_t k, int64_t ldx,
+    uint8_t* __restrict__ q, int64_t ldq, float* __restrict__ scale) {
+  constexpr int V = Vec16<T>::N;
+  const int lane = threadIdx.x & (kWave - 1);
+  const int64_t row = (int64_t)blockIdx.x * (kQuantThreads / kWave) + (threadIdx.x / kWave);
+  if (row >= rows) return;  // the whole wavefront leaves together
+  const int64_t nvec = k / V;
+  const uint4* xr = reinterpret_cast<const uint4*>(x + row * ldx);
+  uint8_t* qr = q + row * ldq;
+  uint4 cache[VPT];
+#pragma unroll
+  for (int i = 0; i < VPT; ++i) {
+    const int64_t v = lane + (int64_t)i * kWave;
+    if (v < nvec) cache[i] = xr[v];
+  }
+  float f[V];
+  float amax = 0.0f;
+#pragma unroll
+  for (int i = 0; i < VPT; ++i) {
+    if (lane + (int64_t)i * kWave < nvec) {
+      unpack16<T>(cache[i], f);
+      amax = absmax_n<V>(f, amax);
+    }
+  }
+  amax = floor_amax(wave_max<kWave>(amax));
+  const float sc = amax / kE4M3Max;
+  if (lane == 0) scale[row] = sc;
+  const Divisor dv = make_divisor(sc);
+#pragma unroll
+  for (int i = 0; i < VPT; ++i) {
+    const int64_t v = lane + (int64_t)i * kWave;
+    if (v < nvec) {
+      unpack16<T>(cache[i], f);
+      store_quant<V>(qr + v * V, f, dv);
     }
   }
 }
@@ -171,12 +222,24 @@ struct MxScale {
   uint8_t code;  // 0 for an all-zero group, else e + 127
   bool zero;
 };
+// The ceiling read from the bits of ratio = 2^k (1 + M / 2^23): an exact power of two
+// (M == 0) gives k. For M >= 64, log2(1 + M / 2^23) >= 1.1e-5 exceeds half an fp32 ulp
+// of every integer |k| <= 127 (at most 2^-18), so the rounded log2 lies above k and the
+// ceiling is k + 1. A subnormal ratio (at least 1e-38, below 2^-126) has its log2 in
+// (-126.2, -126): the clamped result is -126. Only 1 <= M < 64, and NaN or infinity,
+// evaluate the rounded log2.
+__device__ inline float mx_ceil_log2(float ratio) {
+  const uint32_t b = f2u(ratio);
+  const uint32_t ef = (b >> 23) & 0xFFu, m = b & 0x7FFFFFu;
+  if (ef == 0u) return -126.0f;
+  if (ef != 0xFFu && (m == 0u || m >= 64u)) return (float)((int)ef - 127 + (m != 0u ? 1 : 0));
+  return ceilf((float)log2((double)ratio));
+}
 __device__ inline MxScale mx_scale(float amax) {
   MxScale r;
   float ratio = amax / kE4M3Max;
   ratio = ratio < 1e-38f ? 1e-38f : ratio;
-  const float l = (float)log2((double)ratio);
-  float e = ceilf(l);
+  float e = mx_ceil_log2(ratio);
   e = e < -126.0f ? -126.0f : (e > 127.0f ? 127.0f : e);
   const int ei = (int)e;
   r.zero = (amax == 0.0f);
@@ -185,62 +248,81 @@ __device__ inline MxScale mx_scale(float amax) {
   return r;
 }
 
-// GL lanes cooperate on one group; each lane holds VPL 16-byte vectors of it.
+// GL lanes cooperate on one group; each lane holds VPL 16-byte vectors of it. A thread
+// works on kGroupSlots such lane slots, one grid span apart (a multiple of 64 threads,
+// so the GL lanes of a group stay together in one wavefront), with every slot's loads
+// issued before the first reduction.
+constexpr int kGroupSlots = 2;
 template <typename T, int GL, int VPL, bool MX>
 __global__ __launch_bounds__(kQuantThreads) void group_quant_vec_kernel(
     const typename T::storage* __restrict__ x, int64_t rows, int64_t k, int64_t ldx,
     int64_t group, uint8_t* __restrict__ q, int64_t ldq, void* __restrict__ scale_out) {
   constexpr int V = Vec16<T>::N;
   const int64_t gpr = k / group;
-  const int64_t t = (int64_t)blockIdx.x * kQuantThreads + threadIdx.x;
-  const int64_t gi = t / GL;
-  const int lig = (int)(t % GL);
-  const bool live = gi < rows * gpr;
-  const int64_t row = live ? gi / gpr : 0;
-  const int64_t g = live ? gi % gpr : 0;
-  const uint4* xg = reinterpret_cast<const uint4*>(x + row * ldx + g * group);
-  uint8_t* qg = q + row * ldq + g * group;
-  uint4 cache[VPL];
-  float f[V];
-  float amax = 0.0f;
+  const int64_t span = (int64_t)gridDim.x * kQuantThreads;
+  uint4 cache[kGroupSlots][VPL];
+  int64_t row[kGroupSlots], g[kGroupSlots];
+  bool live[kGroupSlots];
+  const int lig = (int)(((int64_t)blockIdx.x * kQuantThreads + threadIdx.x) % GL);
 #pragma unroll
-  for (int j = 0; j < VPL; ++j) {
-    if (live) {
-      cache[j] = xg[lig + j * GL];
-      unpack16<T>(cache[j], f);
-      amax = absmax_n<V>(f, amax);
+  for (int u = 0; u < kGroupSlots; ++u) {
+    const int64_t t = (int64_t)blockIdx.x * kQuantThreads + threadIdx.x + u * span;
+    const int64_t gi = t / GL;
+    live[u] = gi < rows * gpr;
+    row[u] = live[u] ? gi / gpr : 0;
+    g[u] = live[u] ? gi % gpr : 0;
+    const uint4* xg = reinterpret_cast<const uint4*>(x + row[u] * ldx + g[u] * group);
+#pragma unroll
+    for (int j = 0; j < VPL; ++j) {
+      if (live[u]) cache[u][j] = xg[lig + j * GL];
     }
   }
-  amax = wave_max<GL>(amax);  // every lane of the group takes part (GL divides 64)
-  if (!live) return;
-  if constexpr (MX) {
-    const MxScale ms = mx_scale(amax);
-    if (lig == 0) reinterpret_cast<uint8_t*>(scale_out)[row * gpr + g] = ms.code;
+  float f[V];
+#pragma unroll
+  for (int u = 0; u < kGroupSlots; ++u) {
+    float amax = 0.0f;
 #pragma unroll
     for (int j = 0; j < VPL; ++j) {
-      unpack16<T>(cache[j], f);
-      uint32_t w[V / 4] = {};
-      if (!ms.zero) {
-        float q[V];
-#pragma unroll
-        for (int i = 0; i < V; ++i) q[i] = clamp_e4m3(f[i] * ms.inv);
-#pragma unroll
-        for (int i = 0; i < V / 4; ++i) w[i] = e4m3x4_encode(q[4 * i], q[4 * i + 1], q[4 * i + 2], q[4 * i + 3]);
-      }
-      uint8_t* dst = qg + (int64_t)(lig + j * GL) * V;
-      if constexpr (V == 8) {
-        *reinterpret_cast<uint2*>(dst) = make_uint2(w[0], w[1]);
-      } else {
-        *reinterpret_cast<uint32_t*>(dst) = w[0];
+      if (live[u]) {
+        unpack16<T>(cache[u][j], f);
+        amax = absmax_n<V>(f, amax);
       }
     }
-  } else {
-    const float s = floor_amax(amax) / kE4M3Max;
-    if (lig == 0) reinterpret_cast<float*>(scale_out)[row * gpr + g] = s;
+    amax = wave_max<GL>(amax);  // every lane of the group takes part (GL divides 64)
+    if (!live[u]) continue;
+    uint8_t* qg = q + row[u] * ldq + g[u] * group;
+    if constexpr (MX) {
+      const MxScale ms = mx_scale(amax);
+      if (lig == 0) reinterpret_cast<uint8_t*>(scale_out)[row[u] * gpr + g[u]] = ms.code;
 #pragma unroll
-    for (int j = 0; j < VPL; ++j) {
-      unpack16<T>(cache[j], f);
-      store_quant<V>(qg + (int64_t)(lig + j * GL) * V, f, s);
+      for (int j = 0; j < VPL; ++j) {
+        unpack16<T>(cache[u][j], f);
+        uint32_t w[V / 4] = {};
+        if (!ms.zero) {
+          float qv[V];
+#pragma unroll
+          for (int i = 0; i < V; ++i) qv[i] = clamp_e4m3(f[i] * ms.inv);
+#pragma unroll
+          for (int i = 0; i < V / 4; ++i) w[i] = e4m3x4_encode(qv[4 * i], qv[4 * i + 1], qv[4 * i + 2], qv[4 * i + 3]);
+        }
+        uint8_t* dst = qg + (int64_t)(lig + j * GL) * V;
+        if constexpr (V == 8) {
+          *reinterpret_cast<uint2*>(dst) = make_uint2(w[0], w[1]);
+        } else {
+          *reinterpret_cast<uint32_t*>(dst) = w[0];
+        }
+      }
+    } else {
+      const float sc = floor_amax(amax) / kE4M3Max;
+      if (lig == 0) reinterpret_cast<float*>(scale_out)[row[u] * gpr + g[u]] = sc;
+      // IEEE division here: with one scale per 8-16 lanes the reciprocal form measured
+      // slower (37 against 28 us at DSv3 K = 7168), unlike the per-row kernels.
+      const Divisor dv{sc, 0.0f, false};
+#pragma unroll
+      for (int j = 0; j < VPL; ++j) {
+        unpack16<T>(cache[u][j], f);
+        store_quant<V>(qg + (int64_t)(lig + j * GL) * V, f, dv);
+      }
     }
   }
 }
@@ -289,12 +371,22 @@ __global__ __launch_bounds__(kQuantThreads) void static_quant_vec_kernel(
     int scale_dtype, uint8_t* __restrict__ q) {
   constexpr int V = Vec16<T>::N;
   const float s = load_f32(scale, scale_dtype, 0);
+  const Divisor dv = make_divisor(s);
   const uint4* xv = reinterpret_cast<const uint4*>(x);
   const int64_t stride = (int64_t)gridDim.x * kQuantThreads;
   float f[V];
-  for (int64_t v = (int64_t)blockIdx.x * kQuantThreads + threadIdx.x; v < nvec; v += stride) {
-    unpack16<T>(xv[v], f);
-    store_quant<V>(q + v * V, f, s);
+  // Two vectors in flight per thread: both loads are issued before either is converted.
+  for (int64_t v = (int64_t)blockIdx.x * kQuantThreads + threadIdx.x; v < nvec; v += 2 * stride) {
+    const bool second = v + stride < nvec;
+    const uint4 a = xv[v];
+    uint4 b{};
+    if (second) b = xv[v + stride];
+    unpack16<T>(a, f);
+    store_quant<V>(q + v * V, f, dv);
+    if (second) {
+      unpack16<T>(b, f);
+      store_quant<V>(q + (v + stride) * V, f, dv);
+    }
   }
 }
 
@@ -311,6 +403,19 @@ int launch_per_token(const void* x, int64_t rows, int64_t k, int64_t ldx, void* 
   const dim3 grid((unsigned)rows), block(kQuantThreads);
   if (!vec_ok) {
     hipLaunchKernelGGL(per_token_quant_scalar_kernel<T>, grid, block, 0, st, xs, k, ldx, qb, ldq, scale);
+    return check_launch("per_token_quant_fp8");
+  }
+  const int64_t per_lane = cdiv(k / V, kWave);
+  if (per_lane <= 16) {
+    const dim3 wgrid((unsigned)cdiv(rows, kQuantThreads / kWave));
+#define AYK_PW(VPT) \
+  hipLaunchKernelGGL((per_token_quant_wave_kernel<T, VPT>), wgrid, block, 0, st, xs, rows, k, ldx, qb, ldq, scale)
+    if (per_lane <= 1) AYK_PW(1);
+    else if (per_lane <= 2) AYK_PW(2);
+    else if (per_lane <= 4) AYK_PW(4);
+    else if (per_lane <= 8) AYK_PW(8);
+    else AYK_PW(16);
+#undef AYK_PW
     return check_launch("per_token_quant_fp8");
   }
   const int64_t per_thread = cdiv(k / V, kQuantThreads);
@@ -346,7 +451,7 @@ int launch_group(const void* x, int64_t rows, int64_t k, int64_t ldx, int64_t gr
   }
   const int gl = (int)(vecs < 64 ? vecs : 64);
   const int vpl = (int)(vecs / gl);
-  const dim3 grid((unsigned)cdiv(groups * gl, kQuantThreads)), block(kQuantThreads);
+  const dim3 grid((unsigned)cdiv(groups * gl, (int64_t)kQuantThreads * kGroupSlots)), block(kQuantThreads);
 #define AYK_GQ(GL, VPL)                                                                          \
   hipLaunchKernelGGL((group_quant_vec_kernel<T, GL, VPL, MX>), grid, block, 0, st, xs, rows, k, \
                      ldx, group, qb, ldq, scale)

@@ -105,12 +105,13 @@ def test_mx_quant_bit_exact(gpu, dtype, m, k, group):
 
 
 def test_mx_quant_exponent_boundaries(gpu):
-    """Groups whose amax / 448 sits on and just above every power of two."""
+    """Groups whose amax / 448 sits on and up to 129 ulps above every power of two."""
     from ayaka.kernel.hip import per_token_group_quant_mxfp8
 
     _say("per_token_group_quant_mxfp8 exponent boundaries")
     ks = torch.arange(-133, 121, dtype=torch.float64)
-    ns = torch.tensor([0, 1, 2, 3, 5, 8, 13, 21, 40, 64], dtype=torch.float64)
+    # every mantissa offset up to 129 (the bit-level exponent path starts at 64) and a few large ones
+    ns = torch.cat([torch.arange(130, dtype=torch.float64), torch.tensor([1000.0, 2.0**22, 2.0**23 - 1])])
     amax = (448.0 * torch.exp2(ks)[:, None] * (1 + ns[None, :] * 2.0**-23)).reshape(-1).float()
     amax = amax[torch.isfinite(amax) & (amax > 0)]
     rows = amax.numel()
@@ -162,22 +163,24 @@ def test_encode_every_fp32_neighbourhood(gpu):
     assert torch.equal(qb[~nan_r], rb[~nan_r])
 
 
-def test_static_quant_every_fp32_pattern(gpu):
-    """All 2^32 fp32 bit patterns through static quant with scale 1 (x / 1 is x), against
-    torch's clamp + round-to-nearest-even e4m3 cast on the same device, in 2^28 chunks:
-    pins the hardware conversion in the vector store against the cast for every input."""
+@pytest.mark.parametrize("scale", [1.0, 0.3701171875, 7.3e-5])
+def test_static_quant_every_fp32_pattern(gpu, scale):
+    """All 2^32 fp32 bit patterns through static quant, against torch's IEEE division,
+    clamp and round-to-nearest-even e4m3 cast on the same device, in 2^28 chunks. Scale 1
+    pins the hardware conversion for every input; the other scales pin the quotient taken
+    from a reciprocal with Markstein's correction, code for code."""
     from ayaka.kernel.hip import static_quant_fp8
 
     count = 1 << 28
-    one = torch.ones((), dtype=torch.float32, device=gpu)
+    s = torch.tensor(scale, dtype=torch.float32, device=gpu)
     out = torch.empty(count, dtype=torch.float8_e4m3fn, device=gpu)
     for chunk in range(1 << 4):
-        _say(f"static_quant_fp8 fp32 sweep chunk {chunk}")
+        _say(f"static_quant_fp8 fp32 sweep scale={scale} chunk {chunk}")
         start = chunk * count
         start = start - (1 << 32) if start >= (1 << 31) else start
         x = (torch.arange(count, dtype=torch.int32, device=gpu) + start).view(torch.float32)
-        static_quant_fp8(x.view(1 << 14, 1 << 14), one, out=out.view(1 << 14, 1 << 14))
-        ref = x.clamp(-448.0, 448.0).to(torch.float8_e4m3fn)
+        static_quant_fp8(x.view(1 << 14, 1 << 14), s, out=out.view(1 << 14, 1 << 14))
+        ref = (x / s).clamp(-448.0, 448.0).to(torch.float8_e4m3fn)
         bad = int((out.view(torch.uint8) != ref.view(torch.uint8)).sum())
         assert bad == 0, f"{bad} codes differ in chunk {chunk}"
         del x, ref
