@@ -427,7 +427,8 @@ __global__ __launch_bounds__(256) void w8a16_skinny_reduce(SkinnyArgs a, int spl
 }
 
 // Launch plan, a function of the shapes and the scale block width only (the
-// workspace query must reproduce it). The K split is the smallest power of two giving
+// workspace query must reproduce it). Unless the rows alone give >= 768 wavefronts,
+// the K split is the smallest power of two giving
 // >= 1024 wavefronts (each keeps D * 4 KiB of weights in flight); more splits cost
 // more partial-sum traffic than they gain (measured on Llama-3-8B shapes).
 struct SkinnyPlan {
@@ -452,7 +453,10 @@ SkinnyPlan skinny_plan(int64_t M, int64_t N, int64_t K, int64_t bx) {
   };
   const int64_t waves = cdiv(N, 32);
   int64_t split = 1;
-  while (waves * split < 1024 && split * 2 <= units) split *= 2;
+  // A row count that already covers three quarters of the 1024 SIMDs runs unsplit: the
+  // partial sums and the reduce launch cost more than the idle quarter (gate_up at M = 4:
+  // 28 against 31 us).
+  while (waves < 768 && waves * split < 1024 && split * 2 <= units) split *= 2;
   for (;;) {
     const int64_t kps = cdiv(units, split) * unit;
     const size_t lds = lds_for(kps, p.x_pitch, p.s_cols);
