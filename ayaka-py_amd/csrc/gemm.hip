@@ -1223,7 +1223,12 @@ __global__ __launch_bounds__(kBlkThreads, 1) void fp8_grouped_block_kernel(Group
   // prefix passes the tile index owns the expert, and that lane's range is walked.
   const int lane = threadIdx.x & 63;
   const int E = ga.num_experts, per = (E + 63) / 64;
-  const int64_t pid = blockIdx.x;
+  // Workgroup b runs on XCD b % 8. Logical tiles 2x and 2x + 1 of each block of 16 go to
+  // workgroups 8 apart (one XCD, dispatched together): with the row tiles of an expert
+  // enumerated first, an expert's two 128-row tiles of one weight panel then share that
+  // XCD's L2 instead of each reading the panel from HBM. The grid is a multiple of 16.
+  const int64_t b = blockIdx.x;
+  const int64_t pid = (b & ~(int64_t)15) + 2 * (b & 7) + ((b >> 3) & 1);
   int64_t mine = 0;
   for (int i = 0; i < per; ++i) {
     const int e = lane * per + i;
@@ -1600,7 +1605,7 @@ int ayk_fp8_grouped_blockwise_mm(const void* a, const void* b, const float* scal
     return fail(AYK_EINVAL, "%s: operands must be 16-byte aligned (scales 4-byte)", op);
   if (k > 0x7FFFFFFF || n * k > ((int64_t)1 << 31)) return fail(AYK_EINVAL, "%s: expert weight too large", op);
   // Upper bound on the tiles: every expert adds at most one partial M tile.
-  const int64_t bound = (cdiv(m_total, kBlkTile) + num_experts) * cdiv(n, kBlkTile);
+  const int64_t bound = cdiv((cdiv(m_total, kBlkTile) + num_experts) * cdiv(n, kBlkTile), 16) * 16;
   if (bound > 0x7FFFFFFF) return fail(AYK_EINVAL, "%s: problem too large", op);
   if (int rc = check_device()) return rc;
   GroupedBlockArgs ga{};
