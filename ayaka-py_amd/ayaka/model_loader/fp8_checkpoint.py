@@ -34,7 +34,7 @@ import torch
 from torch import nn
 
 from ayaka.exceptions import CheckpointCorruptError, UnsupportedWeightFormatError
-from ayaka.model_loader.fp8 import classify_scale_key, normalize_scale, parse_fp8_config, validate_scale_key_set
+from ayaka.model_loader.fp8 import FP8_SCALE_KEY_SUFFIXES, normalize_scale, parse_fp8_config, validate_scale_key_set
 from ayaka.model_loader.reader import CheckpointReader
 from ayaka.types import DType
 
@@ -125,9 +125,8 @@ def load_fp8_linear(
             raise CheckpointCorruptError(f"{prefix}.weight: input size {entry.shape[1]} differs from {k} of its siblings")
         k = entry.shape[1]
         sizes.append(entry.shape[0])
-        scale_keys = [key for key in reader.keys() if key.startswith(prefix + ".") and classify_scale_key(key)
-                      and key.count(".") == prefix.count(".") + 1]
-        validate_scale_key_set(scale_keys, parsed.recipe.recipe)
+        candidates = (f"{prefix}.{suffix}" for suffixes in FP8_SCALE_KEY_SUFFIXES.values() for suffix in suffixes)
+        validate_scale_key_set([key for key in candidates if key in reader], parsed.recipe.recipe)
 
     layer = nn.Module()
     method.create_weights(layer, output_partition_sizes=sizes, input_size_per_partition=int(k), device=device)

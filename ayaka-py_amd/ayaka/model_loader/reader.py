@@ -157,7 +157,8 @@ class CheckpointReader:
         if raw.device.type == "cpu":
             _read_exact(fd, memoryview(raw.numpy()), entry.byte_offset, key)
             return
-        self._stream_to_device(fd, entry, raw)
+        with torch.cuda.device(raw.device):  # the copies and their events on that device's stream
+            self._stream_to_device(fd, entry, raw)
 
     def _fd(self, file_uri: str) -> int:
         fd = self._fds.get(file_uri)

@@ -306,6 +306,5 @@ inline bool aligned16(const void* p) { return (reinterpret_cast<uintptr_t>(p) & 
 int fail(int status, const char* fmt, ...);
 int check_launch(const char* what);
 int check_device();
-int device_cu_count();
 
 }  // namespace ayk

@@ -53,21 +53,6 @@ int check_device() {
   return AYK_OK;
 }
 
-// Compute units of the current device (cached per device; 256 on MI355X). Persistent
-// kernels launch one workgroup per compute unit.
-static int g_cu_count[64];
-
-int device_cu_count() {
-  int device = 0;
-  if (hipGetDevice(&device) != hipSuccess || device < 0 || device >= 64) return 0;
-  if (g_cu_count[device] <= 0) {
-    int n = 0;
-    if (hipDeviceGetAttribute(&n, hipDeviceAttributeMultiprocessorCount, device) != hipSuccess) return 0;
-    g_cu_count[device] = n;
-  }
-  return g_cu_count[device];
-}
-
 }  // namespace ayk
 
 extern "C" {
