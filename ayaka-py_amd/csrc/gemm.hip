@@ -66,6 +66,9 @@ struct GemmArgs {
   int out_dtype;
   int64_t ldo;
   int tiles_m;     // number of BM tiles along M
+  float* ws;       // split-K partials (block-scaled GEMM), ws_bytes long
+  size_t ws_bytes;
+  int64_t kps;     // general kernel, block mode: K per split (0: no split; blockIdx.y = split)
 };
 
 __device__ inline v16f mfma(const v8i& wa, const v8i& ab, const v16f& c, int sw, int sa) {
@@ -136,8 +139,27 @@ __device__ inline void store4(const GemmArgs& g, int64_t m, int64_t n, const flo
 
 // BN: weight rows per tile, BM: activation rows per tile, WN x WM wavefront grid.
 template <int MODE, int BN, int BM, int WN, int WM>
-__global__ __launch_bounds__(kThreads) void fp8_gemm_kernel(GemmArgs g) {
+__global__ __launch_bounds__(kThreads) void fp8_gemm_kernel(GemmArgs gin) {
   static_assert(WN * WM == kThreads / kWave, "4 wavefronts per workgroup");
+  // Block mode with a K split: blockIdx.y takes K range [y kps, (y + 1) kps) (kps % 128
+  // == 0) and writes fp32 partials to ws[y] ([M, N]); block_split_reduce finishes.
+  GemmArgs g = gin;
+  if constexpr (MODE == MODE_BLOCK) {
+    if (gin.kps > 0) {
+      const int64_t k0 = (int64_t)blockIdx.y * gin.kps, kb0 = k0 / 128, kb_total = gin.K / 128;
+      g.K = gin.K - k0 < gin.kps ? gin.K - k0 : gin.kps;
+      g.a = gin.a + k0;
+      g.w = gin.w + k0;
+      g.sa = static_cast<const float*>(gin.sa) + (gin.sa_vec ? kb0 * gin.M : kb0);
+      g.ld_sa = gin.sa_vec ? 0 : kb_total;
+      g.sb = static_cast<const uint8_t*>(gin.sb) + kb0 * (gin.sb_dtype == AYK_F32 ? 4 : (gin.sb_dtype == AYK_U8 ? 1 : 2));
+      g.ld_sb = kb_total;
+      g.bias = nullptr;
+      g.out = gin.ws + (int64_t)blockIdx.y * gin.M * gin.N;
+      g.out_dtype = AYK_F32;
+      g.ldo = gin.N;
+    }
+  }
   constexpr int TN = BN / WN, TM = BM / WM;  // wavefront tile
   constexpr int FN = TN / 32, FM = TM / 32;  // 32x32 MFMA tiles per wavefront
   static_assert(FN >= 1 && FM >= 1, "wavefront tile must be a multiple of 32x32");
@@ -265,12 +287,13 @@ __global__ __launch_bounds__(kThreads) void fp8_gemm_kernel(GemmArgs g) {
       for (int j = 0; j < FM; ++j) {
         const int64_t m = m_base + wm * TM + j * 32 + frag_row;
         const int64_t mi = m < g.M ? m : g.M - 1;
-        const float sa = load_f32(g.sa, g.sa_dtype, g.sa_vec ? (int64_t)kt * g.M + mi : mi * kblocks + kt);
+        const int64_t sa_ld = g.ld_sa > 0 ? g.ld_sa : kblocks, sb_ld = g.ld_sb > 0 ? g.ld_sb : kblocks;
+        const float sa = load_f32(g.sa, g.sa_dtype, g.sa_vec ? (int64_t)kt * g.M + mi : mi * sa_ld + kt);
 #pragma unroll
         for (int i = 0; i < FN; ++i) {
           const int64_t n = n_base + wn * TN + i * 32;
           const int64_t nb = (n < g.N ? n : g.N - 1) / 128;
-          const float s = sa * load_f32(g.sb, g.sb_dtype, nb * kblocks + kt);
+          const float s = sa * load_f32(g.sb, g.sb_dtype, nb * sb_ld + kt);
 #pragma unroll
           for (int r = 0; r < 16; ++r) acc[i][j][r] = fmaf(part[i][j][r], s, acc[i][j][r]);
         }
@@ -1021,16 +1044,19 @@ __device__ __attribute__((always_inline)) inline void block_gemm_tile(const Gemm
   // [KB, M] (kb * M + m), fp32; lane (frow, h) needs its two m rows. sb is [NB, KB] in
   // fp32 / fp16 / bf16, one value per wavefront, kept as the dword that holds it (its
   // position in the dword is wave-uniform and recomputed at use).
+  // Row strides of the scale tables: ld_sa / ld_sb when set (a K range of a longer K:
+  // the split-K kernel), else this problem's block count.
+  const int64_t sa_ld = g.ld_sa > 0 ? g.ld_sa : kblocks, sb_ld = g.ld_sb > 0 ? g.ld_sb : kblocks;
   int64_t sa_row[FM];
 #pragma unroll
   for (int j = 0; j < FM; ++j) {
     const int64_t m = m_base + wm * 64 + j * 32 + frow;
-    sa_row[j] = (m < g.M ? m : g.M - 1) * (g.sa_vec ? 1 : kblocks);
+    sa_row[j] = (m < g.M ? m : g.M - 1) * (g.sa_vec ? 1 : sa_ld);
   }
   const int64_t nbs = cdiv(g.N, 128);
   const int64_t nb = (n_base + wn * 64) / 128 < nbs ? (n_base + wn * 64) / 128 : nbs - 1;
   const int sb_size = g.sb_dtype == AYK_F32 ? 4 : 2;
-  const int64_t sb_base = nb * kblocks;
+  const int64_t sb_base = nb * sb_ld;
   // Two blocks' scales in flight (slot = block % 2). Slot 1 starts as zeros: the first
   // step folds "the previous block" from it, with zero partials: it adds 0.
   uint32_t sa_w[2][FM], sb_w[2];
@@ -1178,6 +1204,64 @@ __global__ __launch_bounds__(kBlkThreads, 1) void fp8_gemm_block_kernel(GemmArgs
   int tm, tn;
   big_tile_coords(blockIdx.x, g.tiles_m, (int)cdiv(g.N, kBlkTile), tm, tn);
   block_gemm_tile(g, tm, tn, L0, L1, L2, L3);
+}
+
+// Split-K form for launches with too few tiles to fill the machine: blockIdx.y takes the
+// K range [y kps, (y + 1) kps) (kps % 128 == 0) and writes its fp32 partial tile to
+// part[y] ([M, N], row stride N); block_split_reduce sums the partials in split order,
+// adds the bias and rounds once.
+__global__ __launch_bounds__(kBlkThreads, 1) void fp8_gemm_block_split_kernel(GemmArgs g, int64_t kps, float* part) {
+  AYK_BLOCK_LDS;
+  int tm, tn;
+  big_tile_coords(blockIdx.x, g.tiles_m, (int)cdiv(g.N, kBlkTile), tm, tn);
+  const int64_t k0 = (int64_t)blockIdx.y * kps, kb0 = k0 / 128, kb_total = g.K / 128;
+  GemmArgs s = g;
+  s.K = g.K - k0 < kps ? g.K - k0 : kps;
+  s.a = g.a + k0;
+  s.w = g.w + k0;
+  s.sa = static_cast<const float*>(g.sa) + (g.sa_vec ? kb0 * g.M : kb0);
+  s.ld_sa = g.sa_vec ? 0 : kb_total;
+  s.sb = static_cast<const uint8_t*>(g.sb) + kb0 * (g.sb_dtype == AYK_F32 ? 4 : 2);
+  s.ld_sb = kb_total;
+  s.bias = nullptr;
+  s.out = part + (int64_t)blockIdx.y * g.M * g.N;
+  s.out_dtype = AYK_F32;
+  s.ldo = g.N;
+  block_gemm_tile(s, tm, tn, L0, L1, L2, L3);
+}
+
+__global__ __launch_bounds__(256) void block_split_reduce(const float* __restrict__ part, int64_t M, int64_t N, int split,
+                                                          const void* __restrict__ bias, int bias_dtype, void* __restrict__ out,
+                                                          int out_dtype, int64_t ldo) {
+  const int64_t i = (int64_t)blockIdx.x * 256 + threadIdx.x;
+  if (i >= M * N) return;
+  const int64_t m = i / N, n = i - m * N;
+  float v = 0.0f;
+  for (int s = 0; s < split; ++s) v += part[(int64_t)s * M * N + i];
+  if (bias) v += load_f32(bias, bias_dtype, n);
+  store_f32(out, out_dtype, m * ldo + n, v);
+}
+
+// K split of the block-scaled large-tile GEMM: the smallest power of two that gives at
+// least kBlkSplitTarget workgroups, with at least 8 blocks of 128 K per split.
+constexpr int64_t kBlkSplitTarget = 512;
+int64_t block_split(int64_t M, int64_t N, int64_t K) {
+  const int64_t tiles = cdiv(M, kBlkTile) * cdiv(N, kBlkTile);
+  int64_t split = 1;
+  while (tiles * split < kBlkSplitTarget && K / (split * 2) >= 1024 && (K / 128) % (split * 2) == 0) split *= 2;
+  return split;
+}
+// The same rule for the general kernel's 32- or 64-row tiles (M <= 64, K % 128 == 0).
+int64_t general_split(int64_t M, int64_t N, int64_t K) {
+  if (M > 64 || K % 128) return 1;
+  const int64_t tiles = cdiv(M, M <= 32 ? 32 : 64) * cdiv(N, 128);
+  int64_t split = 1;
+  while (tiles * split < kBlkSplitTarget && K / (split * 2) >= 1024 && (K / 128) % (split * 2) == 0) split *= 2;
+  return split;
+}
+size_t block_split_workspace(int64_t M, int64_t N, int64_t K) {
+  const int64_t split = M <= 64 ? general_split(M, N, K) : block_split(M, N, K);
+  return split > 1 ? (size_t)split * (size_t)M * (size_t)N * sizeof(float) : 0;
 }
 
 // ------------------------------------------------------------ MoE grouped block-128 GEMM
@@ -1460,7 +1544,19 @@ int launch_block_big(GemmArgs g, hipStream_t st, const char* op) {
   g.tiles_m = (int)cdiv(g.M, kBlkTile);
   const int64_t tiles = (int64_t)g.tiles_m * cdiv(g.N, kBlkTile);
   if (tiles > 0x7FFFFFFF) return fail(AYK_EINVAL, "%s: problem too large", op);
-  hipLaunchKernelGGL(fp8_gemm_block_kernel, dim3((unsigned)tiles), dim3(kBlkThreads), 0, st, g);
+  const int64_t split = block_split(g.M, g.N, g.K);
+  if (split == 1) {
+    hipLaunchKernelGGL(fp8_gemm_block_kernel, dim3((unsigned)tiles), dim3(kBlkThreads), 0, st, g);
+    return check_launch(op);
+  }
+  const size_t need = block_split_workspace(g.M, g.N, g.K);
+  if (g.ws == nullptr || g.ws_bytes < need)
+    return fail(AYK_EWORKSPACE, "%s: workspace of %zu bytes required, %zu given", op, need, g.ws_bytes);
+  hipLaunchKernelGGL(fp8_gemm_block_split_kernel, dim3((unsigned)tiles, (unsigned)split), dim3(kBlkThreads), 0, st, g,
+                     g.K / split, g.ws);
+  if (int rc = check_launch(op)) return rc;
+  hipLaunchKernelGGL(block_split_reduce, dim3((unsigned)cdiv(g.M * g.N, 256)), dim3(256), 0, st, g.ws, g.M, g.N,
+                     (int)split, g.bias, g.bias_dtype, g.out, g.out_dtype, g.ldo);
   return check_launch(op);
 }
 
@@ -1469,8 +1565,22 @@ int launch_cfg(GemmArgs g, hipStream_t st, const char* op) {
   g.tiles_m = (int)cdiv(g.M, BM);
   const int64_t tiles = (int64_t)g.tiles_m * cdiv(g.N, BN);
   if (tiles > 0x7FFFFFFF) return fail(AYK_EINVAL, "%s: problem too large", op);
-  hipLaunchKernelGGL((fp8_gemm_kernel<MODE, BN, BM, WN, WM>), dim3((unsigned)tiles), dim3(kThreads), 0, st, g);
-  return check_launch(op);
+  const int64_t split = MODE == MODE_BLOCK && BM <= 64 ? general_split(g.M, g.N, g.K) : 1;
+  g.kps = 0;
+  if (split > 1) {
+    const size_t need = block_split_workspace(g.M, g.N, g.K);
+    if (g.ws == nullptr || g.ws_bytes < need)
+      return fail(AYK_EWORKSPACE, "%s: workspace of %zu bytes required, %zu given", op, need, g.ws_bytes);
+    g.kps = g.K / split;
+  }
+  hipLaunchKernelGGL((fp8_gemm_kernel<MODE, BN, BM, WN, WM>), dim3((unsigned)tiles, (unsigned)split), dim3(kThreads), 0, st, g);
+  if (int rc = check_launch(op)) return rc;
+  if (split > 1) {
+    hipLaunchKernelGGL(block_split_reduce, dim3((unsigned)cdiv(g.M * g.N, 256)), dim3(256), 0, st, g.ws, g.M, g.N,
+                       (int)split, g.bias, g.bias_dtype, g.out, g.out_dtype, g.ldo);
+    return check_launch(op);
+  }
+  return AYK_OK;
 }
 
 template <int MODE>
@@ -1490,7 +1600,10 @@ int launch_gemm(const GemmArgs& g, hipStream_t st, const char* op) {
     // The block-scaled large-tile kernel: K % 128 == 0, fp32 activation scales, any float
     // weight-scale dtype, and the same output / bias alignment as above.
     const int64_t out_bytes = g.out_dtype == AYK_F32 ? 4 : 2;
-    const bool big_ok = g.K % 128 == 0 && g.M >= kBlkTile && g.N >= kBlkTile && g.N % 4 == 0 && g.sa_dtype == AYK_F32 &&
+    // 65-127 rows also take it when the K split applies (rows past M read zeros); up to
+    // 64 rows the general kernel's 32- / 64-row tiles split K instead.
+    const bool big_ok = g.K % 128 == 0 && (g.M >= kBlkTile || (g.M > 64 && block_split(g.M, g.N, g.K) > 1)) && g.N >= kBlkTile &&
+                        g.N % 4 == 0 && g.sa_dtype == AYK_F32 &&
                         (g.ldo * out_bytes) % 16 == 0 && aligned16(g.out) &&
                         (g.bias == nullptr || (reinterpret_cast<uintptr_t>(g.bias) & 15) == 0);
     if (big_ok) return launch_block_big(g, st, op);
@@ -1564,10 +1677,16 @@ int ayk_int8_scaled_mm(const void* a, int64_t lda, const void* b, int64_t ldb, i
   return launch_gemm<MODE_INT8>(g, static_cast<hipStream_t>(stream), op);
 }
 
+size_t ayk_fp8_blockwise_mm_workspace_bytes(int64_t M, int64_t N, int64_t K) {
+  if (M < 1 || N < kBlkTile || K < 1 || K % 128) return 0;
+  return block_split_workspace(M, N, K);
+}
+
 int ayk_fp8_blockwise_mm(const void* a, int64_t lda, const void* b, int64_t ldb, int64_t M,
                          int64_t N, int64_t K, const void* scale_a, int sa_dtype, int sa_col_major,
                          const void* scale_b, int sb_dtype, const void* bias, int bias_dtype,
-                         void* out, int out_dtype, int64_t ldo, ayk_stream_t stream) {
+                         void* out, int out_dtype, int64_t ldo, void* workspace, size_t workspace_bytes,
+                         ayk_stream_t stream) {
   const char* op = "fp8_blockwise_mm";
   if (int rc = check_common(op, a, lda, b, ldb, M, N, K, bias, bias_dtype, out_dtype, ldo)) return rc;
   if (!is_float_dtype(sa_dtype) || !is_float_dtype(sb_dtype)) return fail(AYK_EINVAL, "%s: scales must be float32, float16 or bfloat16", op);
@@ -1583,6 +1702,7 @@ int ayk_fp8_blockwise_mm(const void* a, int64_t lda, const void* b, int64_t ldb,
   g.sb = scale_b; g.sb_dtype = sb_dtype;
   g.bias = bias; g.bias_dtype = bias_dtype;
   g.out = out; g.out_dtype = out_dtype; g.ldo = ldo;
+  g.ws = static_cast<float*>(workspace); g.ws_bytes = workspace_bytes;
   return launch_gemm<MODE_BLOCK>(g, static_cast<hipStream_t>(stream), op);
 }
 

@@ -120,7 +120,12 @@ int ayk_fp8_blockwise_mm(const void* a, int64_t lda, const void* b, int64_t ldb,
                          const void* scale_a, int sa_dtype, int sa_col_major,
                          const void* scale_b, int sb_dtype,
                          const void* bias, int bias_dtype,
-                         void* out, int out_dtype, int64_t ldo, ayk_stream_t stream);
+                         void* out, int out_dtype, int64_t ldo,
+                         void* workspace, size_t workspace_bytes, ayk_stream_t stream);
+/* Bytes of split-K partials ayk_fp8_blockwise_mm may need for this shape (0: none). A
+ * launch with fewer tiles than fill the machine splits K and sums fp32 partials in a
+ * fixed order before the single rounding. */
+size_t ayk_fp8_blockwise_mm_workspace_bytes(int64_t M, int64_t N, int64_t K);
 
 /* Replaces fp8_blockwise_scaled_grouped_mm (kernel/triton/moe/moe_grouped_gemm.py:599,
  * kernel :472-585): the MoE grouped block-128 GEMM. Expert e computes rows

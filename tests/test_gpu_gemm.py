@@ -189,6 +189,33 @@ def test_fp8_blockwise_mm(gpu, m, n, k, sdt, col_major):
     assert_linear_close(out, ref, "blockwise_mm")
 
 
+@pytest.mark.parametrize("m,n,k,col_major,sdt,with_bias", [
+    (32, 1024, 4096, False, torch.float32, True),     # K split 4
+    (200, 768, 8192, True, torch.bfloat16, True),     # split 8, column-major activation scales
+    (7, 256, 2048, False, torch.float16, False),      # split 2, 7 rows
+    (256, 2048, 7168, False, torch.float32, False),   # DeepSeek-V3 K, split 4
+    (32, 7168, 18432, False, torch.float32, True),    # DeepSeek-V3 (7168, 18432) at M = 32, split 16
+])
+def test_fp8_blockwise_mm_split_k(gpu, m, n, k, col_major, sdt, with_bias):
+    """Launches with too few 128 x 128 tiles split K over fp32 partials (the workspace the
+    wrapper allocates from the size query) and reduce them in a fixed order."""
+    from ayaka.kernel.hip import _lib, fp8_blockwise_mm
+
+    _say(f"fp8_blockwise_mm split-K m={m} n={n} k={k} col_major={col_major} sdt={sdt} bias={with_bias}")
+    assert _lib.query("ayk_fp8_blockwise_mm_workspace_bytes", m, n, k) > 0, "shape should split"
+    kb, nb = k // 128, -(-n // 128)
+    a = _fp8((m, k), seed=m + 11, scale=30)
+    w = _fp8((n, k), seed=n + 12, scale=30)
+    sa = torch.exp(torch.rand(m, kb, generator=_gen(14)) * -6.9).float()
+    sb = torch.exp(torch.rand(nb, kb, generator=_gen(15)) * -6.9).to(sdt)
+    sa_arg = sa.t().contiguous() if col_major else sa
+    bias = (torch.randn(n, generator=_gen(16)) * 50).to(torch.bfloat16) if with_bias else None
+    ref = ora.fp8_blockwise_mm(a, w, sa_arg, sb, bias, col_major)
+    out = fp8_blockwise_mm(a.to(gpu), w.to(gpu), sa_arg.to(gpu), sb.to(gpu),
+                           bias.to(gpu) if bias is not None else None, a_scale_col_major=col_major)
+    assert_linear_close(out, ref, "blockwise_mm split-K")
+
+
 @pytest.mark.parametrize("m,n,k", [(1, 512, 1024), (1, 1000, 8192), (64, 256, 512), (100, 300, 1024), (512, 512, 2048), (33, 96, 96),
                                    (300, 520, 1024), (777, 1028, 2048),
                                    # 256x256 kernels: codes staged in chunks of four 128-K pairs
