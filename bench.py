@@ -125,7 +125,7 @@ def _bench_gemm(device, reps=20, warmup=5):
     m = 4096
     results = {}
 
-    def run(label, n, k, fn):
+    def run(label, n, k, fn, m=m):
         for _ in range(warmup):
             fn()
         torch.cuda.synchronize()
@@ -159,6 +159,12 @@ def _bench_gemm(device, reps=20, warmup=5):
     sb = torch.rand(n // 128, k // 128, generator=g, device=device)
     out = torch.empty(m, n, dtype=torch.bfloat16, device=device)
     run("block128_dsv3_18432x7168", n, k, lambda: fp8_blockwise_mm(a, w, sa, sb, out=out))
+    # Cfg4's smaller batches: few tiles, so the K split applies (M = 32: 32-row tiles)
+    for m_small in (32, 256):
+        a_s, sa_s = a[:m_small].contiguous(), sa[:m_small].contiguous()
+        out_s = torch.empty(m_small, n, dtype=torch.bfloat16, device=device)
+        run(f"block128_dsv3_18432x7168_m{m_small}", n, k, lambda: fp8_blockwise_mm(a_s, w, sa_s, sb, out=out_s),
+            m=m_small)
     del a, w, out
     # MXFP8, Llama-3-70B gate_up (Cfg5 shape, supplemental M = 4096)
     n, k = 57344, 8192
