@@ -58,7 +58,8 @@ SIGNATURES: dict[str, list[Any]] = {
     "ayk_per_token_group_quant_fp8": [_p, _i, _l, _l, _l, _l, _p, _l, _p, _p],
     "ayk_per_token_group_quant_mxfp8": [_p, _i, _l, _l, _l, _l, _p, _l, _p, _p],
     "ayk_static_quant_fp8": [_p, _i, _l, _p, _i, _p, _p],
-    "ayk_fp8_scaled_mm": [_p, _l, _p, _l, _l, _l, _l, _p, _i, _i, _p, _i, _i, _p, _i, _p, _i, _l, _p],
+    "ayk_fp8_scaled_mm": [_p, _l, _p, _l, _l, _l, _l, _p, _i, _i, _p, _i, _i, _p, _i, _p, _i, _l, _p, _z, _p],
+    "ayk_fp8_scaled_mm_workspace_bytes": [_l, _l, _l],
     "ayk_fp8_blockwise_mm": [_p, _l, _p, _l, _l, _l, _l, _p, _i, _i, _p, _i, _p, _i, _p, _i, _l, _p, _z, _p],
     "ayk_fp8_blockwise_mm_workspace_bytes": [_l, _l, _l],
     "ayk_fp8_grouped_blockwise_mm": [_p, _p, _p, _p, _p, _p, _l, _l, _l, _l, _p, _i, _p],
@@ -78,6 +79,7 @@ _RESTYPES: dict[str, Any] = {
     "ayk_fp8_weight_only_gemv_workspace_bytes": _z,
     "ayk_fp8_blockwise_gemv_workspace_bytes": _z,
     "ayk_fp8_blockwise_mm_workspace_bytes": _z,
+    "ayk_fp8_scaled_mm_workspace_bytes": _z,
     "ayk_fp8_weight_only_gemm_workspace_bytes": _z,
 }
 

@@ -141,19 +141,22 @@ __device__ inline void store4(const GemmArgs& g, int64_t m, int64_t n, const flo
 template <int MODE, int BN, int BM, int WN, int WM>
 __global__ __launch_bounds__(kThreads) void fp8_gemm_kernel(GemmArgs gin) {
   static_assert(WN * WM == kThreads / kWave, "4 wavefronts per workgroup");
-  // Block mode with a K split: blockIdx.y takes K range [y kps, (y + 1) kps) (kps % 128
-  // == 0) and writes fp32 partials to ws[y] ([M, N]); block_split_reduce finishes.
+  // Block or rowwise mode with a K split: blockIdx.y takes K range [y kps, (y + 1) kps)
+  // (kps % 128 == 0) and writes its fp32 partials (rowwise: already scaled) to ws[y]
+  // ([M, N]); block_split_reduce sums them, adds the bias and rounds once.
   GemmArgs g = gin;
-  if constexpr (MODE == MODE_BLOCK) {
+  if constexpr (MODE == MODE_BLOCK || MODE == MODE_SCALED) {
     if (gin.kps > 0) {
       const int64_t k0 = (int64_t)blockIdx.y * gin.kps, kb0 = k0 / 128, kb_total = gin.K / 128;
       g.K = gin.K - k0 < gin.kps ? gin.K - k0 : gin.kps;
       g.a = gin.a + k0;
       g.w = gin.w + k0;
-      g.sa = static_cast<const float*>(gin.sa) + (gin.sa_vec ? kb0 * gin.M : kb0);
-      g.ld_sa = gin.sa_vec ? 0 : kb_total;
-      g.sb = static_cast<const uint8_t*>(gin.sb) + kb0 * (gin.sb_dtype == AYK_F32 ? 4 : (gin.sb_dtype == AYK_U8 ? 1 : 2));
-      g.ld_sb = kb_total;
+      if constexpr (MODE == MODE_BLOCK) {  // K-blocked scale tables follow the K range
+        g.sa = static_cast<const float*>(gin.sa) + (gin.sa_vec ? kb0 * gin.M : kb0);
+        g.ld_sa = gin.sa_vec ? 0 : kb_total;
+        g.sb = static_cast<const uint8_t*>(gin.sb) + kb0 * (gin.sb_dtype == AYK_F32 ? 4 : (gin.sb_dtype == AYK_U8 ? 1 : 2));
+        g.ld_sb = kb_total;
+      }
       g.bias = nullptr;
       g.out = gin.ws + (int64_t)blockIdx.y * gin.M * gin.N;
       g.out_dtype = AYK_F32;
@@ -728,7 +731,22 @@ __global__ __launch_bounds__(kThreads, 1) void fp8_gemm_big_kernel(GemmArgs g) {
 // the first is multiplied. The fragment reads, the MFMA order and the epilogue are the
 // narrow kernel's.
 template <int MODE>
-__global__ __launch_bounds__(kThreads, 1) void fp8_gemm_pair_kernel(GemmArgs g) {
+__global__ __launch_bounds__(kThreads, 1) void fp8_gemm_pair_kernel(GemmArgs gin) {
+  // Rowwise K split (as in the general kernel): blockIdx.y's K range, scaled fp32
+  // partials to ws[y].
+  GemmArgs g = gin;
+  if constexpr (MODE == MODE_SCALED) {
+    if (gin.kps > 0) {
+      const int64_t k0 = (int64_t)blockIdx.y * gin.kps;
+      g.K = gin.K - k0 < gin.kps ? gin.K - k0 : gin.kps;
+      g.a = gin.a + k0;
+      g.w = gin.w + k0;
+      g.bias = nullptr;
+      g.out = gin.ws + (int64_t)blockIdx.y * gin.M * gin.N;
+      g.out_dtype = AYK_F32;
+      g.ldo = gin.N;
+    }
+  }
   static_assert(row_scaled(MODE) || MODE == MODE_MX, "per-row / per-tensor scales or MX codes");
   constexpr int FN = 4, FM = 4;        // 32x32 MFMA tiles per wavefront (n, m)
   constexpr int kPairK = 2 * kBigK;    // 128 K bytes per pair
@@ -1259,6 +1277,33 @@ int64_t general_split(int64_t M, int64_t N, int64_t K) {
   while (tiles * split < kBlkSplitTarget && K / (split * 2) >= 1024 && (K / 128) % (split * 2) == 0) split *= 2;
   return split;
 }
+// Rowwise / per-tensor K split for launches short of one round of bm x bn tiles (one
+// round: 256 workgroups of the 256 x 256 kernel, one per CU; 512 of the general
+// kernel's): as many splits as still fit in that one round, at least 1024 K each (the
+// last may be shorter). Spilling into a second round doubles the time of the splits
+// and multiplies the partial-sum traffic (Qwen2 down at M = 2048: 5 splits 231 us,
+// 2 splits fill the round).
+int64_t scaled_split(int64_t M, int64_t N, int64_t K, int bm, int bn) {
+  if (K % 128) return 1;
+  const int64_t round = bm == kBigTile ? 256 : kBlkSplitTarget;
+  const int64_t tiles = cdiv(M, bm) * cdiv(N, bn);
+  if (tiles * 2 > round) return 1;
+  const int64_t want = round / tiles, most = K / 1024;
+  const int64_t split = want < most ? want : most;
+  if (split <= 1) return 1;
+  const int64_t kps = cdiv(K / 128, split) * 128;
+  return cdiv(K, kps);
+}
+int64_t scaled_kps(int64_t K, int64_t split) { return cdiv(K / 128, split) * 128; }
+size_t scaled_split_workspace(int64_t M, int64_t N, int64_t K) {
+  const int bm = M <= 32 ? 32 : (M <= 64 ? 64 : 128);
+  int64_t split = scaled_split(M, N, K, bm, 128);
+  if (M >= 256 && N >= 256) {
+    const int64_t big = scaled_split(M, N, K, kBigTile, kBigTile);
+    split = big > split ? big : split;
+  }
+  return split > 1 ? (size_t)split * (size_t)M * (size_t)N * sizeof(float) : 0;
+}
 size_t block_split_workspace(int64_t M, int64_t N, int64_t K) {
   const int64_t split = M <= 64 ? general_split(M, N, K) : block_split(M, N, K);
   return split > 1 ? (size_t)split * (size_t)M * (size_t)N * sizeof(float) : 0;
@@ -1533,7 +1578,20 @@ int launch_big(GemmArgs g, hipStream_t st, const char* op) {
     else
       hipLaunchKernelGGL((fp8_gemm_mx128_kernel<MODE>), dim3((unsigned)tiles), dim3(kThreads), 0, st, g);
   } else if (g.K % (2 * kBigK) == 0) {
-    hipLaunchKernelGGL((fp8_gemm_pair_kernel<MODE>), dim3((unsigned)tiles), dim3(kThreads), 0, st, g);
+    const int64_t split = MODE == MODE_SCALED ? scaled_split(g.M, g.N, g.K, kBigTile, kBigTile) : 1;
+    g.kps = 0;
+    if (split > 1) {
+      const size_t need = (size_t)split * (size_t)g.M * (size_t)g.N * sizeof(float);
+      if (g.ws == nullptr || g.ws_bytes < need)
+        return fail(AYK_EWORKSPACE, "%s: workspace of %zu bytes required, %zu given", op, need, g.ws_bytes);
+      g.kps = scaled_kps(g.K, split);
+    }
+    hipLaunchKernelGGL((fp8_gemm_pair_kernel<MODE>), dim3((unsigned)tiles, (unsigned)split), dim3(kThreads), 0, st, g);
+    if (split > 1) {
+      if (int rc = check_launch(op)) return rc;
+      hipLaunchKernelGGL(block_split_reduce, dim3((unsigned)cdiv(g.M * g.N, 256)), dim3(256), 0, st, g.ws, g.M, g.N,
+                         (int)split, g.bias, g.bias_dtype, g.out, g.out_dtype, g.ldo);
+    }
   } else {
     hipLaunchKernelGGL((fp8_gemm_big_kernel<MODE>), dim3((unsigned)tiles), dim3(kThreads), 0, st, g);
   }
@@ -1565,13 +1623,14 @@ int launch_cfg(GemmArgs g, hipStream_t st, const char* op) {
   g.tiles_m = (int)cdiv(g.M, BM);
   const int64_t tiles = (int64_t)g.tiles_m * cdiv(g.N, BN);
   if (tiles > 0x7FFFFFFF) return fail(AYK_EINVAL, "%s: problem too large", op);
-  const int64_t split = MODE == MODE_BLOCK && BM <= 64 ? general_split(g.M, g.N, g.K) : 1;
+  const int64_t split = MODE == MODE_BLOCK && BM <= 64 ? general_split(g.M, g.N, g.K)
+                        : (MODE == MODE_SCALED ? scaled_split(g.M, g.N, g.K, BM, BN) : 1);
   g.kps = 0;
   if (split > 1) {
-    const size_t need = block_split_workspace(g.M, g.N, g.K);
+    const size_t need = (size_t)split * (size_t)g.M * (size_t)g.N * sizeof(float);
     if (g.ws == nullptr || g.ws_bytes < need)
       return fail(AYK_EWORKSPACE, "%s: workspace of %zu bytes required, %zu given", op, need, g.ws_bytes);
-    g.kps = g.K / split;
+    g.kps = MODE == MODE_SCALED ? scaled_kps(g.K, split) : g.K / split;
   }
   hipLaunchKernelGGL((fp8_gemm_kernel<MODE, BN, BM, WN, WM>), dim3((unsigned)tiles, (unsigned)split), dim3(kThreads), 0, st, g);
   if (int rc = check_launch(op)) return rc;
@@ -1634,10 +1693,16 @@ using namespace ayk;
 
 extern "C" {
 
+size_t ayk_fp8_scaled_mm_workspace_bytes(int64_t M, int64_t N, int64_t K) {
+  if (M < 1 || N < 1 || K < 1) return 0;
+  return scaled_split_workspace(M, N, K);
+}
+
 int ayk_fp8_scaled_mm(const void* a, int64_t lda, const void* b, int64_t ldb, int64_t M, int64_t N,
                       int64_t K, const void* scale_a, int sa_dtype, int sa_per_row,
                       const void* scale_b, int sb_dtype, int sb_per_col, const void* bias,
-                      int bias_dtype, void* out, int out_dtype, int64_t ldo, ayk_stream_t stream) {
+                      int bias_dtype, void* out, int out_dtype, int64_t ldo, void* workspace,
+                      size_t workspace_bytes, ayk_stream_t stream) {
   const char* op = "fp8_scaled_mm";
   if (int rc = check_common(op, a, lda, b, ldb, M, N, K, bias, bias_dtype, out_dtype, ldo)) return rc;
   if (!is_float_dtype(sa_dtype) || !is_float_dtype(sb_dtype)) return fail(AYK_EINVAL, "%s: scales must be float32, float16 or bfloat16", op);
@@ -1653,6 +1718,7 @@ int ayk_fp8_scaled_mm(const void* a, int64_t lda, const void* b, int64_t ldb, in
   g.sb = scale_b; g.sb_dtype = sb_dtype; g.sb_vec = sb_per_col;
   g.bias = bias; g.bias_dtype = bias_dtype;
   g.out = out; g.out_dtype = out_dtype; g.ldo = ldo;
+  g.ws = static_cast<float*>(workspace); g.ws_bytes = workspace_bytes;
   return launch_gemm<MODE_SCALED>(g, static_cast<hipStream_t>(stream), op);
 }
 

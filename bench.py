@@ -151,6 +151,16 @@ def _bench_gemm(device, reps=20, warmup=5):
     run("rowwise_qwen2_gate_up", n, k, lambda: fp8_scaled_mm(a, w.t(), sa, sb, out=out))
     run("per_tensor_qwen2_gate_up", n, k, lambda: fp8_scaled_mm(a, w.t(), sa[0], sb[0], out=out))
     del a, w, out
+    # rowwise Qwen2 down (Cfg3) at M = 512 and 2048: few 256 x 256 tiles, so K splits
+    n, k = 3584, 18944
+    w = (torch.randn(n, k, generator=g, device=device) * 50).clamp(-448, 448).to(fp8)
+    sbd = torch.rand(n, generator=g, device=device) * 1e-3
+    for m_small in (512, 2048):
+        a_s = (torch.randn(m_small, k, generator=g, device=device) * 50).clamp(-448, 448).to(fp8)
+        sa_s = torch.rand(m_small, generator=g, device=device) * 1e-3
+        out_s = torch.empty(m_small, n, dtype=torch.bfloat16, device=device)
+        run(f"rowwise_qwen2_down_m{m_small}", n, k, lambda: fp8_scaled_mm(a_s, w.t(), sa_s, sbd, out=out_s), m=m_small)
+    del w, a_s, out_s
     # block-128, DeepSeek-V3 dense (Cfg4, M = 4096)
     n, k = 18432, 7168
     a = (torch.randn(m, k, generator=g, device=device) * 50).clamp(-448, 448).to(fp8)

@@ -114,6 +114,31 @@ def test_fp8_scaled_mm(gpu, m, n, k, rowwise):
     assert_linear_close(out, ref, "fp8_scaled_mm bf16")
 
 
+@pytest.mark.parametrize("m,n,k,rowwise,out_dtype", [
+    (512, 3584, 18944, True, torch.bfloat16),   # 256x256 pair kernel, 28 tiles: 15 K splits
+    (300, 520, 4096, False, torch.float16),     # pair kernel, ragged M / N, per-tensor scales
+    (128, 1024, 4096, True, torch.float32),     # general kernel (128-row tiles)
+    (40, 768, 8192, True, torch.bfloat16),      # general kernel (64-row tiles)
+    (8, 3584, 18944, False, torch.bfloat16),    # general kernel (32-row tiles), last split shorter
+])
+def test_fp8_scaled_mm_split_k(gpu, m, n, k, rowwise, out_dtype):
+    """Launches short of one round of tiles split K: scaled fp32 partials in the workspace
+    the wrapper allocates from the size query, summed in a fixed order with the bias."""
+    from ayaka.kernel.hip import _lib, fp8_scaled_mm
+
+    _say(f"fp8_scaled_mm split-K m={m} n={n} k={k} rowwise={rowwise} out={out_dtype}")
+    assert _lib.query("ayk_fp8_scaled_mm_workspace_bytes", m, n, k) > 0, "shape should split"
+    a = _fp8((m, k), seed=m + 21, scale=40)
+    w = _fp8((n, k), seed=n + 22, scale=40)
+    sa = (torch.rand(m, generator=_gen(23)) * 0.01 + 1e-3) if rowwise else torch.tensor(0.004)
+    sb = (torch.rand(n, generator=_gen(24)) * 0.01 + 1e-3) if rowwise else torch.tensor(0.002)
+    bias = (torch.randn(n, generator=_gen(25)) * 30).to(torch.bfloat16)
+    ref = ora.fp8_scaled_mm(a, w, sa, sb, bias)
+    out = torch.empty(m, n, dtype=out_dtype, device=gpu)
+    fp8_scaled_mm(a.to(gpu), w.to(gpu).t(), sa.to(gpu), sb.to(gpu), bias.to(gpu), out=out)
+    assert_linear_close(out, ref, "fp8_scaled_mm split-K")
+
+
 @pytest.mark.parametrize("out_dtype", [torch.float16, torch.bfloat16, torch.float32])
 def test_fp8_scaled_mm_big_tile_strided_out(gpu, out_dtype):
     """256x256-tile kernel: every output dtype, a padded output row stride, M/N tails."""

@@ -313,7 +313,7 @@ def test_c_abi_rejects_bad_arguments_without_a_gpu():
     assert b"bad shape" in lib.ayk_last_error()
     assert lib.ayk_per_token_group_quant_fp8(None, _lib.AYK_BF16, 4, 128, 128, 96, None, 128, None, None) == _lib.AYK_EINVAL
     assert b"power of two" in lib.ayk_last_error()
-    assert lib.ayk_fp8_scaled_mm(None, 40, None, 40, 4, 4, 40, None, 0, 0, None, 0, 0, None, 0, None, 2, 4, None) == _lib.AYK_EINVAL
+    assert lib.ayk_fp8_scaled_mm(None, 40, None, 40, 4, 4, 40, None, 0, 0, None, 0, 0, None, 0, None, 2, 4, None, 0, None) == _lib.AYK_EINVAL
     assert b"multiple of 16" in lib.ayk_last_error()
     assert lib.ayk_mxfp8_scaled_mm(None, 48, None, 1, None, 48, None, 1, 2, 2, 48, None, 0, None, 2, 2, None) == _lib.AYK_EINVAL
     assert lib.ayk_fp8_weight_only_gemv(None, _lib.AYK_F32, None, 16, 4, 16, None, 0, 1, 1, 16, None, None, 0, None) == _lib.AYK_EINVAL
@@ -321,3 +321,8 @@ def test_c_abi_rejects_bad_arguments_without_a_gpu():
     assert lib.ayk_per_token_quant_fp8(None, _lib.AYK_BF16, 0, 16, 16, None, 16, None, None) == _lib.AYK_OK
     assert lib.ayk_fp8_weight_only_gemv_workspace_bytes(512, 14336) > 0  # split-K shape
     assert lib.ayk_fp8_weight_only_gemv_workspace_bytes(28672, 4096) == 0
+    # GEMM split-K plans: too few tiles split K, a full round does not
+    assert lib.ayk_fp8_scaled_mm_workspace_bytes(512, 3584, 18944) > 0
+    assert lib.ayk_fp8_scaled_mm_workspace_bytes(4096, 37888, 3584) == 0
+    assert lib.ayk_fp8_blockwise_mm_workspace_bytes(32, 7168, 18432) > 0
+    assert lib.ayk_fp8_blockwise_mm_workspace_bytes(4096, 18432, 7168) == 0
