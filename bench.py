@@ -22,6 +22,7 @@ Usage: python bench.py [--gpus 1] [--steps K] [--warmup W] [--no-gemm] [--no-cpu
 """
 
 import argparse
+import itertools
 import json
 import os
 import sys
@@ -151,16 +152,19 @@ def _bench_gemm(device, reps=20, warmup=5):
     run("rowwise_qwen2_gate_up", n, k, lambda: fp8_scaled_mm(a, w.t(), sa, sb, out=out))
     run("per_tensor_qwen2_gate_up", n, k, lambda: fp8_scaled_mm(a, w.t(), sa[0], sb[0], out=out))
     del a, w, out
-    # rowwise Qwen2 down (Cfg3) at M = 512 and 2048: few 256 x 256 tiles, so K splits
+    # rowwise Qwen2 down (Cfg3) at M = 512 and 2048: few 256 x 256 tiles, so K splits.
+    # Weight-bound sizes: 5 rotated weight copies (340 MB) keep every launch on HBM.
     n, k = 3584, 18944
-    w = (torch.randn(n, k, generator=g, device=device) * 50).clamp(-448, 448).to(fp8)
+    wds = [(torch.randn(n, k, generator=g, device=device) * 50).clamp(-448, 448).to(fp8) for _ in range(5)]
     sbd = torch.rand(n, generator=g, device=device) * 1e-3
     for m_small in (512, 2048):
         a_s = (torch.randn(m_small, k, generator=g, device=device) * 50).clamp(-448, 448).to(fp8)
         sa_s = torch.rand(m_small, generator=g, device=device) * 1e-3
         out_s = torch.empty(m_small, n, dtype=torch.bfloat16, device=device)
-        run(f"rowwise_qwen2_down_m{m_small}", n, k, lambda: fp8_scaled_mm(a_s, w.t(), sa_s, sbd, out=out_s), m=m_small)
-    del w, a_s, out_s
+        cyc = itertools.cycle(wds)
+        run(f"rowwise_qwen2_down_m{m_small}", n, k,
+            lambda: fp8_scaled_mm(a_s, next(cyc).t(), sa_s, sbd, out=out_s), m=m_small)
+    del wds, a_s, out_s
     # block-128, DeepSeek-V3 dense (Cfg4, M = 4096)
     n, k = 18432, 7168
     a = (torch.randn(m, k, generator=g, device=device) * 50).clamp(-448, 448).to(fp8)
@@ -169,12 +173,16 @@ def _bench_gemm(device, reps=20, warmup=5):
     sb = torch.rand(n // 128, k // 128, generator=g, device=device)
     out = torch.empty(m, n, dtype=torch.bfloat16, device=device)
     run("block128_dsv3_18432x7168", n, k, lambda: fp8_blockwise_mm(a, w, sa, sb, out=out))
-    # Cfg4's smaller batches: few tiles, so the K split applies (M = 32: 32-row tiles)
+    # Cfg4's smaller batches: few tiles, so the K split applies (M = 32: 32-row tiles).
+    # Weight-bound sizes: 3 rotated weight copies (396 MB) keep every launch on HBM.
+    wbs = [w] + [(torch.randn(n, k, generator=g, device=device) * 50).clamp(-448, 448).to(fp8) for _ in range(2)]
     for m_small in (32, 256):
         a_s, sa_s = a[:m_small].contiguous(), sa[:m_small].contiguous()
         out_s = torch.empty(m_small, n, dtype=torch.bfloat16, device=device)
-        run(f"block128_dsv3_18432x7168_m{m_small}", n, k, lambda: fp8_blockwise_mm(a_s, w, sa_s, sb, out=out_s),
-            m=m_small)
+        cyc = itertools.cycle(wbs)
+        run(f"block128_dsv3_18432x7168_m{m_small}", n, k,
+            lambda: fp8_blockwise_mm(a_s, next(cyc), sa_s, sb, out=out_s), m=m_small)
+    del wbs
     del a, w, out
     # MXFP8, Llama-3-70B gate_up (Cfg5 shape, supplemental M = 4096)
     n, k = 57344, 8192
