@@ -74,11 +74,15 @@ def mxfp8_scaled_mm(
     a_k = kernel_operand(a)
     w_k = kernel_operand(weight)
     ldo = int(result.stride(0)) if rows > 1 else columns
+    # split-K partials for launches short of one round of tiles (torch's allocator: the
+    # graph pool under capture)
+    nbytes = _lib.query("ayk_mxfp8_scaled_mm_workspace_bytes", rows, columns, inner)
+    ws = torch.empty(nbytes, dtype=torch.uint8, device=a.device) if nbytes else None
     _lib.call(
         "ayk_mxfp8_scaled_mm", a_k.data_ptr(), int(a_k.stride(0)) if rows > 1 else inner,
         a_scale.data_ptr(), scale_k, w_k.data_ptr(), int(w_k.stride(0)) if columns > 1 else inner,
         weight_scale.data_ptr(), scale_k, rows, columns, inner,
         _lib.ptr(bias), _lib.dtype_code(bias.dtype) if bias is not None else 0,
-        result.data_ptr(), _lib.dtype_code(result.dtype), ldo, _lib.stream_of(a),
+        result.data_ptr(), _lib.dtype_code(result.dtype), ldo, _lib.ptr(ws), nbytes, _lib.stream_of(a),
     )
     return result

@@ -145,7 +145,7 @@ __global__ __launch_bounds__(kThreads) void fp8_gemm_kernel(GemmArgs gin) {
   // (kps % 128 == 0) and writes its fp32 partials (rowwise: already scaled) to ws[y]
   // ([M, N]); block_split_reduce sums them, adds the bias and rounds once.
   GemmArgs g = gin;
-  if constexpr (MODE == MODE_BLOCK || MODE == MODE_SCALED) {
+  if constexpr (MODE == MODE_BLOCK || MODE == MODE_SCALED || MODE == MODE_MX) {
     if (gin.kps > 0) {
       const int64_t k0 = (int64_t)blockIdx.y * gin.kps, kb0 = k0 / 128, kb_total = gin.K / 128;
       g.K = gin.K - k0 < gin.kps ? gin.K - k0 : gin.kps;
@@ -156,6 +156,10 @@ __global__ __launch_bounds__(kThreads) void fp8_gemm_kernel(GemmArgs gin) {
         g.ld_sa = gin.sa_vec ? 0 : kb_total;
         g.sb = static_cast<const uint8_t*>(gin.sb) + kb0 * (gin.sb_dtype == AYK_F32 ? 4 : (gin.sb_dtype == AYK_U8 ? 1 : 2));
         g.ld_sb = kb_total;
+      }
+      if constexpr (MODE == MODE_MX) {  // UE8M0 code rows: the range's codes start k0 / 32 in
+        g.sa = static_cast<const uint8_t*>(gin.sa) + k0 / 32;
+        g.sb = static_cast<const uint8_t*>(gin.sb) + k0 / 32;
       }
       g.bias = nullptr;
       g.out = gin.ws + (int64_t)blockIdx.y * gin.M * gin.N;
@@ -732,15 +736,19 @@ __global__ __launch_bounds__(kThreads, 1) void fp8_gemm_big_kernel(GemmArgs g) {
 // narrow kernel's.
 template <int MODE>
 __global__ __launch_bounds__(kThreads, 1) void fp8_gemm_pair_kernel(GemmArgs gin) {
-  // Rowwise K split (as in the general kernel): blockIdx.y's K range, scaled fp32
+  // Rowwise / MX K split (as in the general kernel): blockIdx.y's K range, scaled fp32
   // partials to ws[y].
   GemmArgs g = gin;
-  if constexpr (MODE == MODE_SCALED) {
+  if constexpr (MODE == MODE_SCALED || MODE == MODE_MX) {
     if (gin.kps > 0) {
-      const int64_t k0 = (int64_t)blockIdx.y * gin.kps;
+      const int64_t k0 = (int64_t)blockIdx.y * gin.kps;  // MX: kps % 512 == 0 keeps the code rows 16-byte aligned
       g.K = gin.K - k0 < gin.kps ? gin.K - k0 : gin.kps;
       g.a = gin.a + k0;
       g.w = gin.w + k0;
+      if constexpr (MODE == MODE_MX) {
+        g.sa = static_cast<const uint8_t*>(gin.sa) + k0 / 32;
+        g.sb = static_cast<const uint8_t*>(gin.sb) + k0 / 32;
+      }
       g.bias = nullptr;
       g.out = gin.ws + (int64_t)blockIdx.y * gin.M * gin.N;
       g.out_dtype = AYK_F32;
@@ -1573,10 +1581,29 @@ int launch_big(GemmArgs g, hipStream_t st, const char* op) {
   const int64_t tiles = (int64_t)g.tiles_m * cdiv(g.N, kBigTile);
   if (tiles > 0x7FFFFFFF) return fail(AYK_EINVAL, "%s: problem too large", op);
   if constexpr (MODE == MODE_MX) {
-    if (g.K % 512 == 0 && g.ld_sa % 16 == 0 && g.ld_sb % 16 == 0 && aligned16(g.sa) && aligned16(g.sb))
-      hipLaunchKernelGGL((fp8_gemm_pair_kernel<MODE>), dim3((unsigned)tiles), dim3(kThreads), 0, st, g);
-    else
+    if (g.K % 512 == 0 && g.ld_sa % 16 == 0 && g.ld_sb % 16 == 0 && aligned16(g.sa) && aligned16(g.sb)) {
+      int64_t split = scaled_split(g.M, g.N, g.K, kBigTile, kBigTile);
+      g.kps = 0;
+      if (split > 1) {
+        g.kps = cdiv(g.K / 512, split) * 512;  // whole chunks of four 128-K pairs
+        split = cdiv(g.K, g.kps);
+      }
+      if (split > 1) {
+        const size_t need = (size_t)split * (size_t)g.M * (size_t)g.N * sizeof(float);
+        if (g.ws == nullptr || g.ws_bytes < need)
+          return fail(AYK_EWORKSPACE, "%s: workspace of %zu bytes required, %zu given", op, need, g.ws_bytes);
+      } else {
+        g.kps = 0;
+      }
+      hipLaunchKernelGGL((fp8_gemm_pair_kernel<MODE>), dim3((unsigned)tiles, (unsigned)split), dim3(kThreads), 0, st, g);
+      if (split > 1) {
+        if (int rc = check_launch(op)) return rc;
+        hipLaunchKernelGGL(block_split_reduce, dim3((unsigned)cdiv(g.M * g.N, 256)), dim3(256), 0, st, g.ws, g.M, g.N,
+                           (int)split, g.bias, g.bias_dtype, g.out, g.out_dtype, g.ldo);
+      }
+    } else {
       hipLaunchKernelGGL((fp8_gemm_mx128_kernel<MODE>), dim3((unsigned)tiles), dim3(kThreads), 0, st, g);
+    }
   } else if (g.K % (2 * kBigK) == 0) {
     const int64_t split = MODE == MODE_SCALED ? scaled_split(g.M, g.N, g.K, kBigTile, kBigTile) : 1;
     g.kps = 0;
@@ -1624,13 +1651,13 @@ int launch_cfg(GemmArgs g, hipStream_t st, const char* op) {
   const int64_t tiles = (int64_t)g.tiles_m * cdiv(g.N, BN);
   if (tiles > 0x7FFFFFFF) return fail(AYK_EINVAL, "%s: problem too large", op);
   const int64_t split = MODE == MODE_BLOCK && BM <= 64 ? general_split(g.M, g.N, g.K)
-                        : (MODE == MODE_SCALED ? scaled_split(g.M, g.N, g.K, BM, BN) : 1);
+                        : (MODE == MODE_SCALED || MODE == MODE_MX ? scaled_split(g.M, g.N, g.K, BM, BN) : 1);
   g.kps = 0;
   if (split > 1) {
     const size_t need = (size_t)split * (size_t)g.M * (size_t)g.N * sizeof(float);
     if (g.ws == nullptr || g.ws_bytes < need)
       return fail(AYK_EWORKSPACE, "%s: workspace of %zu bytes required, %zu given", op, need, g.ws_bytes);
-    g.kps = MODE == MODE_SCALED ? scaled_kps(g.K, split) : g.K / split;
+    g.kps = MODE == MODE_BLOCK ? g.K / split : scaled_kps(g.K, split);
   }
   hipLaunchKernelGGL((fp8_gemm_kernel<MODE, BN, BM, WN, WM>), dim3((unsigned)tiles, (unsigned)split), dim3(kThreads), 0, st, g);
   if (int rc = check_launch(op)) return rc;
@@ -1812,10 +1839,16 @@ int ayk_fp8_grouped_blockwise_mm(const void* a, const void* b, const float* scal
   return check_launch(op);
 }
 
+size_t ayk_mxfp8_scaled_mm_workspace_bytes(int64_t M, int64_t N, int64_t K) {
+  if (M < 1 || N < 1 || K < 1) return 0;
+  return scaled_split_workspace(M, N, K);
+}
+
 int ayk_mxfp8_scaled_mm(const void* a, int64_t lda, const uint8_t* a_scale, int64_t ld_as,
                         const void* w, int64_t ldw, const uint8_t* w_scale, int64_t ld_ws,
                         int64_t M, int64_t N, int64_t K, const void* bias, int bias_dtype,
-                        void* out, int out_dtype, int64_t ldo, ayk_stream_t stream) {
+                        void* out, int out_dtype, int64_t ldo, void* workspace, size_t workspace_bytes,
+                        ayk_stream_t stream) {
   const char* op = "mxfp8_scaled_mm";
   if (M < 0 || N < 0 || K < 1 || K % 32) return fail(AYK_EINVAL, "%s: K=%lld must be a positive multiple of the MXFP8 group size 32", op, (long long)K);
   if (ld_as < K / 32 || ld_ws < K / 32) return fail(AYK_EINVAL, "%s: scale row strides must be >= K/32", op);
@@ -1840,6 +1873,7 @@ int ayk_mxfp8_scaled_mm(const void* a, int64_t lda, const uint8_t* a_scale, int6
   g.sb = w_scale; g.ld_sb = ld_ws; g.sb_dtype = AYK_U8;
   g.bias = bias; g.bias_dtype = bias_dtype;
   g.out = out; g.out_dtype = out_dtype; g.ldo = ldo;
+  g.ws = static_cast<float*>(workspace); g.ws_bytes = workspace_bytes;
   return launch_gemm<MODE_MX>(g, static_cast<hipStream_t>(stream), op);
 }
 

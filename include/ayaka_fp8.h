@@ -154,7 +154,11 @@ int ayk_mxfp8_scaled_mm(const void* a, int64_t lda, const uint8_t* a_scale, int6
                         const void* w, int64_t ldw, const uint8_t* w_scale, int64_t ld_ws,
                         int64_t M, int64_t N, int64_t K,
                         const void* bias, int bias_dtype,
-                        void* out, int out_dtype, int64_t ldo, ayk_stream_t stream);
+                        void* out, int out_dtype, int64_t ldo,
+                        void* workspace, size_t workspace_bytes, ayk_stream_t stream);
+/* Bytes of split-K partials ayk_mxfp8_scaled_mm may need for this shape (0: none);
+ * the same rule as ayk_fp8_scaled_mm_workspace_bytes. */
+size_t ayk_mxfp8_scaled_mm_workspace_bytes(int64_t M, int64_t N, int64_t K);
 
 /* Replaces ayaka::fp8_weight_only_gemv (gemm/fp8_gemv.py:323; oracle reference/gemm.py:129-157).
  * out[n] = sum_k x[k] * w[n, k] * scale[(n / by) * scale_row_stride + k / bx]

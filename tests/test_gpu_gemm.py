@@ -139,6 +139,31 @@ def test_fp8_scaled_mm_split_k(gpu, m, n, k, rowwise, out_dtype):
     assert_linear_close(out, ref, "fp8_scaled_mm split-K")
 
 
+@pytest.mark.parametrize("m,n,k", [
+    (512, 2048, 4096),   # 256x256 pair kernel: 16 tiles, 4 splits of 1024 K (whole code chunks)
+    (300, 520, 8704),    # pair kernel, ragged M / N, 17 chunks of 512 K: the last split shorter
+    (64, 1024, 8192),    # general kernel, 64-row tiles
+    (5, 768, 4096),      # general kernel, 32-row tiles
+])
+def test_mxfp8_scaled_mm_split_k(gpu, m, n, k):
+    """MXFP8 launches short of one round of tiles split K; each split reads its UE8M0
+    codes from k0 / 32 on in every code row."""
+    from ayaka.kernel.hip import _lib, mxfp8_scaled_mm
+
+    _say(f"mxfp8_scaled_mm split-K m={m} n={n} k={k}")
+    assert _lib.query("ayk_mxfp8_scaled_mm_workspace_bytes", m, n, k) > 0, "shape should split"
+    torch.manual_seed(m + n + k)
+    x = torch.distributions.StudentT(3.0).sample((m, k))
+    wf = torch.randn(n, k, generator=_gen(31))
+    qa, ca = ora.per_token_group_quant_mxfp8(x, 32)
+    qw, cw = ora.per_token_group_quant_mxfp8(wf, 32)
+    bias = (torch.randn(n, generator=_gen(32)) * 10).to(torch.bfloat16)
+    ref = ora.mxfp8_scaled_mm(qa, ca, qw, cw, bias)
+    y = mxfp8_scaled_mm(qa.to(gpu), ca.to(gpu), qw.to(gpu), cw.to(gpu), bias.to(gpu),
+                        out=torch.empty(m, n, dtype=torch.bfloat16, device=gpu))
+    assert_linear_close(y, ref, "mxfp8_scaled_mm split-K")
+
+
 @pytest.mark.parametrize("out_dtype", [torch.float16, torch.bfloat16, torch.float32])
 def test_fp8_scaled_mm_big_tile_strided_out(gpu, out_dtype):
     """256x256-tile kernel: every output dtype, a padded output row stride, M/N tails."""

@@ -315,7 +315,8 @@ def test_c_abi_rejects_bad_arguments_without_a_gpu():
     assert b"power of two" in lib.ayk_last_error()
     assert lib.ayk_fp8_scaled_mm(None, 40, None, 40, 4, 4, 40, None, 0, 0, None, 0, 0, None, 0, None, 2, 4, None, 0, None) == _lib.AYK_EINVAL
     assert b"multiple of 16" in lib.ayk_last_error()
-    assert lib.ayk_mxfp8_scaled_mm(None, 48, None, 1, None, 48, None, 1, 2, 2, 48, None, 0, None, 2, 2, None) == _lib.AYK_EINVAL
+    assert lib.ayk_mxfp8_scaled_mm(None, 48, None, 1, None, 48, None, 1, 2, 2, 48, None, 0, None, 2, 2, None, 0, None) == _lib.AYK_EINVAL
+    assert lib.ayk_mxfp8_scaled_mm_workspace_bytes(64, 8192, 28672) > 0
     assert lib.ayk_fp8_weight_only_gemv(None, _lib.AYK_F32, None, 16, 4, 16, None, 0, 1, 1, 16, None, None, 0, None) == _lib.AYK_EINVAL
     # zero-sized problems are no-ops that succeed without touching a device
     assert lib.ayk_per_token_quant_fp8(None, _lib.AYK_BF16, 0, 16, 16, None, 16, None, None) == _lib.AYK_OK
