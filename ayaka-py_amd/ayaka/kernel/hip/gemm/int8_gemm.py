@@ -72,10 +72,15 @@ def int8_scaled_mm(
         return result
     a_k = kernel_operand(a)
     w_k = kernel_operand(b.t())
+    inner = int(a_k.shape[1])
+    # split-K partials for launches short of one round of tiles
+    nbytes = _lib.query("ayk_int8_scaled_mm_workspace_bytes", rows, columns, inner)
+    ws = torch.empty(nbytes, dtype=torch.uint8, device=a.device) if nbytes else None
     _lib.call(
         "ayk_int8_scaled_mm", a_k.data_ptr(), _row_stride(a_k), w_k.data_ptr(), _row_stride(w_k),
-        rows, columns, int(a_k.shape[1]), scale_a.data_ptr(), scale_b.data_ptr(),
+        rows, columns, inner, scale_a.data_ptr(), scale_b.data_ptr(),
         _lib.ptr(bias), _lib.dtype_code(bias.dtype) if bias is not None else 0,
-        result.data_ptr(), _lib.dtype_code(result.dtype), _row_stride(result), _lib.stream_of(a),
+        result.data_ptr(), _lib.dtype_code(result.dtype), _row_stride(result),
+        _lib.ptr(ws), nbytes, _lib.stream_of(a),
     )
     return result

@@ -145,7 +145,7 @@ __global__ __launch_bounds__(kThreads) void fp8_gemm_kernel(GemmArgs gin) {
   // (kps % 128 == 0) and writes its fp32 partials (rowwise: already scaled) to ws[y]
   // ([M, N]); block_split_reduce sums them, adds the bias and rounds once.
   GemmArgs g = gin;
-  if constexpr (MODE == MODE_BLOCK || MODE == MODE_SCALED || MODE == MODE_MX) {
+  if constexpr (MODE == MODE_BLOCK || MODE == MODE_SCALED || MODE == MODE_MX || MODE == MODE_INT8) {
     if (gin.kps > 0) {
       const int64_t k0 = (int64_t)blockIdx.y * gin.kps, kb0 = k0 / 128, kb_total = gin.K / 128;
       g.K = gin.K - k0 < gin.kps ? gin.K - k0 : gin.kps;
@@ -739,7 +739,7 @@ __global__ __launch_bounds__(kThreads, 1) void fp8_gemm_pair_kernel(GemmArgs gin
   // Rowwise / MX K split (as in the general kernel): blockIdx.y's K range, scaled fp32
   // partials to ws[y].
   GemmArgs g = gin;
-  if constexpr (MODE == MODE_SCALED || MODE == MODE_MX) {
+  if constexpr (MODE == MODE_SCALED || MODE == MODE_MX || MODE == MODE_INT8) {
     if (gin.kps > 0) {
       const int64_t k0 = (int64_t)blockIdx.y * gin.kps;  // MX: kps % 512 == 0 keeps the code rows 16-byte aligned
       g.K = gin.K - k0 < gin.kps ? gin.K - k0 : gin.kps;
@@ -1605,7 +1605,7 @@ int launch_big(GemmArgs g, hipStream_t st, const char* op) {
       hipLaunchKernelGGL((fp8_gemm_mx128_kernel<MODE>), dim3((unsigned)tiles), dim3(kThreads), 0, st, g);
     }
   } else if (g.K % (2 * kBigK) == 0) {
-    const int64_t split = MODE == MODE_SCALED ? scaled_split(g.M, g.N, g.K, kBigTile, kBigTile) : 1;
+    const int64_t split = row_scaled(MODE) ? scaled_split(g.M, g.N, g.K, kBigTile, kBigTile) : 1;
     g.kps = 0;
     if (split > 1) {
       const size_t need = (size_t)split * (size_t)g.M * (size_t)g.N * sizeof(float);
@@ -1651,7 +1651,7 @@ int launch_cfg(GemmArgs g, hipStream_t st, const char* op) {
   const int64_t tiles = (int64_t)g.tiles_m * cdiv(g.N, BN);
   if (tiles > 0x7FFFFFFF) return fail(AYK_EINVAL, "%s: problem too large", op);
   const int64_t split = MODE == MODE_BLOCK && BM <= 64 ? general_split(g.M, g.N, g.K)
-                        : (MODE == MODE_SCALED || MODE == MODE_MX ? scaled_split(g.M, g.N, g.K, BM, BN) : 1);
+                        : (MODE != MODE_BLOCK ? scaled_split(g.M, g.N, g.K, BM, BN) : 1);
   g.kps = 0;
   if (split > 1) {
     const size_t need = (size_t)split * (size_t)g.M * (size_t)g.N * sizeof(float);
@@ -1749,9 +1749,15 @@ int ayk_fp8_scaled_mm(const void* a, int64_t lda, const void* b, int64_t ldb, in
   return launch_gemm<MODE_SCALED>(g, static_cast<hipStream_t>(stream), op);
 }
 
+size_t ayk_int8_scaled_mm_workspace_bytes(int64_t M, int64_t N, int64_t K) {
+  if (M < 1 || N < 1 || K < 1) return 0;
+  return scaled_split_workspace(M, N, K);
+}
+
 int ayk_int8_scaled_mm(const void* a, int64_t lda, const void* b, int64_t ldb, int64_t M, int64_t N,
                        int64_t K, const float* scale_a, const float* scale_b, const void* bias,
-                       int bias_dtype, void* out, int out_dtype, int64_t ldo, ayk_stream_t stream) {
+                       int bias_dtype, void* out, int out_dtype, int64_t ldo, void* workspace, size_t workspace_bytes,
+                       ayk_stream_t stream) {
   const char* op = "int8_scaled_mm";
   if (int rc = check_common(op, a, lda, b, ldb, M, N, K, bias, bias_dtype, out_dtype, ldo)) return rc;
   if ((M > 0 && scale_a == nullptr) || (N > 0 && scale_b == nullptr)) return fail(AYK_EINVAL, "%s: scale_a / scale_b are required", op);
@@ -1767,6 +1773,7 @@ int ayk_int8_scaled_mm(const void* a, int64_t lda, const void* b, int64_t ldb, i
   g.sb = scale_b; g.sb_dtype = AYK_F32; g.sb_vec = 1;
   g.bias = bias; g.bias_dtype = bias_dtype;
   g.out = out; g.out_dtype = out_dtype; g.ldo = ldo;
+  g.ws = static_cast<float*>(workspace); g.ws_bytes = workspace_bytes;
   return launch_gemm<MODE_INT8>(g, static_cast<hipStream_t>(stream), op);
 }
 

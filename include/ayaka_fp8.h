@@ -114,7 +114,11 @@ int ayk_int8_scaled_mm(const void* a, int64_t lda, const void* b, int64_t ldb,
                        int64_t M, int64_t N, int64_t K,
                        const float* scale_a, const float* scale_b,
                        const void* bias, int bias_dtype,
-                       void* out, int out_dtype, int64_t ldo, ayk_stream_t stream);
+                       void* out, int out_dtype, int64_t ldo,
+                       void* workspace, size_t workspace_bytes, ayk_stream_t stream);
+/* Bytes of split-K partials ayk_int8_scaled_mm may need for this shape (0: none); the
+ * same rule as ayk_fp8_scaled_mm_workspace_bytes. */
+size_t ayk_int8_scaled_mm_workspace_bytes(int64_t M, int64_t N, int64_t K);
 
 /* Replaces ayaka::fp8_blockwise_mm (gemm/fp8_gemm.py:370; oracle reference/gemm.py:40-70).
  * out = sum_kb (a[:, kb] @ b[:, kb]^T) * scale_a[m, kb] * scale_b[n / 128, kb] + bias.

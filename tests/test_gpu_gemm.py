@@ -422,6 +422,22 @@ def test_int8_scaled_mm_integer_sum_is_exact(gpu, m, n, k):
     assert torch.equal(out.cpu().to(torch.int64), exact)
 
 
+@pytest.mark.parametrize("m,n,k", [(512, 768, 8192), (40, 768, 8192)])
+def test_int8_scaled_mm_split_k_is_exact(gpu, m, n, k):
+    """Launches short of one round of tiles split K (256x256 kernel, general kernel):
+    with operands in [-8, 8) every partial and the total stay below 2^24, so the fp32
+    split sum equals the integer product exactly, with unit scales."""
+    from ayaka.kernel.hip import _lib, int8_scaled_mm
+
+    _say(f"int8_scaled_mm split-K exact m={m} n={n} k={k}")
+    assert _lib.query("ayk_int8_scaled_mm_workspace_bytes", m, n, k) > 0, "shape should split"
+    a = torch.randint(-8, 8, (m, k), generator=_gen(41), dtype=torch.int8)
+    w = torch.randint(-8, 8, (n, k), generator=_gen(42), dtype=torch.int8)
+    exact = ora.int8_matmul_exact(a, w)
+    out = int8_scaled_mm(a.to(gpu), w.to(gpu).t(), torch.ones(m, device=gpu), torch.ones(n, device=gpu), out_dtype=torch.float32)
+    assert torch.equal(out.cpu().to(torch.int64), exact)
+
+
 def test_int8_scaled_mm_row_major_b_and_contract(gpu):
     from ayaka.kernel.hip import int8_scaled_mm
 
