@@ -1268,12 +1268,19 @@ __global__ __launch_bounds__(256) void block_split_reduce(const float* __restric
   store_f32(out, out_dtype, m * ldo + n, v);
 }
 
-// K split of the block-scaled large-tile GEMM: the smallest power of two that gives at
-// least kBlkSplitTarget workgroups, with at least 8 blocks of 128 K per split.
+// K split of the block-scaled large-tile GEMM (powers of two dividing K / 128, at least
+// 1024 K per split). Under one round of tiles (256, one workgroup per CU): as many
+// splits as still fit in that round (7168 x 18432 at M = 256: 2 splits 94 us, 4 splits
+// 123 us). From one round up to kBlkSplitTarget tiles: splits until that many
+// workgroups (18432 x 7168 at M = 256: 2 splits 130 us, none 139 us).
 constexpr int64_t kBlkSplitTarget = 512;
 int64_t block_split(int64_t M, int64_t N, int64_t K) {
   const int64_t tiles = cdiv(M, kBlkTile) * cdiv(N, kBlkTile);
   int64_t split = 1;
+  if (tiles < 256) {
+    while (tiles * split * 2 <= 256 && K / (split * 2) >= 1024 && (K / 128) % (split * 2) == 0) split *= 2;
+    return split;
+  }
   while (tiles * split < kBlkSplitTarget && K / (split * 2) >= 1024 && (K / 128) % (split * 2) == 0) split *= 2;
   return split;
 }
