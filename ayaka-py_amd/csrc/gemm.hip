@@ -1589,18 +1589,15 @@ int launch_big(GemmArgs g, hipStream_t st, const char* op) {
   if (tiles > 0x7FFFFFFF) return fail(AYK_EINVAL, "%s: problem too large", op);
   if constexpr (MODE == MODE_MX) {
     if (g.K % 512 == 0 && g.ld_sa % 16 == 0 && g.ld_sb % 16 == 0 && aligned16(g.sa) && aligned16(g.sb)) {
-      int64_t split = scaled_split(g.M, g.N, g.K, kBigTile, kBigTile);
-      g.kps = 0;
-      if (split > 1) {
-        g.kps = cdiv(g.K / 512, split) * 512;  // whole chunks of four 128-K pairs
-        split = cdiv(g.K, g.kps);
-      }
+      // K per split in whole chunks of four 128-K pairs (keeps the code rows 16-byte aligned)
+      const int64_t planned = scaled_split(g.M, g.N, g.K, kBigTile, kBigTile);
+      const int64_t kps = planned > 1 ? cdiv(g.K / 512, planned) * 512 : g.K;
+      const int64_t split = cdiv(g.K, kps);
+      g.kps = split > 1 ? kps : 0;
       if (split > 1) {
         const size_t need = (size_t)split * (size_t)g.M * (size_t)g.N * sizeof(float);
         if (g.ws == nullptr || g.ws_bytes < need)
           return fail(AYK_EWORKSPACE, "%s: workspace of %zu bytes required, %zu given", op, need, g.ws_bytes);
-      } else {
-        g.kps = 0;
       }
       hipLaunchKernelGGL((fp8_gemm_pair_kernel<MODE>), dim3((unsigned)tiles, (unsigned)split), dim3(kThreads), 0, st, g);
       if (split > 1) {
