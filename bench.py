@@ -193,7 +193,7 @@ def _bench_gemm(device, reps=20, warmup=5):
     out = torch.empty(m, n, dtype=torch.bfloat16, device=device)
     run("mxfp8_llama70b_gate_up", n, k, lambda: mxfp8_scaled_mm(a, ca, w, cw, out=out))
     del a, w, out
-    # INT8 rowwise (the §8(f) INT8 scaled GEMM), on the Qwen2 gate_up shape
+    # INT8 rowwise scaled GEMM, on the Qwen2 gate_up shape
     from ayaka.kernel.hip import int8_scaled_mm
 
     n, k = 37888, 3584

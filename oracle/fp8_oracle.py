@@ -277,7 +277,7 @@ def fp8_linear(recipe: str, x: torch.Tensor, weight: torch.Tensor, weight_scale:
     return y.reshape(*lead, n)
 
 
-# ------------------------------------------------------------------ KV cache (§8 f3)
+# ------------------------------------------------------------------ KV cache
 def kv_write(source, cache, slots, inverse_scale: float) -> None:
     """Write rows of ``source`` [n, heads, head_dim] to ``cache`` [pages, page_size, heads,
     head_dim] at flattened slots (reference cache_ops.py:40-62 ``_write_reference``, with
