@@ -62,7 +62,8 @@ def test_graph_replays_match_eager(gpu):
 def test_graph_replays_kv_cache_moe_int8_block(gpu):
     """A serving-style step: KV write of the step's tokens into fp8 pages, a
     dequantizing gather, the MoE grouped GEMM (both pointer-table flavours, device-side
-    problem sizes), the INT8 GEMM and the block-128 GEMM, captured once. Writes of the
+    problem sizes), the INT8 GEMM, the block-128 GEMM and split-K block-128 and MXFP8
+    GEMMs, captured once. Writes of the
     same tokens to the same slots are idempotent, so every replay must reproduce the
     eager caches and outputs bit for bit."""
     import ayaka.kernel.hip as H
@@ -97,6 +98,16 @@ def test_graph_replays_kv_cache_moe_int8_block(gpu):
     wb = (torch.randn(256, 512, generator=g, device=gpu) * 40).clamp(-448, 448).to(FP8)
     sab = torch.rand(200, 4, generator=g, device=gpu)
     sbb = torch.rand(2, 4, generator=g, device=gpu)
+    # split-K shapes: block-128 (32 rows, 4 splits) and MXFP8 (64 rows, 8 splits); their
+    # partial-sum workspaces come from the graph's pool
+    a_sk = (torch.randn(32, 4096, generator=g, device=gpu) * 40).clamp(-448, 448).to(FP8)
+    w_sk = (torch.randn(1024, 4096, generator=g, device=gpu) * 40).clamp(-448, 448).to(FP8)
+    sa_sk = torch.rand(32, 32, generator=g, device=gpu)
+    sb_sk = torch.rand(8, 32, generator=g, device=gpu)
+    a_mx = (torch.randn(64, 8192, generator=g, device=gpu) * 40).clamp(-448, 448).to(FP8)
+    w_mx = (torch.randn(1024, 8192, generator=g, device=gpu) * 40).clamp(-448, 448).to(FP8)
+    ca_mx = torch.randint(110, 125, (64, 256), generator=g, device=gpu, dtype=torch.uint8)
+    cw_mx = torch.randint(110, 125, (1024, 256), generator=g, device=gpu, dtype=torch.uint8)
 
     def work():
         H.write_kv(key, val, kc, vc, slots, 0.5, 0.25)
@@ -109,6 +120,8 @@ def test_graph_replays_kv_cache_moe_int8_block(gpu):
             outs.append(o)
         outs.append(H.int8_scaled_mm(a8, w8.t(), s8a, s8w))
         outs.append(H.fp8_blockwise_mm(ab, wb, sab, sbb))
+        outs.append(H.fp8_blockwise_mm(a_sk, w_sk, sa_sk, sb_sk))
+        outs.append(H.mxfp8_scaled_mm(a_mx, ca_mx, w_mx, cw_mx, out=torch.empty(64, 1024, dtype=torch.bfloat16, device=gpu)))
         return outs
 
     eager = [t.clone() for t in work()]
