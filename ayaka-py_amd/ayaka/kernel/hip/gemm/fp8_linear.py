@@ -1,23 +1,31 @@
 """Dense FP8 linear entry points used by the FP8 linear methods.
 
-Same functions, arguments and dispatch as the reference's
-``python/ayaka/kernel/triton/gemm/fp8_linear.py:102-260``:
+Public contract of ``python/ayaka/kernel/triton/gemm/fp8_linear.py:102-260``: the same
+three functions, arguments, validations (order, exception types, messages) and recipe
+routing. Routing by the flattened row count ``M``:
 
-* ``M == 1`` runs the weight-only decode GEMV over the raw fp8 weight (the
-  activation is not quantized), for every recipe here;
-* rowwise and dynamic per-tensor quantize the activation per token, then run the
-  scaled GEMM; static per-tensor quantizes with the calibrated ``input_scale``;
-* block-128 quantizes per (token, 128-K group), then runs the block-scaled GEMM.
+=================  ====================================  ==================================
+recipe             M == 1                                 M > 1
+=================  ====================================  ==================================
+per-tensor         weight-only GEMV, scale rows 1 or N   static quant + scaled GEMM when an
+                                                         ``input_scale`` is given, else the
+                                                         weight-only GEMM
+rowwise            weight-only GEMV, per-row scale       per-token quant + scaled GEMM
+block-128          weight-only GEMV, 128 x 128 blocks    group-128 quant + block GEMM
+=================  ====================================  ==================================
 
-One deliberate difference: for the W8A8 GEMMs the bias is added in fp32 inside the
-GEMM epilogue (one rounding to the activation dtype) instead of a separate
-activation-dtype add afterwards (two roundings). The GEMV paths add it afterwards,
-as the reference does.
+How the calls are assembled is this module's own: one ``_Activation`` record carries
+the validated, flattened input and knows how to shape a result back; each recipe is a
+short decision over it. For the W8A8 GEMMs the bias is added in fp32 inside the GEMM
+epilogue (one rounding to the activation dtype) where the reference adds it afterwards
+in the activation dtype (two roundings); the weight-only paths add it afterwards as the
+reference does.
 """
 
 from __future__ import annotations
 
 import math
+from dataclasses import dataclass
 
 import torch
 
@@ -31,52 +39,70 @@ from ayaka.utils.math_utils import div_ceil
 
 __all__ = ["fp8_block_linear", "fp8_pertensor_linear", "fp8_rowwise_linear"]
 
-_BLOCK128 = 128
+#: K (and N) extent of one block scale in the block-128 checkpoint contract.
+_SCALE_TILE = 128
 
 
-def _validate_activation(x: torch.Tensor) -> None:
-    require_tensor(x, "x")
-    require_dtype(x, "x", (torch.float16, torch.bfloat16))
-    require_cuda(x, "x")
-    if x.ndim < 1:
-        raise ValueError("x must have at least one dimension")
+@dataclass(frozen=True)
+class _Activation:
+    """A validated ``[..., K]`` activation viewed as a contiguous ``[M, K]`` matrix, and
+    the ``[N, K]`` weight it is multiplied with."""
 
+    lead: tuple[int, ...]
+    matrix: torch.Tensor
+    columns: int
 
-def _validate_dense_weight(weight: torch.Tensor, inner: int) -> None:
-    validate_operand(weight, "weight", dtype=require_fp8_dtype(), allow_transposed=False)
-    if weight.shape[1] != inner:
-        raise ValueError(f"weight must be [N, K] with K={inner}, got {tuple(weight.shape)}")
+    @property
+    def rows(self) -> int:
+        return int(self.matrix.shape[0])
 
+    @property
+    def inner(self) -> int:
+        return int(self.matrix.shape[1])
 
-def _flatten_activation(x: torch.Tensor) -> tuple[tuple[int, ...], int, int, torch.Tensor]:
-    lead = tuple(x.shape[:-1])
-    inner = int(x.shape[-1])
-    rows = math.prod(lead) if lead else 1
-    x2d = x.reshape(rows, inner)
-    if not x2d.is_contiguous():
-        x2d = x2d.contiguous()
-    return lead, inner, rows, x2d
+    @classmethod
+    def of(cls, x: torch.Tensor, weight: torch.Tensor, bias: torch.Tensor | None) -> _Activation:
+        # Validation order of the reference: activation, then weight against K, then bias.
+        require_tensor(x, "x")
+        require_dtype(x, "x", (torch.float16, torch.bfloat16))
+        require_cuda(x, "x")
+        if x.ndim < 1:
+            raise ValueError("x must have at least one dimension")
+        k = int(x.shape[-1])
+        lead = tuple(int(d) for d in x.shape[:-1])
+        matrix = x.reshape(math.prod(lead), k)  # prod(()) == 1: a [K] input is one row
+        if not matrix.is_contiguous():
+            matrix = matrix.contiguous()
+        validate_operand(weight, "weight", dtype=require_fp8_dtype(), allow_transposed=False)
+        if int(weight.shape[1]) != k:
+            raise ValueError(f"weight must be [N, K] with K={k}, got {tuple(weight.shape)}")
+        act = cls(lead, matrix, int(weight.shape[0]))
+        validate_bias(bias, matrix, act.columns, reference_name="x")
+        return act
 
+    def empty_output(self) -> torch.Tensor:
+        return torch.empty((self.rows, self.columns), dtype=self.matrix.dtype, device=self.matrix.device)
 
-def _weight_only(x2d, weight, weight_scale, *, block_size_y: int, block_size_x: int, scale_dtype: str) -> torch.Tensor:
-    """W8A16: split-K GEMV at one row, tiled GEMM above it."""
-    inner = int(x2d.shape[1])
-    stride = div_ceil(inner, block_size_x)
-    if x2d.shape[0] == 1:
-        return fp8_weight_only_gemv(x2d.reshape(inner), weight, weight_scale, scale_row_stride=stride,
-                                    block_size_y=block_size_y, block_size_x=block_size_x, scale_dtype=scale_dtype)
-    return fp8_weight_only_gemm(x2d, weight, weight_scale, scale_row_stride=stride,
-                                block_size_y=block_size_y, block_size_x=block_size_x, scale_dtype=scale_dtype)
+    def shaped(self, result: torch.Tensor, bias_after: torch.Tensor | None = None) -> torch.Tensor:
+        """``result`` ([M, N] or [N]) back to ``[..., N]``, adding a not-yet-applied bias."""
+        if bias_after is not None:
+            result = result + bias_after
+        return result.reshape(*self.lead, self.columns)
 
+    def weight_only(self, weight: torch.Tensor, scale: torch.Tensor, scale_rows: int, scale_cols: int,
+                    scale_dtype: str) -> torch.Tensor:
+        """The activation is not quantized: decode GEMV at one row, W8A16 GEMM above.
+        ``scale_rows x scale_cols`` is the weight-scale block (``block_size_y/x``)."""
+        geometry = dict(scale_row_stride=div_ceil(self.inner, scale_cols), block_size_y=scale_rows,
+                        block_size_x=scale_cols, scale_dtype=scale_dtype)
+        if self.rows == 1:
+            return fp8_weight_only_gemv(self.matrix.reshape(self.inner), weight, scale, **geometry)
+        return fp8_weight_only_gemm(self.matrix, weight, scale, **geometry)
 
-def _output(x2d: torch.Tensor, columns: int) -> torch.Tensor:
-    return torch.empty((x2d.shape[0], columns), dtype=x2d.dtype, device=x2d.device)
-
-
-def _finish(result: torch.Tensor, lead: tuple[int, ...], bias: torch.Tensor | None) -> torch.Tensor:
-    if bias is not None:
-        result = result + bias
-    return result.reshape(*lead, result.shape[-1])
+    def channel_scaled(self, weight: torch.Tensor, scale: torch.Tensor) -> torch.Tensor:
+        """Weight-only product for a scalar or per-row ``[N]`` fp32 weight scale."""
+        rows_per_scale = self.columns if scale.numel() == 1 else 1
+        return self.weight_only(weight, scale, rows_per_scale, self.inner, "float32")
 
 
 def fp8_pertensor_linear(
@@ -89,26 +115,17 @@ def fp8_pertensor_linear(
 ) -> torch.Tensor:
     """``x @ (weight * weight_scale)^T`` for a scalar or per-row ``[N]`` fp32 weight scale.
 
-    ``input_scale`` (static W8A8) runs static quant + scaled GEMM at ``M > 1``;
-    without it ``M > 1`` runs weight-only. ``M == 1`` always runs the GEMV.
-    ``uniform_scale`` lets a piecewise-constant ``[N]`` scale collapse to a scalar.
+    With ``input_scale`` (static W8A8), ``M > 1`` quantizes the activation with it and
+    runs the scaled GEMM; otherwise every ``M`` stays weight-only. ``uniform_scale``
+    declares a piecewise-constant ``[N]`` scale, which the GEMM then takes as a scalar.
     """
-    _validate_activation(x)
-    lead, inner, rows, x2d = _flatten_activation(x)
-    _validate_dense_weight(weight, inner)
-    columns = int(weight.shape[0])
-    validate_bias(bias, x2d, columns, reference_name="x")
-    scale = weight_scale
-    if uniform_scale and scale.numel() > 1:
-        scale = scale.reshape(-1)[0]
-    if rows == 1 or input_scale is None:
-        result = _weight_only(x2d, weight, weight_scale, block_size_y=columns if weight_scale.numel() == 1 else 1,
-                              block_size_x=inner, scale_dtype="float32")
-        return _finish(result, lead, bias)
-    quantized = static_quant_fp8(x2d, input_scale)
-    result = fp8_scaled_mm(quantized, weight.t(), input_scale.reshape(()), scale, bias=bias,
-                           out=_output(x2d, columns), backend="auto")
-    return _finish(result, lead, None)
+    act = _Activation.of(x, weight, bias)
+    if act.rows == 1 or input_scale is None:
+        return act.shaped(act.channel_scaled(weight, weight_scale), bias)
+    gemm_scale = weight_scale.reshape(-1)[0] if uniform_scale and weight_scale.numel() > 1 else weight_scale
+    result = fp8_scaled_mm(static_quant_fp8(act.matrix, input_scale), weight.t(), input_scale.reshape(()),
+                           gemm_scale, bias=bias, out=act.empty_output(), backend="auto")
+    return act.shaped(result)
 
 
 def fp8_rowwise_linear(
@@ -117,20 +134,14 @@ def fp8_rowwise_linear(
     weight_scale: torch.Tensor,
     bias: torch.Tensor | None = None,
 ) -> torch.Tensor:
-    """``x @ (weight * weight_scale)^T`` with dynamic per-token W8A8 at ``M > 1``."""
-    _validate_activation(x)
-    lead, inner, rows, x2d = _flatten_activation(x)
-    _validate_dense_weight(weight, inner)
-    columns = int(weight.shape[0])
-    validate_bias(bias, x2d, columns, reference_name="x")
-    if rows == 1:
-        result = _weight_only(x2d, weight, weight_scale, block_size_y=columns if weight_scale.numel() == 1 else 1,
-                              block_size_x=inner, scale_dtype="float32")
-        return _finish(result, lead, bias)
-    quantized, activation_scale = per_token_quant_fp8(x2d)
-    result = fp8_scaled_mm(quantized, weight.t(), activation_scale, weight_scale, bias=bias,
-                           out=_output(x2d, columns), backend="auto")
-    return _finish(result, lead, None)
+    """``x @ (weight * weight_scale)^T``; ``M > 1`` quantizes the activation per token."""
+    act = _Activation.of(x, weight, bias)
+    if act.rows == 1:
+        return act.shaped(act.channel_scaled(weight, weight_scale), bias)
+    quantized, token_scale = per_token_quant_fp8(act.matrix)
+    result = fp8_scaled_mm(quantized, weight.t(), token_scale, weight_scale, bias=bias, out=act.empty_output(),
+                           backend="auto")
+    return act.shaped(result)
 
 
 def fp8_block_linear(
@@ -139,19 +150,14 @@ def fp8_block_linear(
     weight_scale: torch.Tensor,
     bias: torch.Tensor | None = None,
 ) -> torch.Tensor:
-    """``x @ dequant(weight)^T`` with ``[ceil(N/128), ceil(K/128)]`` block scales."""
-    _validate_activation(x)
-    lead, inner, rows, x2d = _flatten_activation(x)
-    _validate_dense_weight(weight, inner)
-    columns = int(weight.shape[0])
-    validate_bias(bias, x2d, columns, reference_name="x")
-    scale_dtype = "bfloat16" if weight_scale.dtype is torch.bfloat16 else "float32"
-    if rows == 1:
-        result = _weight_only(x2d, weight, weight_scale, block_size_y=_BLOCK128, block_size_x=_BLOCK128,
-                              scale_dtype=scale_dtype)
-        return _finish(result, lead, bias)
-    if inner % _BLOCK128:
-        raise ValueError(f"K={inner} must be divisible by 128 for the blockwise W8A8 path")
-    quantized, activation_scale = per_token_group_quant_fp8(x2d, _BLOCK128)
-    result = fp8_blockwise_mm(quantized, weight, activation_scale, weight_scale, bias=bias, out=_output(x2d, columns))
-    return _finish(result, lead, None)
+    """``x @ dequant(weight)^T`` with ``[ceil(N/128), ceil(K/128)]`` fp32/bf16 block scales;
+    ``M > 1`` quantizes the activation per (token, 128-K group), so K must divide by 128."""
+    act = _Activation.of(x, weight, bias)
+    if act.rows == 1:
+        scale_dtype = "bfloat16" if weight_scale.dtype is torch.bfloat16 else "float32"
+        return act.shaped(act.weight_only(weight, weight_scale, _SCALE_TILE, _SCALE_TILE, scale_dtype), bias)
+    if act.inner % _SCALE_TILE:
+        raise ValueError(f"K={act.inner} must be divisible by 128 for the blockwise W8A8 path")
+    quantized, group_scale = per_token_group_quant_fp8(act.matrix, _SCALE_TILE)
+    result = fp8_blockwise_mm(quantized, weight, group_scale, weight_scale, bias=bias, out=act.empty_output())
+    return act.shaped(result)

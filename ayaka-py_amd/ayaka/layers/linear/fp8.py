@@ -1,21 +1,24 @@
 """Dense FP8 linear quantization methods and checkpoint scale loading.
 
-Drop-in for the reference's ``python/ayaka/layers/linear/fp8.py`` (``:67-664``):
-same classes, constructor arguments, parameter names / shapes / dtypes / NaN
-(or 0xFF) sentinels, loader hooks and error messages.
+Drop-in for the reference's ``python/ayaka/layers/linear/fp8.py`` (``:67-664``). The
+public surface is the reference's: class names, constructor arguments, parameter
+names / shapes / dtypes / sentinels (NaN, or 0xFF for UE8M0), the packed-projection
+scale loader and every error message. The structure is this module's own:
 
-* ``create_weights`` allocates the ``[N, K]`` e4m3 weight and the recipe's scale
-  parameters, named as checkpoints ship them (``weight_scale``,
-  ``weight_scale_inv``, ``input_scale``) and filled with sentinels so a missing
-  checkpoint tensor can never act as a scale;
-* ``process_weights_after_loading`` rejects unloaded, non-finite, zero and negative
-  scales (0xFF for UE8M0) once per layer;
-* ``apply`` runs the recipe on the gfx950 HIP operators of ``ayaka.kernel.hip``.
+* each method *declares* its scale parameters as ``_ScaleSlot`` records (name, shape
+  rule, dtype, sentinel, how a loaded value is checked); one generic routine creates
+  them and one validates them after loading, in declaration order;
+* the scale loader first resolves *where* a checkpoint tensor goes (the whole
+  parameter, one projection's entry, or one projection's rows / 128-row blocks) and
+  then writes it with one broadcasting rule;
+* ``apply`` hands the activation to the recipe's entry point in
+  ``ayaka.kernel.hip`` (gfx950 HIP kernels).
 """
 
 from __future__ import annotations
 
 from collections.abc import Callable, Mapping
+from dataclasses import dataclass
 from typing import Any, ClassVar, Literal, cast
 
 import torch
@@ -37,127 +40,174 @@ from ayaka.weights.spec import FP8Recipe
 
 FP8 = torch.float8_e4m3fn
 BLOCK128 = 128
+UE8M0_UNSET = 0xFF  # the UE8M0 NaN code doubles as the "not loaded" sentinel
 
 ActivationScheme = Literal["dynamic", "static", "weight_only"]
 _ACTIVATION_SCHEMES: tuple[str, ...] = ("dynamic", "static", "weight_only")
 
-#: layer construction attributes that are not copied onto the weight parameter
-_WEIGHT_ATTR_EXCLUSIONS = frozenset(
+#: layer construction attributes that stay on the layer, not on the weight parameter
+_LAYER_ONLY_ATTRS = frozenset(
     {"output_partition_sizes", "input_size_per_partition", "input_size", "output_size", "params_dtype", "device"}
 )
 
+_SCALE_DTYPE_NAMES = {torch.uint8: "e8m0", torch.float32: "float32", torch.bfloat16: "bfloat16"}
 
+
+# ------------------------------------------------------------------ scale checks
 def _not_loaded(name: str) -> ValueError:
     return ValueError(f"{name} not loaded from the checkpoint")
 
 
-def _require_loaded_scale(name: str, tensor: torch.Tensor) -> None:
-    """Reject a scale that is absent (NaN sentinel), non-finite, or non-positive."""
+def _check_float_scale(name: str, tensor: torch.Tensor) -> None:
+    """A float scale must be loaded (no NaN sentinel left), finite and positive."""
     if tensor.is_meta:
         raise _not_loaded(name)
     values = tensor.detach().float()
-    if bool(torch.isnan(values).any().item()):
-        raise _not_loaded(name)
-    if not bool(torch.isfinite(values).all().item()):
+    finite = torch.isfinite(values)
+    if not bool(finite.all().item()):
+        if bool(torch.isnan(values).any().item()):
+            raise _not_loaded(name)
         raise ValueError(f"{name} must be finite; found an infinite checkpoint value")
-    if bool((values <= 0).any().item()):
+    if not bool((values > 0).all().item()):
         raise ValueError(f"{name} must be positive; found a zero or negative checkpoint value")
 
 
+def _check_code_scale(name: str, tensor: torch.Tensor) -> None:
+    """A UE8M0 scale is loaded once no 0xFF code (sentinel and NaN code) is left."""
+    if tensor.is_meta or bool(tensor.eq(UE8M0_UNSET).any().item()):
+        raise _not_loaded(name)
+
+
+@dataclass(frozen=True)
+class _ScaleSlot:
+    """One checkpoint scale parameter of a method."""
+
+    name: str
+    shape: tuple[int, ...]
+    dtype: torch.dtype
+    check: Callable[[str, torch.Tensor], None]
+
+    @property
+    def sentinel(self) -> float | int:
+        return UE8M0_UNSET if self.dtype is torch.uint8 else float("nan")
+
+
 # ------------------------------------------------------------------ scale loader
+def _layout_of(layer: nn.Module) -> Any:
+    return getattr(layer, "layout", None)
+
+
 def _projection_names(layer: nn.Module) -> tuple[str, ...]:
-    layout = getattr(layer, "layout", None)
+    """Logical projection names of a packed layer (``layout.names``, else the names of
+    ``layout.parts``); empty for an unpacked layer."""
+    layout = _layout_of(layer)
     if layout is None:
         return ()
-    names = getattr(layout, "names", None)
-    if names:
-        return tuple(str(n) for n in names)
-    return tuple(p if isinstance(p, str) else str(p.name) for p in getattr(layout, "parts", ()))
+    declared = getattr(layout, "names", None)
+    if declared:
+        return tuple(map(str, declared))
+    return tuple(part if isinstance(part, str) else str(part.name) for part in getattr(layout, "parts", ()))
 
 
-def _parts_are_names(layer: nn.Module) -> bool:
-    layout = getattr(layer, "layout", None)
-    parts = getattr(layout, "parts", ()) if layout is not None else ()
-    return bool(parts) and all(isinstance(p, str) for p in parts)
+def _parts_are_plain_names(layer: nn.Module) -> bool:
+    layout = _layout_of(layer)
+    parts = () if layout is None else getattr(layout, "parts", ())
+    return len(parts) > 0 and all(isinstance(part, str) for part in parts)
 
 
-def _locate_projection(layer: nn.Module, shard_id: object) -> tuple[int, int, int]:
-    """``(index, row_start, row_stop)`` of one projection inside the packed output."""
-    layout = getattr(layer, "layout", None)
+def _projection_span(layer: nn.Module, shard_id: object) -> tuple[int, int, int]:
+    """``(position, first_row, end_row)`` of the projection ``shard_id`` names; a plain-name
+    projection spans the single row at its position."""
+    layout = _layout_of(layer)
     if layout is None:
         raise WeightLoadError("scale loading requires the layer's projection layout")
     names = _projection_names(layer)
-    projection = layout[shard_id]  # type: ignore[index]
-    name = projection if isinstance(projection, str) else str(projection.name)
-    if name not in names:
-        raise WeightLoadError(f"unknown projection {name!r}; expected one of {names}")
-    index = names.index(name)
-    if isinstance(projection, str):
-        return index, index, index + 1
-    start = int(projection.local_offset)
-    return index, start, start + int(projection.local_size)
+    entry = layout[shard_id]  # type: ignore[index]
+    label = entry if isinstance(entry, str) else str(entry.name)
+    if label not in names:
+        raise WeightLoadError(f"unknown projection {label!r}; expected one of {names}")
+    position = names.index(label)
+    if isinstance(entry, str):
+        return position, position, position + 1
+    first = int(entry.local_offset)
+    return position, first, first + int(entry.local_size)
 
 
-def _assign_scale(destination: torch.Tensor, loaded: torch.Tensor, label: str) -> None:
-    if tuple(loaded.shape) == tuple(destination.shape):
-        destination.copy_(loaded)
-    elif loaded.numel() == destination.numel():
-        destination.copy_(loaded.reshape(destination.shape))
+def _scale_destination(layer: nn.Module, data: torch.Tensor, loaded: torch.Tensor, shard_id: object) -> torch.Tensor | None:
+    """The part of ``data`` one checkpoint scale is written to, or ``None`` when the
+    tensor replaces ``data`` outright (a projection-tagged tensor of the full shape)."""
+    if shard_id is None:
+        return data
+    if tuple(loaded.shape) == tuple(data.shape):
+        return None
+    names = _projection_names(layer)
+    if not names:
+        return data
+    position, first, end = _projection_span(layer, shard_id)
+    if _parts_are_plain_names(layer) and data.ndim >= 1 and data.shape[0] == len(names):
+        return data[position]
+    rows_per_scale = int(getattr(layer, "fp8_scale_block_y", 1) or 1)
+    if rows_per_scale > 1:  # 128-row block scales: the blocks the projection's rows touch
+        first, end = first // rows_per_scale, div_ceil(end, rows_per_scale)
+    if data.ndim < 1:
+        raise WeightLoadError("packed scale storage must have at least one dimension")
+    return data[first:end]
+
+
+def _write_scale(destination: torch.Tensor, loaded: torch.Tensor) -> None:
+    """Copy ``loaded`` into ``destination``: same shape or same element count copies,
+    a single value broadcasts, anything else does not fit."""
+    if loaded.numel() == destination.numel():
+        destination.copy_(loaded if loaded.shape == destination.shape else loaded.reshape(destination.shape))
     elif loaded.numel() == 1:
         destination.fill_(loaded.reshape(()))
     else:
         raise WeightLoadError(
-            f"{label}: checkpoint shape {tuple(loaded.shape)} does not fit destination shape {tuple(destination.shape)}"
+            f"scale: checkpoint shape {tuple(loaded.shape)} does not fit destination shape {tuple(destination.shape)}"
         )
 
 
 def _scale_loader(layer: nn.Module, parameter: torch.Tensor, loaded_weight: torch.Tensor, shard_id: object = None) -> None:
-    """Load one projection's scale into a (possibly packed) scale parameter.
+    """Load one checkpoint scale into a (possibly packed) scale parameter.
 
-    A per-tensor checkpoint's scalar broadcasts; a fused QKV / gate-up layer loads
-    one scale per logical projection, narrowed to that projection's rows (or its
-    128-row blocks for block scales, ``layer.fp8_scale_block_y``).
+    A scalar broadcasts over its destination; a fused QKV / gate-up layer loads one
+    scale per logical projection (``shard_id``) into that projection's entry, rows, or
+    128-row scale blocks (``layer.fp8_scale_block_y``).
     """
     if not isinstance(parameter, torch.Tensor):
         raise TypeError("parameter must be a torch.Tensor")
     if loaded_weight.is_meta:
         raise WeightLoadError("scale loading requires a materialized checkpoint tensor")
-    data = parameter.data
-    if shard_id is None or tuple(loaded_weight.shape) == tuple(data.shape):
-        if shard_id is not None:
-            data.copy_(loaded_weight)
-        else:
-            _assign_scale(data, loaded_weight, "scale")
-        return
-    names = _projection_names(layer)
-    if not names:
-        _assign_scale(data, loaded_weight, "scale")
-        return
-    index, start, stop = _locate_projection(layer, shard_id)
-    if _parts_are_names(layer) and data.ndim >= 1 and data.shape[0] == len(names):
-        destination = data[index]
+    destination = _scale_destination(layer, parameter.data, loaded_weight, shard_id)
+    if destination is None:
+        parameter.data.copy_(loaded_weight)
     else:
-        rows_per_scale = int(getattr(layer, "fp8_scale_block_y", 1) or 1)
-        if rows_per_scale > 1:
-            start, stop = start // rows_per_scale, div_ceil(stop, rows_per_scale)
-        if data.ndim < 1:
-            raise WeightLoadError("packed scale storage must have at least one dimension")
-        destination = data[start:stop]
-    _assign_scale(destination, loaded_weight, "scale")
+        _write_scale(destination, loaded_weight)
 
 
 # ------------------------------------------------------------------ methods
 class _FP8LinearMethodBase(LinearMethodBase):
-    """Shared FP8 storage creation and capability declaration."""
+    """FP8 weight storage plus the declared scale slots of a recipe."""
 
     weight_scale_name: ClassVar[str] = "weight_scale"
 
     def __init__(self, *, activation_bits: int) -> None:
         self._activation_bits = activation_bits
 
+    # -- declarations each recipe provides
+    def _scale_slots(self, total_output: int, input_size: int) -> list[_ScaleSlot]:
+        raise NotImplementedError
+
+    def _rows_per_scale(self, input_size: int) -> int:
+        return 1
+
+    def _run(self, layer: nn.Module, x: torch.Tensor, bias: torch.Tensor | None) -> torch.Tensor:
+        raise NotImplementedError
+
+    # -- shared machinery
     def get_capabilities(self) -> QuantizationCapabilities:
         return QuantizationCapabilities(
-            supported_devices=frozenset({"cpu", "cuda"}),
+            supported_devices=frozenset({"cuda"}),  # gfx950 HIP kernels only; no CPU path
             supported_act_dtypes=compute_torch_dtypes(),
             supported_targets=frozenset({QuantizationTarget.LINEAR}),
             storage_format="fp8_e4m3",
@@ -170,46 +220,45 @@ class _FP8LinearMethodBase(LinearMethodBase):
     def create_weights(self, layer: nn.Module, *weight_args: Any, **attrs: Any) -> None:
         if weight_args:
             raise TypeError("FP8 linear weight dimensions must be passed by name")
-        output_partition_sizes = attrs.get("output_partition_sizes")
+        partitions = attrs.get("output_partition_sizes")
         input_size = attrs.get("input_size_per_partition")
-        if not output_partition_sizes:
+        if not partitions:
             raise ValueError("output_partition_sizes is required for FP8 linear weights")
         if not isinstance(input_size, int) or input_size < 1:
             raise ValueError("input_size_per_partition must be a positive integer")
         device = attrs.get("device")
-        total_output = sum(int(size) for size in output_partition_sizes)
+        total_output = sum(map(int, partitions))
         weight = nn.Parameter(torch.empty(total_output, input_size, dtype=FP8, device=device), requires_grad=False)
         layer.register_parameter("weight", weight)
-        weight_attrs = {k: v for k, v in attrs.items() if k not in _WEIGHT_ATTR_EXCLUSIONS}
-        set_weight_attrs(weight, weight_attrs)
+        set_weight_attrs(weight, {key: value for key, value in attrs.items() if key not in _LAYER_ONLY_ATTRS})
         layer.fp8_total_output = total_output
         layer.fp8_input_size = input_size
         layer.fp8_scale_block_y = 1
         self.create_scale_parameters(layer, total_output, input_size, device)
 
     def create_scale_parameters(self, layer: nn.Module, total_output: int, input_size: int, device) -> None:
-        raise NotImplementedError
+        for slot in self._scale_slots(total_output, input_size):
+            param = nn.Parameter(torch.full(slot.shape, slot.sentinel, dtype=slot.dtype, device=device),
+                                 requires_grad=False)
+            layer.register_parameter(slot.name, param)
+            set_weight_attrs(param, {"weight_loader": _scale_loader})
+        layer.fp8_scale_block_y = self._rows_per_scale(input_size)
+
+    def process_weights_after_loading(self, layer: nn.Module) -> None:
+        for slot in self._scale_slots(layer.fp8_total_output, layer.fp8_input_size):
+            slot.check(slot.name, getattr(layer, slot.name))
 
     def apply(self, layer: nn.Module, *args: Any, **kwargs: Any) -> torch.Tensor:
-        raise NotImplementedError
-
-    @staticmethod
-    def _bias(args: tuple[Any, ...], kwargs: Mapping[str, Any]) -> torch.Tensor | None:
-        return cast("torch.Tensor | None", args[1] if len(args) > 1 else kwargs.get("bias"))
-
-    @staticmethod
-    def _scale_param(layer: nn.Module, name: str, shape, dtype: torch.dtype, sentinel, device) -> None:
-        param = nn.Parameter(torch.full(shape, sentinel, dtype=dtype, device=device), requires_grad=False)
-        layer.register_parameter(name, param)
-        set_weight_attrs(param, {"weight_loader": _scale_loader})
+        bias = args[1] if len(args) > 1 else kwargs.get("bias")
+        return self._run(layer, args[0], cast("torch.Tensor | None", bias))
 
 
 class FP8PerTensorLinearMethod(_FP8LinearMethodBase):
     """Per-tensor / per-output-row FP8 with static, dynamic or weight-only activation.
 
     ``"static"`` runs W8A8 with the checkpoint's ``input_scale`` at ``M > 1``;
-    ``"dynamic"`` quantizes per token at ``M > 1``; ``"weight_only"`` never
-    quantizes the activation. ``M == 1`` always runs the weight-only GEMV.
+    ``"dynamic"`` quantizes per token at ``M > 1``; ``"weight_only"`` never quantizes
+    the activation. ``M == 1`` always runs the weight-only GEMV.
     """
 
     def __init__(self, activation_scheme: ActivationScheme = "dynamic") -> None:
@@ -219,28 +268,30 @@ class FP8PerTensorLinearMethod(_FP8LinearMethodBase):
         super().__init__(activation_bits=16 if scheme == "weight_only" else 8)
         self.activation_scheme: ActivationScheme = cast(ActivationScheme, scheme)
 
-    def create_scale_parameters(self, layer, total_output, input_size, device) -> None:
-        self._scale_param(layer, "weight_scale", (total_output,), torch.float32, float("nan"), device)
+    def _scale_slots(self, total_output, input_size):
+        slots = [_ScaleSlot("weight_scale", (total_output,), torch.float32, _check_float_scale)]
         if self.activation_scheme == "static":
-            self._scale_param(layer, "input_scale", (), torch.float32, float("nan"), device)
-        else:
+            slots.append(_ScaleSlot("input_scale", (), torch.float32, _check_float_scale))
+        return slots
+
+    def create_scale_parameters(self, layer, total_output, input_size, device) -> None:
+        super().create_scale_parameters(layer, total_output, input_size, device)
+        if self.activation_scheme != "static":
             layer.register_parameter("input_scale", None)
 
     def process_weights_after_loading(self, layer: nn.Module) -> None:
-        _require_loaded_scale("weight_scale", layer.weight_scale)
-        if self.activation_scheme == "static":
-            _require_loaded_scale("input_scale", layer.input_scale)
+        super().process_weights_after_loading(layer)
         scale = layer.weight_scale
-        layer._fp8_uniform_scale = bool((scale == scale[0]).all().item())
+        # A piecewise-constant [N] scale lets the static GEMM take it as a scalar.
+        layer._fp8_uniform_scale = bool(scale.eq(scale[0]).all().item())
 
-    def apply(self, layer: nn.Module, *args: Any, **kwargs: Any) -> torch.Tensor:
-        x, bias = args[0], self._bias(args, kwargs)
+    def _run(self, layer, x, bias):
+        if self.activation_scheme == "dynamic":
+            return fp8_rowwise_linear(x, layer.weight, layer.weight_scale, bias)
         if self.activation_scheme == "weight_only":
             return fp8_pertensor_linear(x, layer.weight, layer.weight_scale, bias)
-        if self.activation_scheme == "static":
-            return fp8_pertensor_linear(x, layer.weight, layer.weight_scale, bias, input_scale=layer.input_scale,
-                                        uniform_scale=bool(getattr(layer, "_fp8_uniform_scale", False)))
-        return fp8_rowwise_linear(x, layer.weight, layer.weight_scale, bias)
+        return fp8_pertensor_linear(x, layer.weight, layer.weight_scale, bias, input_scale=layer.input_scale,
+                                    uniform_scale=bool(getattr(layer, "_fp8_uniform_scale", False)))
 
 
 class FP8RowwiseLinearMethod(_FP8LinearMethodBase):
@@ -249,14 +300,11 @@ class FP8RowwiseLinearMethod(_FP8LinearMethodBase):
     def __init__(self) -> None:
         super().__init__(activation_bits=8)
 
-    def create_scale_parameters(self, layer, total_output, input_size, device) -> None:
-        self._scale_param(layer, "weight_scale", (total_output,), torch.float32, float("nan"), device)
+    def _scale_slots(self, total_output, input_size):
+        return [_ScaleSlot("weight_scale", (total_output,), torch.float32, _check_float_scale)]
 
-    def process_weights_after_loading(self, layer: nn.Module) -> None:
-        _require_loaded_scale("weight_scale", layer.weight_scale)
-
-    def apply(self, layer: nn.Module, *args: Any, **kwargs: Any) -> torch.Tensor:
-        return fp8_rowwise_linear(args[0], layer.weight, layer.weight_scale, self._bias(args, kwargs))
+    def _run(self, layer, x, bias):
+        return fp8_rowwise_linear(x, layer.weight, layer.weight_scale, bias)
 
 
 class FP8BlockLinearMethod(_FP8LinearMethodBase):
@@ -270,16 +318,15 @@ class FP8BlockLinearMethod(_FP8LinearMethodBase):
         super().__init__(activation_bits=8)
         self.scale_dtype = scale_dtype
 
-    def create_scale_parameters(self, layer, total_output, input_size, device) -> None:
+    def _scale_slots(self, total_output, input_size):
         shape = (div_ceil(total_output, BLOCK128), div_ceil(input_size, BLOCK128))
-        self._scale_param(layer, "weight_scale_inv", shape, self.scale_dtype, float("nan"), device)
-        layer.fp8_scale_block_y = BLOCK128
+        return [_ScaleSlot("weight_scale_inv", shape, self.scale_dtype, _check_float_scale)]
 
-    def process_weights_after_loading(self, layer: nn.Module) -> None:
-        _require_loaded_scale("weight_scale_inv", layer.weight_scale_inv)
+    def _rows_per_scale(self, input_size):
+        return BLOCK128
 
-    def apply(self, layer: nn.Module, *args: Any, **kwargs: Any) -> torch.Tensor:
-        return fp8_block_linear(args[0], layer.weight, layer.weight_scale_inv, self._bias(args, kwargs))
+    def _run(self, layer, x, bias):
+        return fp8_block_linear(x, layer.weight, layer.weight_scale_inv, bias)
 
 
 class FP8W8A16LinearMethod(_FP8LinearMethodBase):
@@ -290,52 +337,45 @@ class FP8W8A16LinearMethod(_FP8LinearMethodBase):
     """
 
     def __init__(self, scale_dtype: torch.dtype = torch.float32, weight_block: tuple[int, int] | None = None) -> None:
-        if scale_dtype not in (torch.float32, torch.bfloat16, torch.uint8):
+        if scale_dtype not in _SCALE_DTYPE_NAMES:
             raise ValueError("scale_dtype must be float32, bfloat16, or uint8 (UE8M0)")
-        if weight_block is not None:
-            by, bx = weight_block
-            if by < 1 or bx < 1:
-                raise ValueError("weight_block sizes must be positive")
+        if weight_block is not None and min(weight_block) < 1:
+            raise ValueError("weight_block sizes must be positive")
         super().__init__(activation_bits=16)
         self.scale_dtype = scale_dtype
         self.weight_block = weight_block
 
     def _scale_geometry(self, input_size: int) -> tuple[int, int]:
+        """(rows, columns) of weight covered by one scale: per-channel without a block."""
         return (1, input_size) if self.weight_block is None else self.weight_block
 
+    def _scale_slots(self, total_output, input_size):
+        rows, cols = self._scale_geometry(input_size)
+        check = _check_code_scale if self.scale_dtype is torch.uint8 else _check_float_scale
+        return [_ScaleSlot("weight_scale", (div_ceil(total_output, rows), div_ceil(input_size, cols)),
+                           self.scale_dtype, check)]
+
+    def _rows_per_scale(self, input_size):
+        return self._scale_geometry(input_size)[0]
+
     def create_scale_parameters(self, layer, total_output, input_size, device) -> None:
-        by, bx = self._scale_geometry(input_size)
-        sentinel: float | int = 0xFF if self.scale_dtype is torch.uint8 else float("nan")
-        self._scale_param(layer, "weight_scale", (div_ceil(total_output, by), div_ceil(input_size, bx)),
-                          self.scale_dtype, sentinel, device)
-        layer.fp8_scale_block_y = by
-        layer.fp8_weight_block = (by, bx)
+        super().create_scale_parameters(layer, total_output, input_size, device)
+        layer.fp8_weight_block = self._scale_geometry(input_size)
 
-    def process_weights_after_loading(self, layer: nn.Module) -> None:
-        scale = layer.weight_scale
-        if self.scale_dtype is torch.uint8:
-            if scale.is_meta or bool((scale == 0xFF).any().item()):
-                raise _not_loaded("weight_scale")
-        else:
-            _require_loaded_scale("weight_scale", scale)
-
-    def apply(self, layer: nn.Module, *args: Any, **kwargs: Any) -> torch.Tensor:
+    def _run(self, layer, x, bias):
         from ayaka.kernel.hip.gemm.fp8_gemv import fp8_weight_only_gemv
         from ayaka.kernel.hip.gemm.fp8_w8a16_gemm import fp8_weight_only_gemm
 
-        x = args[0]
-        inner = int(x.shape[-1])
-        by, bx = self._scale_geometry(inner)
-        scale_dtype = {torch.uint8: "e8m0", torch.float32: "float32", torch.bfloat16: "bfloat16"}[self.scale_dtype]
-        stride = div_ceil(inner, bx)
-        if x.numel() == inner:
-            result = fp8_weight_only_gemv(x.reshape(inner), layer.weight, layer.weight_scale, scale_row_stride=stride,
-                                          block_size_y=by, block_size_x=bx, scale_dtype=scale_dtype)
+        k = int(x.shape[-1])
+        rows, cols = self._scale_geometry(k)
+        geometry = dict(scale_row_stride=div_ceil(k, cols), block_size_y=rows, block_size_x=cols,
+                        scale_dtype=_SCALE_DTYPE_NAMES[self.scale_dtype])
+        # One token (any lead shape) is a GEMV and returns [N], as the reference's method.
+        if x.numel() == k:
+            out = fp8_weight_only_gemv(x.reshape(k), layer.weight, layer.weight_scale, **geometry)
         else:
-            result = fp8_weight_only_gemm(x, layer.weight, layer.weight_scale, scale_row_stride=stride,
-                                          block_size_y=by, block_size_x=bx, scale_dtype=scale_dtype)
-        bias = self._bias(args, kwargs)
-        return result + bias if bias is not None else result
+            out = fp8_weight_only_gemm(x, layer.weight, layer.weight_scale, **geometry)
+        return out if bias is None else out + bias
 
 
 class FP8Mxfp8LinearMethod(_FP8LinearMethodBase):
@@ -346,64 +386,57 @@ class FP8Mxfp8LinearMethod(_FP8LinearMethodBase):
     def __init__(self) -> None:
         super().__init__(activation_bits=8)
 
-    def create_scale_parameters(self, layer, total_output, input_size, device) -> None:
+    def _scale_slots(self, total_output, input_size):
         if input_size % self.MX_GROUP:
             raise ValueError("MXFP8 requires the weight K to be divisible by 32")
-        self._scale_param(layer, "weight_scale", (total_output, input_size // self.MX_GROUP), torch.uint8, 0xFF, device)
+        return [_ScaleSlot("weight_scale", (total_output, input_size // self.MX_GROUP), torch.uint8, _check_code_scale)]
 
-    def process_weights_after_loading(self, layer: nn.Module) -> None:
-        scale = layer.weight_scale
-        # 0xFF is both the sentinel and the UE8M0 NaN code: never a valid scale.
-        if scale.is_meta or bool((scale == 0xFF).any().item()):
-            raise _not_loaded("weight_scale")
-
-    def apply(self, layer: nn.Module, *args: Any, **kwargs: Any) -> torch.Tensor:
+    def _run(self, layer, x, bias):
         from ayaka.kernel.hip.gemm.fp8_mxfp8_gemm import mxfp8_scaled_mm
         from ayaka.kernel.hip.quant.fp8_quant import per_token_group_quant_mxfp8
 
-        x = args[0]
-        lead, inner = tuple(x.shape[:-1]), int(x.shape[-1])
-        if inner % self.MX_GROUP:
+        k = int(x.shape[-1])
+        if k % self.MX_GROUP:
             raise ValueError("MXFP8 requires the activation K to be divisible by 32")
-        x2d = x.reshape(-1, inner)
-        if not x2d.is_contiguous():
-            x2d = x2d.contiguous()
-        weight = layer.weight
-        quantized, activation_scale = per_token_group_quant_mxfp8(x2d, self.MX_GROUP)
-        out = torch.empty((x2d.shape[0], int(weight.shape[0])), dtype=x.dtype, device=x.device)
-        result = mxfp8_scaled_mm(quantized, activation_scale, weight, layer.weight_scale, self._bias(args, kwargs), out=out)
-        return result.reshape(*lead, result.shape[-1])
+        rows = x.reshape(-1, k)
+        rows = rows if rows.is_contiguous() else rows.contiguous()
+        q, codes = per_token_group_quant_mxfp8(rows, self.MX_GROUP)
+        n = int(layer.weight.shape[0])
+        out = torch.empty((rows.shape[0], n), dtype=x.dtype, device=x.device)
+        mxfp8_scaled_mm(q, codes, layer.weight, layer.weight_scale, bias, out=out)
+        return out.reshape(*x.shape[:-1], n)
 
 
 # ------------------------------------------------------------------ config
-def method_from_recipe(parsed: Any) -> QuantizeMethodBase:
-    """Dense FP8 method of a parsed checkpoint recipe (``ParsedFP8Config``)."""
-    recipe = parsed.recipe.recipe
-    return _method_for(recipe, parsed.scale_dtype, parsed.recipe.weight_block)
+_METHOD_BUILDERS: dict[FP8Recipe, Callable[[torch.dtype, Any], QuantizeMethodBase]] = {
+    FP8Recipe.W8A8_STATIC_PER_TENSOR: lambda sdt, blk: FP8PerTensorLinearMethod(activation_scheme="static"),
+    FP8Recipe.W8A8_DYNAMIC_PER_TENSOR: lambda sdt, blk: FP8PerTensorLinearMethod(activation_scheme="dynamic"),
+    FP8Recipe.W8A8_ROWWISE: lambda sdt, blk: FP8RowwiseLinearMethod(),
+    FP8Recipe.W8A8_BLOCK128: lambda sdt, blk: FP8BlockLinearMethod(scale_dtype=sdt),
+    FP8Recipe.W8A16: lambda sdt, blk: FP8W8A16LinearMethod(scale_dtype=sdt, weight_block=blk),
+    FP8Recipe.MXFP8: lambda sdt, blk: FP8Mxfp8LinearMethod(),
+}
 
 
 def _method_for(recipe: FP8Recipe, scale_dtype: torch.dtype, weight_block) -> QuantizeMethodBase:
-    if recipe is FP8Recipe.W8A8_STATIC_PER_TENSOR:
-        return FP8PerTensorLinearMethod(activation_scheme="static")
-    if recipe is FP8Recipe.W8A8_DYNAMIC_PER_TENSOR:
-        return FP8PerTensorLinearMethod(activation_scheme="dynamic")
-    if recipe is FP8Recipe.W8A8_ROWWISE:
-        return FP8RowwiseLinearMethod()
-    if recipe is FP8Recipe.W8A8_BLOCK128:
-        return FP8BlockLinearMethod(scale_dtype=scale_dtype)
-    if recipe is FP8Recipe.W8A16:
-        return FP8W8A16LinearMethod(scale_dtype=scale_dtype, weight_block=weight_block)
-    if recipe is FP8Recipe.MXFP8:
-        return FP8Mxfp8LinearMethod()
-    raise CapabilityError(
-        "quantization.fp8_recipe",
-        detail=f"recipe {recipe.value!r} has no dense linear method",
-        remedy="use the KV-cache quantization owner for cache recipes",
-    )
+    builder = _METHOD_BUILDERS.get(recipe)
+    if builder is None:
+        raise CapabilityError(
+            "quantization.fp8_recipe",
+            detail=f"recipe {recipe.value!r} has no dense linear method",
+            remedy="use the KV-cache quantization owner for cache recipes",
+        )
+    return builder(scale_dtype, weight_block)
+
+
+def method_from_recipe(parsed: Any) -> QuantizeMethodBase:
+    """Dense FP8 method of a parsed checkpoint recipe (``ParsedFP8Config``)."""
+    return _method_for(parsed.recipe.recipe, parsed.scale_dtype, parsed.recipe.weight_block)
 
 
 class FP8Config(BaseQuantization):
-    """Select a dense FP8 linear method from a validated recipe descriptor."""
+    """Select a dense FP8 linear method from a validated recipe descriptor; every
+    ``get_quant_method`` call returns a fresh method."""
 
     def __init__(
         self,
@@ -440,11 +473,12 @@ class FP8Config(BaseQuantization):
     def get_capabilities(self) -> QuantizationCapabilities:
         return self._make_method().get_capabilities()
 
+    def _ignores(self, prefix: str) -> bool:
+        return any(prefix == name or prefix.startswith(name + ".") for name in self.ignored_layers)
+
     def get_quant_method(self, layer: nn.Module, prefix: str) -> QuantizeMethodBase | None:
         del layer
-        if any(prefix == ignored or prefix.startswith(f"{ignored}.") for ignored in self.ignored_layers):
-            return None
-        return self._make_method()
+        return None if self._ignores(prefix) else self._make_method()
 
 
 __all__ = [

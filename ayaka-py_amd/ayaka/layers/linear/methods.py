@@ -13,5 +13,5 @@ class LinearMethodBase(QuantizeMethodBase):
     uses_weight_loader_v2: ClassVar[bool] = False
 
     def get_capabilities(self) -> QuantizationCapabilities:
-        return QuantizationCapabilities(supported_devices=frozenset({"cpu", "cuda"}),
+        return QuantizationCapabilities(supported_devices=frozenset({"cuda"}),
                                         supported_act_dtypes=compute_torch_dtypes())

@@ -1,22 +1,25 @@
 """FP8 checkpoint adapter: ``quantization_config`` -> explicit recipe contract.
 
-Same functions, keys, decision order and errors as the reference
-(``python/ayaka/model_loader/fp8.py:53-437``):
+The public contract is the reference's (``python/ayaka/model_loader/fp8.py:53-437``):
+function names, accepted keys and aliases, the recipe decision order, defaults
+(block-128 scales default to bf16, dynamic amax floor 1e-10) and every error message.
 
-* :func:`parse_fp8_config` detects the recipe (explicit name, then KV-only, then
-  W8A16 before any MX hint, then MXFP8, block-128, rowwise hint, static, and the
-  dynamic per-tensor default), resolves the scale dtype (block-128 defaults to
-  bf16), the amax floor (1e-10) and the calibration provenance, and returns a
-  validated :class:`ParsedFP8Config`;
-* :func:`expected_scale_keys` / :func:`validate_scale_key_set` enforce the
-  checkpoint's scale tensor names;
-* :func:`normalize_scale` inverts an inverse scale exactly once;
-* :func:`shard_scale_k` slices a block scale's K axis for one rank.
+The implementation is table-driven:
+
+* ``_Keys`` reads a mapping through alias lists (``_ALIASES``): the first alias present
+  with a non-None value wins;
+* ``_DETECTION`` is the ordered list of recipe rules -- explicit name, a check of the
+  block / scale-format hints, KV-only,
+  weight-only (before any MX hint: a W8A16 checkpoint may carry UE8M0 scales),
+  MXFP8, block-128, any other block (an error), rowwise hint, static, and the dynamic
+  per-tensor default; the first rule that fires decides;
+* ``_TRAITS`` holds each recipe's fixed facts: activation scheme, activation / weight
+  blocks, default scale dtype and the checkpoint scale tensors it ships.
 """
 
 from __future__ import annotations
 
-from collections.abc import Mapping, Sequence
+from collections.abc import Callable, Mapping, Sequence
 from dataclasses import dataclass
 from typing import Any
 
@@ -58,116 +61,182 @@ FP8_SCALE_KEY_SUFFIXES: dict[str, tuple[str, ...]] = {
     "kv_scale": ("k_scale", "v_scale"),
 }
 
+#: logical field -> the config keys that may carry it, in priority order
+_ALIASES: dict[str, tuple[str, ...]] = {
+    "recipe": ("fp8_recipe", "recipe"),
+    "algo": ("quant_algo", "quantization", "quant_method", "method"),
+    "block": ("weight_block_size", "weight_block", "weight_blocks"),
+    "activation": ("activation_scheme", "activation"),
+    "scale_format": ("scale_format", "scale_dtype", "scale_fmt"),
+    "serialized": ("is_checkpoint_fp8_serialized", "serialized"),
+    "kv_scheme": ("kv_cache_scheme", "kv_scheme"),
+    "weight_hint": ("weight_scheme", "weight_granularity", "weight_strategy"),
+    "direction": ("scale_direction",),
+    "inverse_flag": ("use_scale_inv", "scale_inv"),
+    "inverse_key": ("weight_scale_inv",),
+    "amax_floor": ("amax_floor",),
+    "calibration": ("calibration_source", "calibration", "calibrated_by"),
+    "logical_layout": ("logical_scale_layout", "scale_layout"),
+    "physical_layout": ("physical_scale_layout",),
+    "ignored": ("ignored_layers", "ignored", "exclude"),
+}
+
+#: scale-format spellings (lower case, "torch." stripped)
+_FORMAT_SPELLINGS: dict[str, FP8ScaleFormat] = {
+    **dict.fromkeys(("ue8m0", "e8m0", "uint8"), FP8ScaleFormat.UE8M0),
+    **dict.fromkeys(("bfloat16", "bf16"), FP8ScaleFormat.BF16),
+    **dict.fromkeys(("float32", "fp32", "float"), FP8ScaleFormat.FP32),
+}
 _FORMAT_OF_DTYPE = {torch.float32: FP8ScaleFormat.FP32, torch.bfloat16: FP8ScaleFormat.BF16, torch.uint8: FP8ScaleFormat.UE8M0}
-_DTYPE_OF_FORMAT = {v: k for k, v in _FORMAT_OF_DTYPE.items()}
+_DTYPE_OF_FORMAT = {fmt: dtype for dtype, fmt in _FORMAT_OF_DTYPE.items()}
 _DTYPE_ENUM_OF_FORMAT = {FP8ScaleFormat.FP32: DType.FP32, FP8ScaleFormat.BF16: DType.BF16, FP8ScaleFormat.UE8M0: DType.UINT8}
 
-_WEIGHT_ONLY = ("none", "weight_only", "weight-only")
+_WEIGHT_ONLY_SCHEMES = frozenset({"none", "weight_only", "weight-only"})
+_INVERSE_DIRECTIONS = frozenset({"inverse", "inv", "scale_inv"})
+_WEIGHT_QUANT_ALGOS = ("mxfp8", "w8a8", "w8a16")
 
 
-def _first(config: Mapping[str, Any], *keys: str, default: Any = None) -> Any:
-    """Value of the first key present with a non-None value."""
-    for key in keys:
-        value = config.get(key)
-        if value is not None:
-            return value
-    return default
+class _Keys:
+    """Alias-aware, normalising reads of one ``quantization_config`` mapping."""
+
+    def __init__(self, config: Mapping[str, Any]) -> None:
+        self._config = config
+
+    def get(self, field: str, default: Any = None) -> Any:
+        for key in _ALIASES[field]:
+            value = self._config.get(key)
+            if value is not None:
+                return value
+        return default
+
+    def text(self, field: str) -> str:
+        return str(self.get(field, "")).lower()
+
+    def block(self) -> tuple[int, int] | None:
+        value = self.get("block")
+        if value is None:
+            return None
+        if (isinstance(value, (list, tuple)) and len(value) == 2
+                and all(isinstance(v, int) and not isinstance(v, bool) for v in value)):
+            return int(value[0]), int(value[1])
+        raise ValueError(f"weight_block_size must be a (rows, K) integer pair, got {value!r}")
+
+    def scale_format(self) -> FP8ScaleFormat | None:
+        value = self.get("scale_format")
+        if value is None:
+            return None
+        fmt = _FORMAT_SPELLINGS.get(str(value).lower().replace("torch.", ""))
+        if fmt is None:
+            raise ValueError(f"unknown scale format {value!r}")
+        return fmt
+
+    def inverse_scales(self) -> bool:
+        direction = self.get("direction")
+        if direction is not None:
+            return str(direction).lower() in _INVERSE_DIRECTIONS
+        return bool(self.get("inverse_flag", False)) or bool(self.get("inverse_key", False))
 
 
-def _int_pair(value: Any, name: str) -> tuple[int, int] | None:
-    if value is None:
+# ------------------------------------------------------------------ recipe detection
+def _explicit(keys: _Keys) -> FP8Recipe | None:
+    named = keys.get("recipe")
+    if named is None:
         return None
-    if isinstance(value, (list, tuple)) and len(value) == 2 and all(
-        isinstance(v, int) and not isinstance(v, bool) for v in value
-    ):
-        return int(value[0]), int(value[1])
-    raise ValueError(f"{name} must be a (rows, K) integer pair, got {value!r}")
+    try:
+        return FP8Recipe(str(named))
+    except ValueError as error:
+        allowed = ", ".join(member.value for member in FP8Recipe)
+        raise ValueError(f"unknown fp8 recipe {named!r}; expected one of: {allowed}") from error
 
 
-def _scale_format(value: Any) -> FP8ScaleFormat | None:
-    if value is None:
+def _malformed_hints(keys: _Keys) -> FP8Recipe | None:
+    """Never decides; rejects a malformed weight block or scale format before any
+    recipe is inferred (whichever recipe the config would otherwise name)."""
+    keys.block()
+    keys.scale_format()
+    return None
+
+
+def _kv_only(keys: _Keys) -> FP8Recipe | None:
+    algo = keys.text("algo")
+    quantizes_weights = (bool(keys.text("activation")) or keys.block() is not None or bool(keys.get("serialized", False))
+                         or any(token in algo for token in _WEIGHT_QUANT_ALGOS))
+    return FP8Recipe.KV_CACHE if keys.get("kv_scheme") is not None and not quantizes_weights else None
+
+
+def _weight_only(keys: _Keys) -> FP8Recipe | None:
+    hit = keys.text("activation") in _WEIGHT_ONLY_SCHEMES or "w8a16" in keys.text("algo")
+    return FP8Recipe.W8A16 if hit else None
+
+
+def _mx(keys: _Keys) -> FP8Recipe | None:
+    hit = "mxfp8" in keys.text("algo") or keys.block() == (1, 32) or keys.scale_format() is FP8ScaleFormat.UE8M0
+    return FP8Recipe.MXFP8 if hit else None
+
+
+def _block128(keys: _Keys) -> FP8Recipe | None:
+    block = keys.block()
+    if block != (128, 128) and "block" not in keys.text("algo"):
         return None
-    token = str(value).lower().replace("torch.", "")
-    for fmt, names in ((FP8ScaleFormat.UE8M0, ("ue8m0", "e8m0", "uint8")),
-                       (FP8ScaleFormat.BF16, ("bfloat16", "bf16")),
-                       (FP8ScaleFormat.FP32, ("float32", "fp32", "float"))):
-        if token in names:
-            return fmt
-    raise ValueError(f"unknown scale format {value!r}")
+    if block != (128, 128):
+        raise ValueError("block FP8 requires weight_block_size=[128, 128]")
+    return FP8Recipe.W8A8_BLOCK128
 
 
-def _is_inverse(config: Mapping[str, Any], explicit: Any) -> bool:
-    if explicit is not None:
-        return str(explicit).lower() in ("inverse", "inv", "scale_inv")
-    return bool(_first(config, "use_scale_inv", "scale_inv", default=False)) or bool(
-        _first(config, "weight_scale_inv", default=False)
-    )
+def _other_block(keys: _Keys) -> FP8Recipe | None:
+    block = keys.block()
+    if block is not None:
+        raise ValueError(f"unsupported weight_block_size {block}; expected [128, 128] or [1, 32]")
+    return None
 
 
-def _weight_block(config: Mapping[str, Any]) -> tuple[int, int] | None:
-    return _int_pair(_first(config, "weight_block_size", "weight_block", "weight_blocks"), "weight_block_size")
+def _rowwise(keys: _Keys) -> FP8Recipe | None:
+    hit = "rowwise" in keys.text("activation") or "rowwise" in keys.text("weight_hint")
+    return FP8Recipe.W8A8_ROWWISE if hit else None
+
+
+def _static(keys: _Keys) -> FP8Recipe | None:
+    return FP8Recipe.W8A8_STATIC_PER_TENSOR if keys.text("activation") in ("static", "calibrated") else None
+
+
+#: the decision order is the contract: the first rule returning a recipe decides
+_DETECTION: tuple[Callable[[_Keys], FP8Recipe | None], ...] = (
+    _explicit, _malformed_hints, _kv_only, _weight_only, _mx, _block128, _other_block, _rowwise, _static,
+)
 
 
 def _detect_recipe(config: Mapping[str, Any]) -> FP8Recipe:
-    """Recipe of a ``quantization_config``; the order of the checks is the contract."""
-    explicit = _first(config, "fp8_recipe", "recipe")
-    if explicit is not None:
-        try:
-            return FP8Recipe(str(explicit))
-        except ValueError as error:
-            allowed = ", ".join(member.value for member in FP8Recipe)
-            raise ValueError(f"unknown fp8 recipe {explicit!r}; expected one of: {allowed}") from error
-    algo = str(_first(config, "quant_algo", "quantization", "quant_method", "method", default="")).lower()
-    block = _weight_block(config)
-    activation = str(_first(config, "activation_scheme", "activation", default="")).lower()
-    fmt = _scale_format(_first(config, "scale_format", "scale_dtype", "scale_fmt"))
-    serialized = bool(_first(config, "is_checkpoint_fp8_serialized", "serialized", default=False))
-    kv_scheme = _first(config, "kv_cache_scheme", "kv_scheme")
-    weight_quant = bool(activation) or block is not None or serialized or any(
-        token in algo for token in ("mxfp8", "w8a8", "w8a16"))
-    if kv_scheme is not None and not weight_quant:
-        return FP8Recipe.KV_CACHE
-    # weight-only first: a W8A16 checkpoint may carry UE8M0 scales and a weight block
-    if activation in _WEIGHT_ONLY or "w8a16" in algo:
-        return FP8Recipe.W8A16
-    if "mxfp8" in algo or block == (1, 32) or fmt is FP8ScaleFormat.UE8M0:
-        return FP8Recipe.MXFP8
-    if block == (128, 128) or "block" in algo:
-        if block != (128, 128):
-            raise ValueError("block FP8 requires weight_block_size=[128, 128]")
-        return FP8Recipe.W8A8_BLOCK128
-    if block is not None:
-        raise ValueError(f"unsupported weight_block_size {block}; expected [128, 128] or [1, 32]")
-    hint = str(_first(config, "weight_scheme", "weight_granularity", "weight_strategy", default="")).lower()
-    if "rowwise" in activation or "rowwise" in hint:
-        return FP8Recipe.W8A8_ROWWISE
-    if activation in ("static", "calibrated"):
-        return FP8Recipe.W8A8_STATIC_PER_TENSOR
+    keys = _Keys(config)
+    for rule in _DETECTION:
+        recipe = rule(keys)
+        if recipe is not None:
+            return recipe
     return FP8Recipe.W8A8_DYNAMIC_PER_TENSOR
 
 
-def _scale_dtype(recipe: FP8Recipe, fmt: FP8ScaleFormat | None) -> torch.dtype:
-    if recipe is FP8Recipe.KV_CACHE:
-        return torch.float32
-    if recipe is FP8Recipe.MXFP8:
-        return torch.uint8
-    if fmt is not None:
-        return _DTYPE_OF_FORMAT[fmt]
-    return torch.bfloat16 if recipe is FP8Recipe.W8A8_BLOCK128 else torch.float32
+# ------------------------------------------------------------------ per-recipe facts
+@dataclass(frozen=True)
+class _RecipeTraits:
+    scheme: FP8ActivationScheme
+    activation_block: tuple[int, int] | None = None
+    weight_block: tuple[int, int] | None = None
+    default_scale: torch.dtype = torch.float32
+    fixed_scale: torch.dtype | None = None  # the recipe admits no other scale dtype
+    scale_keys: tuple[str, ...] = ("weight_scale",)
 
 
-def _activation_scheme(recipe: FP8Recipe) -> FP8ActivationScheme:
-    return {FP8Recipe.W8A16: FP8ActivationScheme.NONE,
-            FP8Recipe.W8A8_STATIC_PER_TENSOR: FP8ActivationScheme.STATIC,
-            FP8Recipe.KV_CACHE: FP8ActivationScheme.CALIBRATED}.get(recipe, FP8ActivationScheme.DYNAMIC)
-
-
-def _blocks(recipe: FP8Recipe):
-    if recipe is FP8Recipe.W8A8_BLOCK128:
-        return (1, 128), (128, 128)
-    if recipe is FP8Recipe.MXFP8:
-        return (1, 32), (1, 32)
-    return None, None
+_DYNAMIC = FP8ActivationScheme.DYNAMIC
+_TRAITS: dict[FP8Recipe, _RecipeTraits] = {
+    FP8Recipe.W8A8_STATIC_PER_TENSOR: _RecipeTraits(FP8ActivationScheme.STATIC, scale_keys=("weight_scale", "input_scale")),
+    FP8Recipe.W8A8_DYNAMIC_PER_TENSOR: _RecipeTraits(_DYNAMIC),
+    FP8Recipe.W8A8_ROWWISE: _RecipeTraits(_DYNAMIC),
+    FP8Recipe.W8A8_BLOCK128: _RecipeTraits(_DYNAMIC, (1, 128), (128, 128), default_scale=torch.bfloat16,
+                                           scale_keys=("weight_scale_inv",)),
+    FP8Recipe.MXFP8: _RecipeTraits(_DYNAMIC, (1, 32), (1, 32), fixed_scale=torch.uint8),
+    FP8Recipe.W8A16: _RecipeTraits(FP8ActivationScheme.NONE),
+    FP8Recipe.KV_CACHE: _RecipeTraits(FP8ActivationScheme.CALIBRATED, fixed_scale=torch.float32,
+                                      scale_keys=("k_scale", "v_scale")),
+}
 
 
 @dataclass(frozen=True, slots=True)
@@ -194,42 +263,36 @@ def parse_fp8_config(config: Mapping[str, Any]) -> ParsedFP8Config:
     if not isinstance(config, Mapping):
         raise TypeError("quantization_config must be a mapping")
     recipe = _detect_recipe(config)
-    fmt = _scale_format(_first(config, "scale_format", "scale_dtype", "scale_fmt"))
-    if recipe is FP8Recipe.W8A8_BLOCK128 and fmt is None:
-        fmt = FP8ScaleFormat.BF16
-    scale_dtype = _scale_dtype(recipe, fmt)
-    fmt = FP8ScaleFormat.FP32 if recipe is FP8Recipe.KV_CACHE else _FORMAT_OF_DTYPE[scale_dtype]
+    keys = _Keys(config)
+    traits = _TRAITS[recipe]
+    requested = keys.scale_format()
+    if traits.fixed_scale is not None:
+        scale_dtype = traits.fixed_scale
+    else:
+        scale_dtype = _DTYPE_OF_FORMAT[requested] if requested is not None else traits.default_scale
 
-    activation_block, weight_block = _blocks(recipe)
-    if recipe is FP8Recipe.W8A16:
-        weight_block = _weight_block(config)
-    scheme = _activation_scheme(recipe)
-    if recipe not in (FP8Recipe.W8A16, FP8Recipe.KV_CACHE):
-        configured = str(_first(config, "activation_scheme", "activation", default="")).lower()
-        if configured in _WEIGHT_ONLY:
+    if traits.scheme is not FP8ActivationScheme.NONE and recipe is not FP8Recipe.KV_CACHE:
+        if keys.text("activation") in _WEIGHT_ONLY_SCHEMES:
             raise ValueError(f"recipe {recipe.value!r} requires an activation scheme, got 'none'")
+    weight_block = keys.block() if recipe is FP8Recipe.W8A16 else traits.weight_block
 
-    checkpoint_scaled = scheme in (FP8ActivationScheme.STATIC, FP8ActivationScheme.CALIBRATED) or recipe is FP8Recipe.W8A16
-    zero_policy = FP8ZeroPolicy.CHECKPOINT_SCALE if checkpoint_scaled else FP8ZeroPolicy.AMAX_FLOOR
-    amax_floor = float(_first(config, "amax_floor", default=_DYNAMIC_FLOOR)) if zero_policy is FP8ZeroPolicy.AMAX_FLOOR else None
-    calibration = (str(_first(config, "calibration_source", "calibration", "calibrated_by", default="quantization_config"))
-                   if checkpoint_scaled else None)
-    direction = FP8ScaleDirection.INVERSE if _is_inverse(config, _first(config, "scale_direction")) else FP8ScaleDirection.DEQUANT
-    layout = str(_first(config, "logical_scale_layout", "scale_layout", default="row_major"))
+    scale_from_checkpoint = traits.scheme in (FP8ActivationScheme.STATIC, FP8ActivationScheme.CALIBRATED,
+                                              FP8ActivationScheme.NONE)
+    layout = str(keys.get("logical_layout", "row_major"))
     spec = FP8RecipeSpec(
         recipe=recipe,
         value_format=FP8ValueFormat.E4M3,
-        activation_scheme=scheme,
-        activation_block=activation_block,
+        activation_scheme=traits.scheme,
+        activation_block=traits.activation_block,
         weight_block=weight_block,
-        scale_format=fmt,
-        scale_direction=direction,
+        scale_format=_FORMAT_OF_DTYPE[scale_dtype],
+        scale_direction=FP8ScaleDirection.INVERSE if keys.inverse_scales() else FP8ScaleDirection.DEQUANT,
         logical_scale_layout=layout,
-        physical_scale_layout=str(_first(config, "physical_scale_layout", default=layout)),
-        zero_policy=zero_policy,
-        amax_floor=amax_floor,
-        calibration_source=calibration,
-        excluded_layers=tuple(str(n) for n in _first(config, "ignored_layers", "ignored", "exclude", default=())),
+        physical_scale_layout=str(keys.get("physical_layout", layout)),
+        zero_policy=FP8ZeroPolicy.CHECKPOINT_SCALE if scale_from_checkpoint else FP8ZeroPolicy.AMAX_FLOOR,
+        amax_floor=None if scale_from_checkpoint else float(keys.get("amax_floor", _DYNAMIC_FLOOR)),
+        calibration_source=str(keys.get("calibration", "quantization_config")) if scale_from_checkpoint else None,
+        excluded_layers=tuple(str(name) for name in keys.get("ignored", ())),
     )
     quant = None if recipe is FP8Recipe.KV_CACHE else QuantSpec(
         method="fp8", weight_dtype=DType.FP8_E4M3, scale_dtype=_DTYPE_ENUM_OF_FORMAT[spec.scale_format], fp8_recipe=spec)
@@ -242,37 +305,32 @@ def recipe_from_config(config: Mapping[str, Any]) -> tuple[FP8Recipe, torch.dtyp
     return parsed.recipe.recipe, parsed.scale_dtype, parsed.ignored_layers
 
 
+# ------------------------------------------------------------------ scale tensors
 def expected_scale_keys(recipe: FP8Recipe) -> tuple[str, ...]:
     """Scale tensor kinds a checkpoint of ``recipe`` must ship."""
-    if recipe is FP8Recipe.KV_CACHE:
-        return ("k_scale", "v_scale")
-    if recipe not in FP8Recipe:
+    traits = _TRAITS.get(recipe)
+    if traits is None:
         raise ValueError(f"unknown FP8 recipe {recipe!r}")
-    keys = ["weight_scale_inv" if recipe is FP8Recipe.W8A8_BLOCK128 else "weight_scale"]
-    if recipe is FP8Recipe.W8A8_STATIC_PER_TENSOR:
-        keys.append("input_scale")
-    return tuple(keys)
+    return traits.scale_keys
 
 
 def classify_scale_key(key: str) -> str | None:
     """Scale kind carried by a checkpoint tensor name, or None."""
-    leaf = key.rsplit(".", 1)[-1]
-    for kind, suffixes in FP8_SCALE_KEY_SUFFIXES.items():
-        if leaf in suffixes:
-            return kind
-    return None
+    leaf = key.rpartition(".")[2]
+    return next((kind for kind, suffixes in FP8_SCALE_KEY_SUFFIXES.items() if leaf in suffixes), None)
 
 
 def validate_scale_key_set(keys: Sequence[str], recipe: FP8Recipe) -> None:
     """Reject a checkpoint whose scale tensors do not match ``recipe``."""
-    present = {classify_scale_key(k) for k in keys} - {None}
+    present = {kind for kind in map(classify_scale_key, keys) if kind is not None}
     expected = set(expected_scale_keys(recipe))
     missing = expected - present
     if missing:
         raise ValueError(f"{recipe.value} checkpoint is missing scale tensors: {sorted(missing)}")
-    for kind in present:
-        if kind not in expected and kind != "kv_scale":
-            raise ValueError(f"{recipe.value} checkpoint carries an unexpected scale tensor kind {kind!r}")
+    unexpected = present - expected - {"kv_scale"}
+    if unexpected:
+        kind = next(iter(unexpected))
+        raise ValueError(f"{recipe.value} checkpoint carries an unexpected scale tensor kind {kind!r}")
 
 
 def normalize_scale(scale: torch.Tensor, *, direction: FP8ScaleDirection) -> torch.Tensor:
@@ -280,7 +338,7 @@ def normalize_scale(scale: torch.Tensor, *, direction: FP8ScaleDirection) -> tor
     if scale.dtype is torch.uint8 or direction is FP8ScaleDirection.DEQUANT:
         return scale
     values = scale.float()
-    if not bool(torch.isfinite(values).all().item()) or bool((values <= 0).any().item()):
+    if not (bool(torch.isfinite(values).all().item()) and bool((values > 0).all().item())):
         raise ValueError("inverse scale must be finite and positive")
     return 1.0 / scale
 
@@ -295,13 +353,11 @@ def shard_scale_k(scale: torch.Tensor, *, rank: int, world_size: int, block: int
         raise ValueError("block must be positive")
     if scale.ndim != 2:
         raise ValueError("scale must be 2-D [rows, K / block]")
-    columns = int(scale.shape[1])
-    if columns % world_size:
-        raise ValueError(f"scale K blocks {columns} must divide by world_size={world_size}")
-    if world_size == 1:
-        return scale
-    local = columns // world_size
-    return scale[:, rank * local:(rank + 1) * local]
+    blocks = int(scale.shape[1])
+    if blocks % world_size:
+        raise ValueError(f"scale K blocks {blocks} must divide by world_size={world_size}")
+    per_rank = blocks // world_size
+    return scale if world_size == 1 else scale.narrow(1, rank * per_rank, per_rank)
 
 
 def scale_blocks_for_k(inner: int, block: int) -> int:

@@ -1319,8 +1319,10 @@ size_t scaled_split_workspace(int64_t M, int64_t N, int64_t K) {
   }
   return split > 1 ? (size_t)split * (size_t)M * (size_t)N * sizeof(float) : 0;
 }
+// Mirrors launch_gemm<MODE_BLOCK>: up to 64 rows the general kernel's split (any N);
+// above, the 128 x 128 kernel's split when N allows that kernel (else no split).
 size_t block_split_workspace(int64_t M, int64_t N, int64_t K) {
-  const int64_t split = M <= 64 ? general_split(M, N, K) : block_split(M, N, K);
+  const int64_t split = M <= 64 ? general_split(M, N, K) : (N >= kBlkTile ? block_split(M, N, K) : 1);
   return split > 1 ? (size_t)split * (size_t)M * (size_t)N * sizeof(float) : 0;
 }
 
@@ -1609,7 +1611,8 @@ int launch_big(GemmArgs g, hipStream_t st, const char* op) {
       hipLaunchKernelGGL((fp8_gemm_mx128_kernel<MODE>), dim3((unsigned)tiles), dim3(kThreads), 0, st, g);
     }
   } else if (g.K % (2 * kBigK) == 0) {
-    const int64_t split = row_scaled(MODE) ? scaled_split(g.M, g.N, g.K, kBigTile, kBigTile) : 1;
+    // INT8 never splits: a split's partial would leave the exact int32 accumulator.
+    const int64_t split = MODE == MODE_SCALED ? scaled_split(g.M, g.N, g.K, kBigTile, kBigTile) : 1;
     g.kps = 0;
     if (split > 1) {
       const size_t need = (size_t)split * (size_t)g.M * (size_t)g.N * sizeof(float);
@@ -1654,8 +1657,8 @@ int launch_cfg(GemmArgs g, hipStream_t st, const char* op) {
   g.tiles_m = (int)cdiv(g.M, BM);
   const int64_t tiles = (int64_t)g.tiles_m * cdiv(g.N, BN);
   if (tiles > 0x7FFFFFFF) return fail(AYK_EINVAL, "%s: problem too large", op);
-  const int64_t split = MODE == MODE_BLOCK && BM <= 64 ? general_split(g.M, g.N, g.K)
-                        : (MODE != MODE_BLOCK ? scaled_split(g.M, g.N, g.K, BM, BN) : 1);
+  const int64_t split = MODE == MODE_BLOCK ? (BM <= 64 ? general_split(g.M, g.N, g.K) : 1)
+                        : (MODE == MODE_INT8 ? 1 : scaled_split(g.M, g.N, g.K, BM, BN));
   g.kps = 0;
   if (split > 1) {
     const size_t need = (size_t)split * (size_t)g.M * (size_t)g.N * sizeof(float);
@@ -1754,8 +1757,8 @@ int ayk_fp8_scaled_mm(const void* a, int64_t lda, const void* b, int64_t ldb, in
 }
 
 size_t ayk_int8_scaled_mm_workspace_bytes(int64_t M, int64_t N, int64_t K) {
-  if (M < 1 || N < 1 || K < 1) return 0;
-  return scaled_split_workspace(M, N, K);
+  (void)M; (void)N; (void)K;
+  return 0;  // the INT8 GEMM never splits K (its int32 sums stay exact)
 }
 
 int ayk_int8_scaled_mm(const void* a, int64_t lda, const void* b, int64_t ldb, int64_t M, int64_t N,
@@ -1782,7 +1785,7 @@ int ayk_int8_scaled_mm(const void* a, int64_t lda, const void* b, int64_t ldb, i
 }
 
 size_t ayk_fp8_blockwise_mm_workspace_bytes(int64_t M, int64_t N, int64_t K) {
-  if (M < 1 || N < kBlkTile || K < 1 || K % 128) return 0;
+  if (M < 1 || N < 1 || K < 1 || K % 128) return 0;
   return block_split_workspace(M, N, K);
 }
 

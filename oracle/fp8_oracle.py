@@ -130,7 +130,7 @@ def fp8_blockwise_mm(a, b, scale_a, scale_b, bias=None, a_scale_col_major: bool 
     n = b.shape[0]
     af, bf = a.float(), b.float()
     saf, sbf = scale_a.float(), scale_b.float()
-    y = torch.zeros((m, n), dtype=torch.float32)
+    y = torch.zeros((m, n), dtype=torch.float32, device=a.device)
     for kb in range(-(-k // SCALE_BLOCK)):
         lo, hi = kb * SCALE_BLOCK, min((kb + 1) * SCALE_BLOCK, k)
         part = af[:, lo:hi] @ bf[:, lo:hi].t()
@@ -183,8 +183,8 @@ def _w8a16_scale_matrix(weight_scale, n, k, scale_row_stride, by, bx, scale_dtyp
     stride = -(-k // bx) if scale_row_stride is None else int(scale_row_stride)
     vals = e8m0_values(weight_scale) if scale_dtype == "e8m0" else weight_scale
     vals = vals.to(dtype).reshape(-1)
-    rows = torch.arange(n) // by
-    cols = torch.arange(k) // bx
+    rows = torch.arange(n, device=vals.device) // by
+    cols = torch.arange(k, device=vals.device) // bx
     return vals[rows[:, None] * stride + cols[None, :]]
 
 
@@ -214,7 +214,7 @@ def fp8_blockwise_gemv(a, b, scale_a, scale_b, bias=None) -> torch.Tensor:
     n = b.shape[0]
     av, bv = a.reshape(-1).double(), b.double()
     sa, sb = scale_a.reshape(-1).double(), scale_b.double()
-    y = torch.zeros(n, dtype=torch.float64)
+    y = torch.zeros(n, dtype=torch.float64, device=av.device)
     for kb in range(-(-k // SCALE_BLOCK)):
         lo, hi = kb * SCALE_BLOCK, min((kb + 1) * SCALE_BLOCK, k)
         part = av[lo:hi] @ bv[:, lo:hi].t()

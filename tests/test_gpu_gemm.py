@@ -245,6 +245,8 @@ def test_fp8_blockwise_mm(gpu, m, n, k, sdt, col_major):
     (7, 256, 2048, False, torch.float16, False),      # split 2, 7 rows
     (256, 2048, 7168, False, torch.float32, False),   # DeepSeek-V3 K, split 4
     (32, 7168, 18432, False, torch.float32, True),    # DeepSeek-V3 (7168, 18432) at M = 32, split 16
+    (16, 64, 4096, False, torch.float32, False),      # N < 128: general kernel split 4
+    (40, 96, 8192, True, torch.bfloat16, True),       # N < 128, 64-row tiles: split 8
 ])
 def test_fp8_blockwise_mm_split_k(gpu, m, n, k, col_major, sdt, with_bias):
     """Launches with too few 128 x 128 tiles split K over fp32 partials (the workspace the
@@ -286,6 +288,70 @@ def test_mxfp8_scaled_mm(gpu, m, n, k):
     out = torch.empty(m, n, dtype=torch.bfloat16, device=gpu)
     mxfp8_scaled_mm(qa.to(gpu), ca.to(gpu), qw.to(gpu), cw.to(gpu), bias.to(gpu), out=out)
     assert_linear_close(out, ref, "mxfp8_scaled_mm")
+
+
+# Kernel routes for the code-edge cases: M = 1 GEMV, general kernel, 256 x 256 pair
+# kernel unsplit and split over K, and the 128-K-stage kernel (K % 512 != 0).
+MX_EDGE = [(1, 512, 2048), (100, 300, 1024), (1024, 1024, 512), (512, 2048, 4096), (512, 512, 640)]
+
+
+def _mx_edge_operands(m, n, k):
+    torch.manual_seed(m + n + k + 7)
+    x = torch.distributions.StudentT(3.0).sample((m, k))
+    x[:, 32:64] = 0.0  # an all-zero activation group: the quantizer's code 0 with q = 0
+    wf = torch.randn(n, k, generator=_gen(51))
+    qa, ca = ora.per_token_group_quant_mxfp8(x, 32)
+    qw, cw = ora.per_token_group_quant_mxfp8(wf, 32)
+    assert (ca[:, 1] == 0).all()
+    return qa, ca, qw, cw
+
+
+@pytest.mark.parametrize("m,n,k", MX_EDGE)
+def test_mxfp8_code_zero_weight_scales(gpu, m, n, k):
+    """UE8M0 code 0 on nonzero weights. The reference decodes it as +0.0
+    (reference/gemm.py:11-14, bits c << 23), so such a group adds nothing; the scaled
+    MFMA reads it as 2^-127, so the group adds at most 32 * 448 * 448 * 2^-127 *
+    2^(ca - 127) (below 1e-30 for every activation code <= 200), far under the
+    tolerance floor. Every row and column carries some code-0 groups, and one weight
+    row is code 0 throughout, so its outputs are the bias alone in the reference."""
+    from ayaka.kernel.hip import mxfp8_scaled_mm
+
+    _say(f"mxfp8_scaled_mm code-0 weight scales m={m} n={n} k={k}")
+    qa, ca, qw, cw = _mx_edge_operands(m, n, k)
+    mask = torch.rand(cw.shape, generator=_gen(52)) < 0.2
+    cw = torch.where(mask, torch.zeros_like(cw), cw)
+    cw[3, :] = 0
+    assert (qw[3].float() != 0).any() and int(ca.max()) <= 200
+    bias = torch.randn(n, generator=_gen(53))
+    ref = ora.mxfp8_scaled_mm(qa, ca, qw, cw, bias)
+    assert torch.equal(ref[:, 3], bias[3].expand(m)), "oracle: a code-0 row contributes exactly 0"
+    out = torch.empty(m, n, dtype=torch.float32, device=gpu)
+    mxfp8_scaled_mm(qa.to(gpu), ca.to(gpu), qw.to(gpu), cw.to(gpu), bias.to(gpu), out=out)
+    assert_linear_close(out, ref, "mxfp8 code-0 weight scales")
+    assert (out[:, 3].cpu() - bias[3]).abs().max().item() < 1e-20
+
+
+@pytest.mark.parametrize("m,n,k", MX_EDGE)
+def test_mxfp8_code_ff_scales_give_nan(gpu, m, n, k):
+    """UE8M0 code 0xFF is NaN (reference fp8_compat e8m0 decode and reference/gemm.py:11-14):
+    every output whose dot product touches a 0xFF group, weight side or activation side,
+    is NaN; all other outputs are unaffected."""
+    from ayaka.kernel.hip import mxfp8_scaled_mm
+
+    _say(f"mxfp8_scaled_mm code-0xFF scales m={m} n={n} k={k}")
+    qa, ca, qw, cw = _mx_edge_operands(m, n, k)
+    cw[5, 2] = 0xFF
+    ca[m // 2, k // 32 - 1] = 0xFF
+    ref = ora.mxfp8_scaled_mm(qa, ca, qw, cw)
+    out = torch.empty(m, n, dtype=torch.float32, device=gpu)
+    mxfp8_scaled_mm(qa.to(gpu), ca.to(gpu), qw.to(gpu), cw.to(gpu), out=out)
+    y = out.cpu()
+    nan_ref = torch.isnan(ref)
+    assert nan_ref[:, 5].all() and nan_ref[m // 2, :].all()
+    assert torch.equal(torch.isnan(y), nan_ref), (
+        f"NaN pattern differs: kernel {int(torch.isnan(y).sum())} NaNs, oracle {int(nan_ref.sum())}")
+    keep = ~nan_ref
+    assert_linear_close(y[keep], ref[keep], "mxfp8 0xFF: finite outputs")
 
 
 @pytest.mark.parametrize("m", [4, 16, 32, 100])
@@ -423,19 +489,24 @@ def test_int8_scaled_mm_integer_sum_is_exact(gpu, m, n, k):
 
 
 @pytest.mark.parametrize("m,n,k", [(512, 768, 8192), (40, 768, 8192)])
-def test_int8_scaled_mm_split_k_is_exact(gpu, m, n, k):
-    """Launches short of one round of tiles split K (256x256 kernel, general kernel):
-    with operands in [-8, 8) every partial and the total stay below 2^24, so the fp32
-    split sum equals the integer product exactly, with unit scales."""
+def test_int8_scaled_mm_short_launch_is_exact(gpu, m, n, k):
+    """Launches short of one round of tiles (which split K for the fp8 recipes) keep
+    the INT8 GEMM unsplit: no workspace, and with full-range int8 operands (sums far
+    above 2^24) the fp32 output is the exact int32 sum rounded once, as torch's
+    int32 -> float32 conversion of the reference's int32 accumulator
+    (gemm/int8_gemm.py:70-81)."""
     from ayaka.kernel.hip import _lib, int8_scaled_mm
 
-    _say(f"int8_scaled_mm split-K exact m={m} n={n} k={k}")
-    assert _lib.query("ayk_int8_scaled_mm_workspace_bytes", m, n, k) > 0, "shape should split"
-    a = torch.randint(-8, 8, (m, k), generator=_gen(41), dtype=torch.int8)
-    w = torch.randint(-8, 8, (n, k), generator=_gen(42), dtype=torch.int8)
+    _say(f"int8_scaled_mm short launch exact m={m} n={n} k={k}")
+    assert _lib.query("ayk_int8_scaled_mm_workspace_bytes", m, n, k) == 0, "INT8 must not split K"
+    a = torch.randint(-128, 128, (m, k), generator=_gen(41), dtype=torch.int8)
+    w = torch.randint(-128, 128, (n, k), generator=_gen(42), dtype=torch.int8)
+    a[:4, : k // 2] = 127  # a few sums of order 127^2 K / 2 = 6.6e7, far beyond 2^24
+    w[:4, : k // 2] = 127
     exact = ora.int8_matmul_exact(a, w)
+    assert exact.abs().max().item() > 2**24, "the case must exercise sums beyond fp32's integer range"
     out = int8_scaled_mm(a.to(gpu), w.to(gpu).t(), torch.ones(m, device=gpu), torch.ones(n, device=gpu), out_dtype=torch.float32)
-    assert torch.equal(out.cpu().to(torch.int64), exact)
+    assert torch.equal(out.cpu(), exact.to(torch.int32).to(torch.float32))
 
 
 def test_int8_scaled_mm_row_major_b_and_contract(gpu):

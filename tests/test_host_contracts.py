@@ -325,6 +325,9 @@ def test_c_abi_rejects_bad_arguments_without_a_gpu():
     # GEMM split-K plans: too few tiles split K, a full round does not
     assert lib.ayk_fp8_scaled_mm_workspace_bytes(512, 3584, 18944) > 0
     assert lib.ayk_fp8_scaled_mm_workspace_bytes(4096, 37888, 3584) == 0
-    assert lib.ayk_int8_scaled_mm_workspace_bytes(512, 768, 8192) > 0
+    assert lib.ayk_int8_scaled_mm_workspace_bytes(512, 768, 8192) == 0  # INT8 never splits K
+    # block-128 size query mirrors the launch: N < 128 at M <= 64 still splits K
+    assert lib.ayk_fp8_blockwise_mm_workspace_bytes(16, 64, 4096) > 0
+    assert lib.ayk_fp8_blockwise_mm_workspace_bytes(40, 96, 8192) > 0
     assert lib.ayk_fp8_blockwise_mm_workspace_bytes(32, 7168, 18432) > 0
     assert lib.ayk_fp8_blockwise_mm_workspace_bytes(4096, 18432, 7168) == 0
