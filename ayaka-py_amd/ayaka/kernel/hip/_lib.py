@@ -71,6 +71,8 @@ SIGNATURES: dict[str, list[Any]] = {
     "ayk_mxfp8_scaled_mm_workspace_bytes": [_l, _l, _l],
     "ayk_fp8_weight_only_gemv": [_p, _i, _p, _l, _l, _l, _p, _i, _l, _l, _l, _p, _p, _z, _p],
     "ayk_fp8_weight_only_gemv_workspace_bytes": [_l, _l],
+    "ayk_fp8_weight_only_gemv_static": [_p, _i, _p, _l, _l, _l, _p, _i, _l, _l, _l, _p, _p],
+    "ayk_fp8_weight_only_gemv_static_max_bytes": [],
     "ayk_fp8_weight_only_gemm": [_p, _i, _l, _l, _p, _l, _l, _l, _p, _i, _l, _l, _l, _p, _l, _p, _z, _p],
     "ayk_fp8_weight_only_gemm_workspace_bytes": [_l, _l, _l, _l],
     "ayk_fp8_blockwise_gemv": [_p, _p, _l, _l, _l, _p, _i, _p, _i, _p, _i, _p, _i, _p, _z, _p],
@@ -85,6 +87,7 @@ _RESTYPES: dict[str, Any] = {
     "ayk_int8_scaled_mm_workspace_bytes": _z,
     "ayk_mxfp8_scaled_mm_workspace_bytes": _z,
     "ayk_fp8_weight_only_gemm_workspace_bytes": _z,
+    "ayk_fp8_weight_only_gemv_static_max_bytes": _z,
 }
 
 _lock = threading.Lock()

@@ -17,6 +17,8 @@
 // so it is loaded once (L1/L2 resident) and reused R times. A K split (grid.y) is
 // used only when N alone cannot fill the 256 CUs; its fp32 partials are summed by a
 // second kernel in a fixed order, so results are deterministic.
+#include <mutex>
+
 #include "ayk_common.h"
 
 namespace ayk {
@@ -611,11 +613,67 @@ int mx_gemv(const void* a, const uint8_t* a_scale, const void* w, int64_t ldw,
   return check_launch("mxfp8_scaled_mm(M=1)");
 }
 
+// ---------------------------------------------------------------- allocation-free form
+// A file-scope device array replaces the caller's workspace for callers that cannot
+// allocate. The split plan bounds the partials: the split doubles only while
+// waves * split < 4096 with waves = ceil(N / 2), so split * N < 16384 and the partials
+// stay below 64 KiB for every shape. Each GPU holds its own copy of the array; its
+// address is looked up once per device (hipGetSymbolAddress) and only that address is
+// handed to kernels. Every split writes all N of its partials before the reduce reads
+// them, so nothing needs clearing between calls.
+constexpr size_t kScratchBytes = 64 * 1024;
+static __device__ __align__(256) float scratch[kScratchBytes / sizeof(float)];
+
+constexpr int kMaxDevices = 64;
+std::mutex g_scratch_mutex;
+float* g_scratch_ptr[kMaxDevices] = {};
+
+int scratch_of_current_device(float** out) {
+  int device = 0;
+  if (hipGetDevice(&device) != hipSuccess) return fail(AYK_EARCH, "no HIP device is available");
+  if (device < 0 || device >= kMaxDevices) return fail(AYK_EARCH, "device index %d out of range", device);
+  std::lock_guard<std::mutex> lock(g_scratch_mutex);
+  if (g_scratch_ptr[device] == nullptr) {
+    void* p = nullptr;
+    const hipError_t err = hipGetSymbolAddress(&p, HIP_SYMBOL(scratch));
+    if (err != hipSuccess || p == nullptr) {
+      return fail(AYK_ELAUNCH, "static scratch of device %d unavailable: %s", device, hipGetErrorString(err));
+    }
+    g_scratch_ptr[device] = static_cast<float*>(p);
+  }
+  *out = g_scratch_ptr[device];
+  return AYK_OK;
+}
+
 }  // namespace ayk
 
 using namespace ayk;
 
 extern "C" {
+
+int ayk_fp8_weight_only_gemv_static(const void* x, int x_dtype, const void* w, int64_t ldw, int64_t N,
+                                    int64_t K, const void* scale, int scale_dtype,
+                                    int64_t scale_row_stride, int64_t block_size_y,
+                                    int64_t block_size_x, void* out, ayk_stream_t stream) {
+  const char* op = "fp8_weight_only_gemv_static";
+  if (N > 0 && K > 0) {
+    const size_t need = gemv_workspace(ACT_BF16, AS_NONE, N, K);
+    if (need > kScratchBytes) {
+      return fail(AYK_EWORKSPACE, "%s: N=%lld K=%lld needs %zu bytes of partials, above the static scratch of %zu",
+                  op, (long long)N, (long long)K, need, kScratchBytes);
+    }
+  }
+  if (N <= 0 || K <= 0) {  // the allocating entry point reports the argument error
+    return ayk_fp8_weight_only_gemv(x, x_dtype, w, ldw, N, K, scale, scale_dtype, scale_row_stride, block_size_y,
+                                    block_size_x, out, nullptr, 0, stream);
+  }
+  float* ws = nullptr;
+  if (int rc = scratch_of_current_device(&ws)) return rc;
+  return ayk_fp8_weight_only_gemv(x, x_dtype, w, ldw, N, K, scale, scale_dtype, scale_row_stride, block_size_y,
+                                  block_size_x, out, ws, kScratchBytes, stream);
+}
+
+size_t ayk_fp8_weight_only_gemv_static_max_bytes(void) { return kScratchBytes; }
 
 size_t ayk_fp8_weight_only_gemv_workspace_bytes(int64_t N, int64_t K) { return gemv_workspace(ACT_BF16, AS_NONE, N, K); }
 size_t ayk_fp8_blockwise_gemv_workspace_bytes(int64_t N, int64_t K) { return gemv_workspace(ACT_E4M3, AS_BLOCK128, N, K); }

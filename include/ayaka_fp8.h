@@ -175,6 +175,19 @@ int ayk_fp8_weight_only_gemv(const void* x, int x_dtype, const void* w, int64_t 
                              void* workspace, size_t workspace_bytes, ayk_stream_t stream);
 size_t ayk_fp8_weight_only_gemv_workspace_bytes(int64_t N, int64_t K);
 
+/* No counterpart in the reference. ayk_fp8_weight_only_gemv without a workspace
+ * argument, for callers that cannot allocate device memory (code under HIP graph
+ * capture, serving loops, harnesses that forbid hipMalloc): the split-K partials live
+ * in a static per-device array of ayk_fp8_weight_only_gemv_static_max_bytes() bytes
+ * (64 KiB, enough for every shape; a shape needing more is rejected with
+ * AYK_EWORKSPACE). Allocates nothing. All calls on one GPU share that array, so calls
+ * that overlap on one GPU (different streams, or host threads) race. */
+int ayk_fp8_weight_only_gemv_static(const void* x, int x_dtype, const void* w, int64_t ldw,
+                                    int64_t N, int64_t K, const void* scale, int scale_dtype,
+                                    int64_t scale_row_stride, int64_t block_size_y,
+                                    int64_t block_size_x, void* out, ayk_stream_t stream);
+size_t ayk_fp8_weight_only_gemv_static_max_bytes(void);
+
 /* Replaces ayaka::fp8_weight_only_gemm (gemm/fp8_w8a16_gemm.py:144; oracle
  * reference/gemm.py:95-126). The [M, K] form of ayk_fp8_weight_only_gemv; out dtype ==
  * x dtype. Each dequantized weight w * scale is rounded to the activation dtype before
