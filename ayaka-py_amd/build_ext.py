@@ -48,9 +48,17 @@ def _hipcc() -> str:
     raise RuntimeError("hipcc not found (expected /opt/rocm/bin/hipcc)")
 
 
+# Per-file flags. gemm_block.hip keeps its MFMA accumulators in VGPRs: it rescales them
+# with VALU multiplies every 128-K block, which the AGPR form would turn into AGPR
+# read / multiply / write triples.
+FILE_FLAGS: dict[str, list[str]] = {
+    "gemm_block.hip": ["-mllvm", "-amdgpu-mfma-vgpr-form"],
+}
+
+
 def _compile(hipcc: str, src: pathlib.Path) -> pathlib.Path:
     obj = BUILD_DIR / (src.stem + ".o")
-    cmd = [hipcc, *HIP_FLAGS, f"-I{INCLUDE}", f"-I{CSRC}", "-c", str(src), "-o", str(obj)]
+    cmd = [hipcc, *HIP_FLAGS, *FILE_FLAGS.get(src.name, []), f"-I{INCLUDE}", f"-I{CSRC}", "-c", str(src), "-o", str(obj)]
     proc = subprocess.run(cmd, capture_output=True, text=True)
     if proc.returncode != 0:
         raise RuntimeError(f"hipcc failed on {src.name}:\n{proc.stderr}")

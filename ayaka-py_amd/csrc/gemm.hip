@@ -23,7 +23,9 @@
 // global loads are issued before the current step's MFMAs. LDS rows are padded to
 // 144 bytes so the 32 rows a wavefront reads at one K offset fall on distinct banks.
 #include "ayk_common.h"
+#include "gemm_block.h"
 #include "gemm_tiles.h"
+#include "gemm_util.h"
 
 namespace ayk {
 
@@ -369,24 +371,9 @@ __global__ __launch_bounds__(kThreads) void fp8_gemm_kernel(GemmArgs gin) {
 //    rows past M / N read zero and are never stored.
 constexpr int kBigTile = 256;
 constexpr int kBigK = 64;                         // K bytes per stage
-// Word 3 of a raw (unstructured, stride 0) buffer resource on gfx9-family GPUs.
-constexpr int kBufferFlags = 0x00020000;
 constexpr int kBigStage = 2 * kBigTile * kBigK;   // weights + activations of one stage, bytes
 constexpr int kEpilogueLds = 64 * 1024;           // epilogue staging tile (first stage object)
 
-// s_waitcnt with only the vector-memory count constrained (gfx9 encoding: vmcnt in
-// bits [3:0] and [15:14], expcnt [6:4] and lgkmcnt [11:8] left at their maxima).
-template <int N>
-__device__ inline void wait_vmcnt() {
-  static_assert(N >= 0 && N < 64, "vmcnt range");
-  __builtin_amdgcn_s_waitcnt((N & 15) | ((N >> 4) << 14) | (7 << 4) | (15 << 8));
-}
-// Workgroup barrier after this wavefront's LDS accesses completed (lgkmcnt(0)); unlike
-// __syncthreads it does not wait for outstanding global loads.
-__device__ inline void lds_barrier() {
-  __builtin_amdgcn_s_waitcnt(0xC07F);
-  __builtin_amdgcn_s_barrier();
-}
 
 // Four consecutive bias values n .. n+3 (n + 3 < N, n % 4 == 0) as floats.
 __device__ inline void load_bias4(const GemmArgs& g, int64_t n, float* b) {
@@ -428,15 +415,6 @@ __device__ inline void store4_typed(const GemmArgs& g, int64_t m, int64_t n, con
 template <int OUT>
 struct OutBytes { static constexpr int v = OUT == AYK_F32 ? 4 : 2; };
 
-// A raw buffer resource from wave-uniform values, forced into SGPRs: a descriptor the
-// compiler cannot prove uniform is wrapped in a readfirstlane loop at every load.
-__device__ inline __amdgpu_buffer_rsrc_t uniform_rsrc(const void* base, int32_t records) {
-  const uint64_t p = reinterpret_cast<uint64_t>(base);
-  const uint32_t lo = (uint32_t)__builtin_amdgcn_readfirstlane((int)(uint32_t)p);
-  const uint32_t hi = (uint32_t)__builtin_amdgcn_readfirstlane((int)(uint32_t)(p >> 32));
-  return __builtin_amdgcn_make_buffer_rsrc(reinterpret_cast<void*>(((uint64_t)hi << 32) | lo), (short)0,
-                                           __builtin_amdgcn_readfirstlane(records), kBufferFlags);
-}
 
 // Output scales of one lane of the 256 x 256 kernels: the activation scale of each of
 // its four m-fragment rows and the weight scales of its 64 output columns. They are
@@ -490,13 +468,6 @@ __device__ __attribute__((always_inline)) inline BigScales load_big_scales(const
   return sc;
 }
 
-// Two floats -> two bf16 (round to nearest even) in one dword, with the gfx950
-// packed converter.
-__device__ inline uint32_t pack_bf16x2(float a, float b) {
-  typedef float f2 __attribute__((ext_vector_type(2)));
-  typedef __bf16 bf2 __attribute__((ext_vector_type(2)));
-  return __builtin_bit_cast(uint32_t, __builtin_convertvector((f2{a, b}), bf2));
-}
 
 template <int MODE, int OUT, bool BIAS>
 __device__ __attribute__((always_inline)) inline void big_epilogue_impl(const GemmArgs& g, const v16f (&acc)[4][4], const BigScales& sc,
@@ -1321,8 +1292,15 @@ size_t scaled_split_workspace(int64_t M, int64_t N, int64_t K) {
 }
 // Mirrors launch_gemm<MODE_BLOCK>: up to 64 rows the general kernel's split (any N);
 // above, the 128 x 128 kernel's split when N allows that kernel (else no split).
+bool block256_wanted(int64_t M, int64_t N, int64_t K);
 size_t block_split_workspace(int64_t M, int64_t N, int64_t K) {
-  const int64_t split = M <= 64 ? general_split(M, N, K) : (N >= kBlkTile ? block_split(M, N, K) : 1);
+  int64_t split = M <= 64 ? general_split(M, N, K) : (N >= kBlkTile ? block_split(M, N, K) : 1);
+  // The 256 x 256 kernel when it takes the launch (an upper bound: alignment may still
+  // send the launch to the 128 x 128 kernel).
+  if (block256_wanted(M, N, K)) {
+    const int64_t s256 = block256_split(M, N, K);
+    split = s256 > split ? s256 : split;
+  }
   return split > 1 ? (size_t)split * (size_t)M * (size_t)N * sizeof(float) : 0;
 }
 
@@ -1676,6 +1654,27 @@ int launch_cfg(GemmArgs g, hipStream_t st, const char* op) {
   return AYK_OK;
 }
 
+// The 256 x 256 block-scaled kernel serves launches of at least half a round (128) of
+// its tiles; smaller ones keep the 128 x 128 tiles and their K split.
+bool block256_wanted(int64_t M, int64_t N, int64_t K) {
+  return K % 128 == 0 && M >= 256 && N >= 256 && cdiv(M, 256) * cdiv(N, 256) >= 128;
+}
+Block256Args block256_args(const GemmArgs& g) {
+  Block256Args b{};
+  b.a = g.a; b.lda = g.lda;
+  b.w = g.w; b.ldw = g.ldw;
+  b.M = g.M; b.N = g.N; b.K = g.K;
+  b.sa = static_cast<const float*>(g.sa);
+  b.ld_sa = g.ld_sa > 0 ? g.ld_sa : g.K / 128;
+  b.sa_col_major = g.sa_vec;
+  b.sb = g.sb; b.sb_dtype = g.sb_dtype;
+  b.ld_sb = g.ld_sb > 0 ? g.ld_sb : cdiv(g.K, 128);
+  b.bias = g.bias; b.bias_dtype = g.bias_dtype;
+  b.out = g.out; b.out_dtype = g.out_dtype; b.ldo = g.ldo;
+  b.ws = g.ws; b.ws_bytes = g.ws_bytes;
+  return b;
+}
+
 template <int MODE>
 int launch_gemm(const GemmArgs& g, hipStream_t st, const char* op) {
   // The large-tile kernels need K % 64 == 0 (128 for MXFP8), fp32 scales, N % 4 == 0 and 16-byte
@@ -1690,7 +1689,12 @@ int launch_gemm(const GemmArgs& g, hipStream_t st, const char* op) {
                       (g.bias == nullptr || (reinterpret_cast<uintptr_t>(g.bias) & 15) == 0);
   if (big_ok) return launch_big<MODE>(g, st, op);
   } else {
-    // The block-scaled large-tile kernel: K % 128 == 0, fp32 activation scales, any float
+    // The 256 x 256 block-scaled kernel from half a round of its tiles on.
+    if (g.sa_dtype == AYK_F32 && block256_wanted(g.M, g.N, g.K)) {
+      const Block256Args b = block256_args(g);
+      if (block256_supported(b)) return block256_launch(b, st, op);
+    }
+    // The block-scaled 128 x 128 kernel: K % 128 == 0, fp32 activation scales, any float
     // weight-scale dtype, and the same output / bias alignment as above.
     const int64_t out_bytes = g.out_dtype == AYK_F32 ? 4 : 2;
     // 65-127 rows also take it when the K split applies (rows past M read zeros); up to

@@ -1,0 +1,40 @@
+// Block-scaled (128 x 128 weight blocks, 1 x 128 activation groups) fp8 GEMM with
+// 256 x 256 tiles: the launcher that gemm.hip's fp8_blockwise_mm dispatch calls.
+#pragma once
+
+#include <stddef.h>
+#include <stdint.h>
+
+#include <hip/hip_runtime.h>
+
+namespace ayk {
+
+struct Block256Args {
+  const uint8_t* a;  // [M, K] e4m3, row stride lda
+  int64_t lda;
+  const uint8_t* w;  // [N, K] e4m3, row stride ldw
+  int64_t ldw;
+  int64_t M, N, K;
+  const float* sa;   // fp32 activation scales: [M, ld_sa] (sa_col_major = 0) or [KB, M]
+  int64_t ld_sa;     // row stride of sa in elements (row-major form)
+  int sa_col_major;
+  const void* sb;    // weight scales [ceil(N / 128), ld_sb], fp32 / fp16 / bf16
+  int sb_dtype;
+  int64_t ld_sb;
+  const void* bias;  // [N] or nullptr
+  int bias_dtype;
+  void* out;         // [M, N], row stride ldo
+  int out_dtype;
+  int64_t ldo;
+  float* ws;         // split-K partials [split, M, N] fp32
+  size_t ws_bytes;
+};
+
+// Whether the 256 x 256 kernel takes this problem (shape, alignment and dtype rules).
+bool block256_supported(const Block256Args& g);
+// K splits the 256 x 256 kernel uses (1: none); a function of the shape only.
+int64_t block256_split(int64_t M, int64_t N, int64_t K);
+// Launch (the kernel and, with a K split, the reduce). Returns an ayk_status.
+int block256_launch(const Block256Args& g, hipStream_t st, const char* op);
+
+}  // namespace ayk

@@ -1,0 +1,407 @@
+// Block-scaled fp8 GEMM (fp8_blockwise_mm) on 256 x 256 tiles, gfx950.
+//
+//   out[m, n] = sum_kb (a[m, kb] . w[n, kb]) * sa[m, kb] * sb[n / 128, kb]  (+ bias[n])
+//
+// with 128-wide K blocks kb (python/ayaka/kernel/triton/gemm/fp8_gemm.py:127-204;
+// oracle reference/gemm.py:40-70).
+//
+// Rescaling without a per-block fold. Each block's scale c = sa[m, kb] * sb[nb, kb] is
+// split into a power of two and a mantissa, c = mu * 2^E with mu in [1, 2). The power of
+// two goes into the scaled MFMA's E8M0 activation-scale operand (one code per lane, i.e.
+// per activation row m), which multiplies the block's products by exactly 2^E. The
+// accumulator U holds the running sum in units of the current block's mantissa:
+//   U_kb = U_{kb-1} * (mu_{kb-1} / mu_kb) + 2^E_kb * P_kb,   out = U_last * mu_last,
+// so a block costs one multiply per accumulator (the ratio) instead of a fold of a
+// separate partial (a read and an fma), and the accumulators stay within a factor of two
+// of the true sum. A zero or subnormal c is passed as code 0 (2^-127: such a block adds
+// below 1e-38 of its products) with mu unchanged; an infinite or NaN c as code 0xFF,
+// which the MFMA turns into NaN.
+//
+// Tiling. 512 threads = 8 wavefronts, two per SIMD, so one wavefront's rescale (VALU)
+// runs beside the other's MFMAs. Wavefront (wn, wm) owns weight rows [128 wn, +128) --
+// inside one 128-row scale block -- and activation rows [64 wm, +64): 4 x 2 MFMA tiles of
+// 32 x 32, 128 fp32 accumulators in VGPRs (this file is compiled with the VGPR form of
+// the MFMAs). One 128-K block is one "pair" of 64-K MFMA steps; operands move HBM/L2 ->
+// LDS with direct-to-LDS 16-byte loads covering 8 rows x 128 bytes each, into two 64 KB
+// pair buffers (the next pair lands while the current one is multiplied). Wavefronts
+// 0-3 load the 256 weight rows, 4-7 the 256 activation rows. LDS row r holds logical
+// 16-byte chunk c at physical chunk c ^ ((r >> 1) & 7), so the 32 rows of a fragment
+// read fall on distinct banks.
+#include "gemm_block.h"
+
+#include "ayk_common.h"
+#include "gemm_tiles.h"
+#include "gemm_util.h"
+
+namespace ayk {
+namespace {
+
+typedef int v8i __attribute__((ext_vector_type(8)));
+typedef int v4i __attribute__((ext_vector_type(4)));
+typedef float v16f __attribute__((ext_vector_type(16)));
+
+constexpr int kThreads = 512;
+constexpr int kTile = 256;
+constexpr int kPairK = 128;                      // K bytes per pair buffer: one scale block
+constexpr int kPairBytes = 2 * kTile * kPairK;   // 64 KB: 256 weight rows, then 256 activation rows
+constexpr int kDma = kPairBytes / 1024 / 8;      // direct loads per wavefront per pair (8)
+constexpr int FN = 4, FM = 2;                    // MFMA tiles per wavefront (n, m)
+constexpr int kCodeOne = 127;                    // UE8M0 code of 1.0
+constexpr int kRegion = 16 * 1024;               // a wavefront's epilogue staging region
+
+__device__ inline v16f mfma_scaled(const v8i& w, const v8i& a, const v16f& c, int code_a) {
+  return __builtin_amdgcn_mfma_scale_f32_32x32x64_f8f6f4(w, a, c, 0, 0, 0, kCodeOne, 0, code_a);
+}
+
+// Block scale c -> (E8M0 code of its power of two, its mantissa); mu keeps the previous
+// mantissa for a zero, subnormal or non-finite c (see the file comment).
+__device__ inline int split_scale(float c, float mu_prev, float& mu) {
+  const uint32_t b = __float_as_uint(c);
+  const uint32_t e = (b >> 23) & 0xFFu;
+  const uint32_t normal = (e - 1u < 254u) ? 0xFFFFFFFFu : 0u;  // a v_cmp + v_cndmask, no branch
+  mu = __uint_as_float((((b & 0x807FFFFFu) | 0x3F800000u) & normal) | (__float_as_uint(mu_prev) & ~normal));
+  const uint32_t special = e == 0 ? 0u : 0xFFu;
+  return (int)((e & normal) | (special & ~normal));
+}
+
+template <int OUT>
+struct OutBytes { static constexpr int v = OUT == AYK_F32 ? 4 : 2; };
+
+// Epilogue: out = U * mu (+ bias), one rounding. Each wavefront stages its 128 (n) x 32
+// (m) slab of m-fragment j in a private 16 KB LDS region (16-byte chunks XOR-swizzled by
+// row), then stores it row by row with coalesced 16-byte stores. No workgroup barrier:
+// the region belongs to the wavefront.
+template <int OUT, bool BIAS>
+__device__ __attribute__((always_inline)) inline void block256_epilogue(const Block256Args& g, const v16f (&U)[FN][FM],
+                                                                        const float (&mu)[FM], int64_t m_tile,
+                                                                        int64_t n_tile, uint8_t* region) {
+  constexpr int EB = OutBytes<OUT>::v;
+  constexpr int kRowBytes = 128 * EB;
+  constexpr int kChunks = kRowBytes / 16;           // 16 (bf16 / fp16) or 32 (fp32)
+  constexpr int kRowsPerStore = 64 / kChunks;       // rows one store instruction covers
+  static_assert(32 * kRowBytes <= kRegion, "staging slab must fit the region");
+  const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+  const int wn = wave >> 2, wm = wave & 3, h = lane >> 5, frow = lane & 31;
+  const int64_t n_w = n_tile + wn * 128;
+#pragma unroll
+  for (int j = 0; j < FM; ++j) {
+#pragma unroll
+    for (int i = 0; i < FN; ++i) {
+#pragma unroll
+      for (int grp = 0; grp < 4; ++grp) {
+        const int nl = 32 * i + 8 * grp + 4 * h;  // column within the wavefront's 128
+        float bias[4] = {0.0f, 0.0f, 0.0f, 0.0f};
+        if constexpr (BIAS) {
+          const int64_t n = n_w + nl;
+          if (n < g.N) {
+            if (g.bias_dtype == AYK_F32) {
+              const float4 t = *reinterpret_cast<const float4*>(static_cast<const float*>(g.bias) + n);
+              bias[0] = t.x; bias[1] = t.y; bias[2] = t.z; bias[3] = t.w;
+            } else {
+              const uint2 t = *reinterpret_cast<const uint2*>(static_cast<const uint16_t*>(g.bias) + n);
+              const uint32_t wds[2] = {t.x, t.y};
+#pragma unroll
+              for (int q = 0; q < 4; ++q) {
+                const uint16_t bits = (uint16_t)(wds[q / 2] >> (16 * (q % 2)));
+                bias[q] = g.bias_dtype == AYK_BF16 ? bf16_bits_to_f32(bits) : f16_bits_to_f32(bits);
+              }
+            }
+          }
+        }
+        float v[4];
+#pragma unroll
+        for (int q = 0; q < 4; ++q) v[q] = U[i][j][4 * grp + q] * mu[j] + bias[q];
+        const int byte = nl * EB;
+        const int chunk = (byte >> 4) ^ (frow & (kChunks - 1) & 15);
+        uint8_t* dst = region + frow * kRowBytes + chunk * 16 + (byte & 15);
+        if constexpr (OUT == AYK_F32) {
+          *reinterpret_cast<float4*>(dst) = make_float4(v[0], v[1], v[2], v[3]);
+        } else if constexpr (OUT == AYK_BF16) {
+          *reinterpret_cast<uint2*>(dst) = make_uint2(pack_bf16x2(v[0], v[1]), pack_bf16x2(v[2], v[3]));
+        } else {
+          *reinterpret_cast<uint2*>(dst) =
+              make_uint2((uint32_t)f32_to_f16_bits(v[0]) | ((uint32_t)f32_to_f16_bits(v[1]) << 16),
+                         (uint32_t)f32_to_f16_bits(v[2]) | ((uint32_t)f32_to_f16_bits(v[3]) << 16));
+        }
+      }
+    }
+    // The wavefront's own staging writes are complete before it reads them back (and the
+    // compiler may not move LDS accesses across this point).
+    asm volatile("s_waitcnt lgkmcnt(0)" ::: "memory");
+#pragma unroll
+    for (int r0 = 0; r0 < 32; r0 += kRowsPerStore) {
+      const int rr = r0 + lane / kChunks, cc = lane % kChunks;
+      const int64_t gm = m_tile + wm * 64 + j * 32 + rr;
+      const int64_t gn = n_w + (int64_t)cc * (16 / EB);
+      const uint4 val = *reinterpret_cast<const uint4*>(region + rr * kRowBytes + ((cc ^ (rr & (kChunks - 1) & 15)) * 16));
+      if (gm < g.M && gn < g.N) {
+        uint8_t* out = static_cast<uint8_t*>(g.out) + (gm * g.ldo + gn) * EB;
+        if (gn + 16 / EB <= g.N) *reinterpret_cast<uint4*>(out) = val;
+        else *reinterpret_cast<uint2*>(out) = make_uint2(val.x, val.y);  // N % 4 == 0
+      }
+    }
+    asm volatile("s_waitcnt lgkmcnt(0)" ::: "memory");
+  }
+}
+
+template <int OUT>
+__device__ __attribute__((always_inline)) inline void block256_epilogue_out(const Block256Args& g, const v16f (&U)[FN][FM],
+                                                                            const float (&mu)[FM], int64_t m_tile,
+                                                                            int64_t n_tile, uint8_t* region) {
+  if (g.bias) block256_epilogue<OUT, true>(g, U, mu, m_tile, n_tile, region);
+  else block256_epilogue<OUT, false>(g, U, mu, m_tile, n_tile, region);
+}
+
+// blockIdx.x: tile (XCD-aware order); blockIdx.y: K split (kps > 0: K range
+// [y kps, (y + 1) kps), fp32 partial to ws[y], no bias).
+__global__ __launch_bounds__(kThreads, 1) void fp8_block256_kernel(Block256Args gin, int tiles_m, int64_t kps) {
+  __shared__ __attribute__((aligned(1024))) uint8_t P0[kPairBytes];
+  __shared__ __attribute__((aligned(1024))) uint8_t P1[kPairBytes];
+
+  Block256Args g = gin;
+  int64_t k0 = 0, klen = gin.K;
+  if (kps > 0) {
+    k0 = (int64_t)blockIdx.y * kps;
+    klen = gin.K - k0 < kps ? gin.K - k0 : kps;
+    g.bias = nullptr;
+    g.out = gin.ws + (int64_t)blockIdx.y * gin.M * gin.N;
+    g.out_dtype = AYK_F32;
+    g.ldo = gin.N;
+  }
+
+  const int tid = threadIdx.x, lane = tid & 63;
+  const int wave_u = __builtin_amdgcn_readfirstlane(tid >> 6);
+  const int wn = wave_u >> 2, wm = wave_u & 3;
+  const int h = lane >> 5, frow = lane & 31;
+  int tm, tn;
+  big_tile_coords(blockIdx.x, tiles_m, (int)cdiv(g.N, kTile), tm, tn);
+  const int64_t n_base = (int64_t)tn * kTile, m_base = (int64_t)tm * kTile;
+  const int np = (int)(klen / kPairK);   // K blocks of this range (>= 1)
+  const int npairs = (np + 1) & ~1;      // the loop runs pairs two at a time
+  const int kb0 = (int)(k0 / kPairK);
+  // K stagger: tile (tm, tn) starts at block (tm mod 8) + (tn mod 2), so the tiles an XCD
+  // runs together do not request the same K slices in lockstep.
+  const int stag = __builtin_amdgcn_readfirstlane((int)((unsigned)((tm & 7) + (tn & 1)) % (unsigned)np));
+  auto block_of = [&](int p) {  // local block of loop pair p (< np)
+    const int b = p + stag;
+    return __builtin_amdgcn_readfirstlane(b >= np ? b - np : b);
+  };
+
+  // Direct loads: wavefront w < 4 fetches weight rows [64 w, 64 w + 64), w >= 4 activation
+  // rows [64 (w - 4), +64). Load jj covers rows 8 jj + L / 8 (lane L), 128 K bytes, written
+  // as LDS rows 256 (w / 4) + 64 (w % 4) + 8 jj + L / 8; lane L fetches logical chunk
+  // (L & 7) ^ ((4 (jj & 1) + (L >> 4)) & 7) so that it lands at physical chunk L & 7.
+  const int side = wave_u >> 2;
+  const int64_t ld = side == 0 ? g.ldw : g.lda;
+  const int ld_u = __builtin_amdgcn_readfirstlane((int)ld);
+  const OperandWindow win = operand_window((side == 0 ? n_base : m_base) + 64 * (wave_u & 3), side == 0 ? g.N : g.M, ld);
+  const __amdgpu_buffer_rsrc_t rsrc = uniform_rsrc((side == 0 ? g.w : g.a) + win.base_offset + k0, win.records);
+  const int voff_e = (lane >> 3) * ld_u + (((lane & 7) ^ ((lane >> 4) & 7)) << 4);
+  const int voff_o = (lane >> 3) * ld_u + (((lane & 7) ^ ((4 + (lane >> 4)) & 7)) << 4);
+  auto issue = [&](int p, uint8_t* dst) {
+    const int kb = block_of(p);
+#pragma unroll
+    for (int jj = 0; jj < kDma; ++jj) {
+      const int soff = __builtin_amdgcn_readfirstlane(jj * 8 * ld_u + kb * kPairK);
+      __builtin_amdgcn_raw_ptr_buffer_load_lds(rsrc, (__attribute__((address_space(3))) void*)(dst + (wave_u * kDma + jj) * 1024),
+                                               16, (jj & 1) ? voff_o : voff_e, soff, 0, 0);
+    }
+  };
+
+  // Scales of a block: this lane's two activation rows, and the wavefront's weight block
+  // row (its 128 weight rows share one). They are fetched as raw dwords through buffer
+  // descriptors (32-bit offsets, no waits at the load) and decoded in `prepare`, after
+  // the pair's vector-memory wait.
+  const int64_t nbs = cdiv(g.N, 128);
+  const int64_t nb = (n_base + wn * 128) / 128 < nbs ? (n_base + wn * 128) / 128 : nbs - 1;
+  const int sb_size = g.sb_dtype == AYK_F32 ? 4 : 2;
+  const int64_t sa_elems = g.sa_col_major ? cdiv(g.K, 128) * g.M : g.M * g.ld_sa;
+  const __amdgpu_buffer_rsrc_t sa_rsrc = uniform_rsrc(g.sa, (int32_t)(sa_elems * 4 < 0x7FFFFFFF ? sa_elems * 4 : 0x7FFFFFFF));
+  // sb through a descriptor on its 4-byte-aligned span: a 16-bit scale is read as the
+  // aligned dword that holds it, which never leaves that span.
+  const uintptr_t sb_addr = reinterpret_cast<uintptr_t>(g.sb);
+  const int sb_lead = (int)(sb_addr & 3);
+  const int64_t sb_span = (sb_lead + nbs * g.ld_sb * sb_size + 3) & ~(int64_t)3;
+  const __amdgpu_buffer_rsrc_t sb_rsrc =
+      uniform_rsrc(reinterpret_cast<const void*>(sb_addr - sb_lead), (int32_t)(sb_span < 0x7FFFFFFF ? sb_span : 0x7FFFFFFC));
+  const int sb_row_byte = sb_lead + (int)(nb * g.ld_sb * sb_size);
+  uint32_t sa_off[FM];  // byte offsets of this lane's rows at block 0
+#pragma unroll
+  for (int j = 0; j < FM; ++j) {
+    const int64_t m = m_base + wm * 64 + j * 32 + frow;
+    const int64_t mi = m < g.M ? m : g.M - 1;
+    sa_off[j] = (uint32_t)((g.sa_col_major ? mi : mi * g.ld_sa) * 4);
+  }
+  const uint32_t sa_kstride = (uint32_t)((g.sa_col_major ? g.M : 1) * 4);
+  struct Scales {
+    uint32_t sa[FM];
+    uint32_t sb;   // the dword holding sb[nb, kb]
+    uint32_t sh;   // bit position of sb in it (fp16 / bf16)
+  };
+  auto load_scales = [&](int p) {
+    const int kb = kb0 + block_of(p);
+    Scales s;
+#pragma unroll
+    for (int j = 0; j < FM; ++j)
+      s.sa[j] = (uint32_t)__builtin_amdgcn_raw_buffer_load_b32(sa_rsrc, (int)(sa_off[j] + (uint32_t)kb * sa_kstride), 0, 0);
+    const int sb_byte = __builtin_amdgcn_readfirstlane(sb_row_byte + kb * sb_size);
+    s.sb = (uint32_t)__builtin_amdgcn_raw_buffer_load_b32(sb_rsrc, 0, sb_byte & ~3, 0);
+    s.sh = (uint32_t)(sb_byte & 3) * 8;
+    return s;
+  };
+  const bool sb_f32 = g.sb_dtype == AYK_F32, sb_bf16 = g.sb_dtype == AYK_BF16;
+  float mu[FM] = {1.0f, 1.0f}, ratio[FM] = {1.0f, 1.0f};
+  int code[FM] = {kCodeOne, kCodeOne};
+  auto prepare = [&](Scales s) {
+    asm volatile("" : "+v"(s.sb));
+    const uint32_t half = (s.sb >> s.sh) & 0xFFFFu;
+    const float sbv = sb_f32 ? __uint_as_float(s.sb) : (sb_bf16 ? __uint_as_float(half << 16) : f16_bits_to_f32((uint16_t)half));
+#pragma unroll
+    for (int j = 0; j < FM; ++j) {
+      asm volatile("" : "+v"(s.sa[j]));
+      float m_new;
+      code[j] = split_scale(__uint_as_float(s.sa[j]) * sbv, mu[j], m_new);
+      ratio[j] = mu[j] / m_new;
+      mu[j] = m_new;
+    }
+  };
+
+  // Fragment reads (the 256 x 256 rowwise kernel's scheme): LDS row of weight row R is R,
+  // of activation row R is 256 + R; step t reads logical chunks 4 t + h and 4 t + 2 + h.
+  const int fsw = (frow >> 1) & 7;
+  const int off_t[2][2] = {{frow * kPairK + ((h ^ fsw) << 4), frow * kPairK + (((2 + h) ^ fsw) << 4)},
+                           {frow * kPairK + (((4 + h) ^ fsw) << 4), frow * kPairK + (((6 + h) ^ fsw) << 4)}};
+  auto frag = [&](const uint8_t* buf, int row0, int t) -> v8i {
+    const v4i lo = *reinterpret_cast<const v4i*>(buf + (row0 * kPairK + off_t[t][0]));
+    const v4i hi = *reinterpret_cast<const v4i*>(buf + (row0 * kPairK + off_t[t][1]));
+    return __builtin_shufflevector(lo, hi, 0, 1, 2, 3, 4, 5, 6, 7);
+  };
+  v8i wf[2][FN], af[2][FM];
+  auto read_frags = [&](int set, const uint8_t* buf, int t) {
+#pragma unroll
+    for (int i = 0; i < FN; ++i) wf[set][i] = frag(buf, wn * 128 + i * 32, t);
+#pragma unroll
+    for (int j = 0; j < FM; ++j) af[set][j] = frag(buf, 256 + wm * 64 + j * 32, t);
+  };
+
+  v16f U[FN][FM];
+#pragma unroll
+  for (int i = 0; i < FN; ++i)
+#pragma unroll
+    for (int j = 0; j < FM; ++j)
+#pragma unroll
+      for (int r = 0; r < 16; ++r) U[i][j][r] = 0.0f;
+
+  // Prologue: pair 0 (and pair 1) in flight with their scales; pair 0 visible.
+  Scales s_next = load_scales(0);
+  issue(0, P0);
+  wait_vmcnt<0>();
+  lds_barrier();
+  prepare(s_next);
+  if (np > 1) {
+    s_next = load_scales(1);
+    issue(1, P1);
+  }
+  read_frags(0, P0, 0);
+
+  // Pair p in `cur` (visible, step-0 fragments in set 0, rescale of block p prepared);
+  // pair p + 1 in flight into `nxt` with its scales in s_next.
+  auto pair = [&](int p, uint8_t* cur, uint8_t* nxt) {
+    const bool live = p < np;  // wave-uniform
+    if (live) {
+#pragma unroll
+      for (int j = 0; j < FM; ++j)
+#pragma unroll
+        for (int i = 0; i < FN; ++i) {
+#pragma unroll
+          for (int r = 0; r < 16; ++r) U[i][j][r] *= ratio[j];
+          U[i][j] = mfma_scaled(wf[0][i], af[0][j], U[i][j], code[j]);
+        }
+      read_frags(1, cur, 1);
+#pragma unroll
+      for (int i = 0; i < FN; ++i) U[i][0] = mfma_scaled(wf[1][i], af[1][0], U[i][0], code[0]);
+    }
+    const int code_tail = code[1];
+    __builtin_amdgcn_sched_barrier(0);
+    wait_vmcnt<0>();  // pair p + 1 and its scales have landed
+    lds_barrier();    // ... for every wavefront, and no wavefront reads `cur` any more
+    __builtin_amdgcn_sched_barrier(0);
+    if (p + 1 < np) {
+      prepare(s_next);
+      if (p + 2 < np) {
+        s_next = load_scales(p + 2);
+        issue(p + 2, cur);
+      }
+      read_frags(0, nxt, 0);
+    }
+    if (live) {
+#pragma unroll
+      for (int i = 0; i < FN; ++i) U[i][1] = mfma_scaled(wf[1][i], af[1][1], U[i][1], code_tail);
+    }
+  };
+  for (int p = 0; p < npairs; p += 2) {
+    pair(p, P0, P1);
+    pair(p + 1, P1, P0);
+  }
+  wait_vmcnt<0>();
+  lds_barrier();  // no wavefront still reads a pair buffer: they become staging regions
+
+  uint8_t* region = (wave_u < 4 ? P0 : P1) + (wave_u & 3) * kRegion;
+  if (g.out_dtype == AYK_BF16) block256_epilogue_out<AYK_BF16>(g, U, mu, m_base, n_base, region);
+  else if (g.out_dtype == AYK_F16) block256_epilogue_out<AYK_F16>(g, U, mu, m_base, n_base, region);
+  else block256_epilogue_out<AYK_F32>(g, U, mu, m_base, n_base, region);
+}
+
+// Fixed-order sum of the K-split partials, bias, one rounding.
+__global__ __launch_bounds__(256) void block256_reduce(const float* __restrict__ part, int64_t M, int64_t N, int split,
+                                                       const void* __restrict__ bias, int bias_dtype, void* __restrict__ out,
+                                                       int out_dtype, int64_t ldo) {
+  const int64_t i = (int64_t)blockIdx.x * 256 + threadIdx.x;
+  if (i >= M * N) return;
+  const int64_t m = i / N, n = i - m * N;
+  float v = 0.0f;
+  for (int s = 0; s < split; ++s) v += part[(int64_t)s * M * N + i];
+  if (bias) v += load_f32(bias, bias_dtype, n);
+  store_f32(out, out_dtype, m * ldo + n, v);
+}
+
+}  // namespace
+
+bool block256_supported(const Block256Args& g) {
+  const int64_t out_bytes = g.out_dtype == AYK_F32 ? 4 : 2;
+  return g.K % kPairK == 0 && g.K < ((int64_t)1 << 30) && g.M >= kTile && g.N >= kTile && g.N % 4 == 0 &&
+         (g.ldo * out_bytes) % 16 == 0 && aligned16(g.out) && aligned16(g.a) && aligned16(g.w) &&
+         g.lda % 16 == 0 && g.ldw % 16 == 0 && 64 * g.lda < ((int64_t)1 << 31) && 64 * g.ldw < ((int64_t)1 << 31) &&
+         (g.bias == nullptr || aligned16(g.bias)) && (g.sb_dtype == AYK_F32 || g.sb_dtype == AYK_BF16 || g.sb_dtype == AYK_F16);
+}
+
+// Under one round of tiles (256 workgroups, one per CU): the largest power-of-two K
+// split that still fits in that round, at least 1024 K per split.
+int64_t block256_split(int64_t M, int64_t N, int64_t K) {
+  const int64_t tiles = cdiv(M, kTile) * cdiv(N, kTile);
+  int64_t split = 1;
+  while (tiles * split * 2 <= 256 && K / (split * 2) >= 1024 && (K / kPairK) % (split * 2) == 0) split *= 2;
+  return split;
+}
+
+int block256_launch(const Block256Args& g, hipStream_t st, const char* op) {
+  const int tiles_m = (int)cdiv(g.M, kTile);
+  const int64_t tiles = (int64_t)tiles_m * cdiv(g.N, kTile);
+  if (tiles > 0x7FFFFFFF) return fail(AYK_EINVAL, "%s: problem too large", op);
+  const int64_t split = block256_split(g.M, g.N, g.K);
+  if (split == 1) {
+    hipLaunchKernelGGL(fp8_block256_kernel, dim3((unsigned)tiles), dim3(kThreads), 0, st, g, tiles_m, (int64_t)0);
+    return check_launch(op);
+  }
+  const size_t need = (size_t)split * (size_t)g.M * (size_t)g.N * sizeof(float);
+  if (g.ws == nullptr || g.ws_bytes < need)
+    return fail(AYK_EWORKSPACE, "%s: workspace of %zu bytes required, %zu given", op, need, g.ws_bytes);
+  hipLaunchKernelGGL(fp8_block256_kernel, dim3((unsigned)tiles, (unsigned)split), dim3(kThreads), 0, st, g, tiles_m,
+                     g.K / split);
+  if (int rc = check_launch(op)) return rc;
+  hipLaunchKernelGGL(block256_reduce, dim3((unsigned)cdiv(g.M * g.N, 256)), dim3(256), 0, st, g.ws, g.M, g.N, (int)split,
+                     g.bias, g.bias_dtype, g.out, g.out_dtype, g.ldo);
+  return check_launch(op);
+}
+
+}  // namespace ayk

@@ -239,6 +239,65 @@ def test_fp8_blockwise_mm(gpu, m, n, k, sdt, col_major):
     assert_linear_close(out, ref, "blockwise_mm")
 
 
+# The 256 x 256 block-scaled kernel (launches of >= 128 tiles of 256 x 256): ragged M / N
+# tails, an odd number of 128-K blocks (a padded loop pair), column-major activation
+# scales, 16-bit weight scales, every output dtype and the K-split form (exactly 128 tiles).
+BLOCK256 = [
+    (2100, 4200, 640, False, torch.float32, torch.bfloat16, True),
+    (4096, 2304, 1152, True, torch.bfloat16, torch.float32, False),
+    (2304, 4352, 384, False, torch.float16, torch.float16, True),
+    (2048, 4096, 8192, False, torch.float32, torch.bfloat16, True),   # 128 tiles: K split 2
+    (4096, 2048, 256, True, torch.float32, torch.bfloat16, False),    # two blocks, one pair
+]
+
+
+@pytest.mark.parametrize("m,n,k,col_major,sdt,out_dtype,with_bias", BLOCK256)
+def test_fp8_blockwise_mm_256(gpu, m, n, k, col_major, sdt, out_dtype, with_bias):
+    from ayaka.kernel.hip import fp8_blockwise_mm
+
+    _say(f"fp8_blockwise_mm 256-tile m={m} n={n} k={k} col_major={col_major} sdt={sdt} out={out_dtype} bias={with_bias}")
+    kb, nb = k // 128, -(-n // 128)
+    a = _fp8((m, k), seed=m + 3, scale=30)
+    w = _fp8((n, k), seed=n + 4, scale=30)
+    # scales over eight decades, so the per-block exponent / mantissa split sees widely
+    # different exponents from block to block
+    sa = torch.exp(torch.rand(m, kb, generator=_gen(24)) * -18.0).float()
+    sb = torch.exp(torch.rand(nb, kb, generator=_gen(25)) * -6.9).to(sdt)
+    sa_arg = sa.t().contiguous() if col_major else sa
+    bias = (torch.randn(n, generator=_gen(26)) * 0.01).to(torch.bfloat16) if with_bias else None
+    ref = ora.fp8_blockwise_mm(a, w, sa_arg, sb, bias, col_major)
+    out = torch.empty(m, n, dtype=out_dtype, device=gpu)
+    fp8_blockwise_mm(a.to(gpu), w.to(gpu), sa_arg.to(gpu), sb.to(gpu), bias.to(gpu) if bias is not None else None,
+                     out=out, a_scale_col_major=col_major)
+    assert_linear_close(out, ref, "blockwise_mm 256-tile")
+
+
+def test_fp8_blockwise_mm_256_scale_edges(gpu):
+    """Zero weight-block scales add nothing (the MFMA exponent code 0 weighs a block's
+    products by 2^-127), and a NaN scale poisons exactly the outputs whose sums include it,
+    as in the oracle."""
+    from ayaka.kernel.hip import fp8_blockwise_mm
+
+    m, n, k = 2048, 4096, 1024
+    _say(f"fp8_blockwise_mm 256-tile scale edges m={m} n={n} k={k}")
+    kb, nb = k // 128, n // 128
+    a = _fp8((m, k), seed=31, scale=30)
+    w = _fp8((n, k), seed=32, scale=30)
+    sa = torch.exp(torch.rand(m, kb, generator=_gen(33)) * -6.9).float()
+    sb = torch.exp(torch.rand(nb, kb, generator=_gen(34)) * -6.9).float()
+    sb[3, :] = 0.0      # weight rows 384..511 contribute nothing
+    sb[5, 2] = 0.0      # one block of rows 640..767
+    sa[7, 4] = float("nan")  # activation row 7: every output NaN
+    ref = ora.fp8_blockwise_mm(a, w, sa, sb)
+    out = torch.empty(m, n, dtype=torch.float32, device=gpu)
+    fp8_blockwise_mm(a.to(gpu), w.to(gpu), sa.to(gpu), sb.to(gpu), out=out)
+    y = out.cpu()
+    assert torch.equal(torch.isnan(y), torch.isnan(ref))
+    keep = ~torch.isnan(ref)
+    assert_linear_close(y[keep], ref[keep], "blockwise_mm 256-tile edges")
+    assert y[:, 384:512][keep[:, 384:512]].abs().max().item() < 1e-25
+
+
 @pytest.mark.parametrize("m,n,k,col_major,sdt,with_bias", [
     (32, 1024, 4096, False, torch.float32, True),     # K split 4
     (200, 768, 8192, True, torch.bfloat16, True),     # split 8, column-major activation scales
