@@ -1657,7 +1657,7 @@ int launch_cfg(GemmArgs g, hipStream_t st, const char* op) {
 // The 256 x 256 block-scaled kernel serves launches of at least half a round (128) of
 // its tiles; smaller ones keep the 128 x 128 tiles and their K split.
 bool block256_wanted(int64_t M, int64_t N, int64_t K) {
-  return K % 128 == 0 && M >= 256 && N >= 256 && cdiv(M, 256) * cdiv(N, 256) >= 128;
+  return K % 128 == 0 && M >= 256 && N >= 256 && cdiv(M, 256) * cdiv(N, 256) >= 16;
 }
 Block256Args block256_args(const GemmArgs& g) {
   Block256Args b{};

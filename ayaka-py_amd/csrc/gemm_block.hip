@@ -306,37 +306,76 @@ __global__ __launch_bounds__(kThreads, 1) void fp8_block256_kernel(Block256Args 
 
   // Pair p in `cur` (visible, step-0 fragments in set 0, rescale of block p prepared);
   // pair p + 1 in flight into `nxt` with its scales in s_next.
+  // A pair runs in two phases around its barrier, eight MFMAs each, so that the LDS reads
+  // and the rescale multiplies spread over MFMAs of the same wavefront:
+  //  * before the barrier: step 0's MFMAs; beside them, step 1's fragment reads and the
+  //    m-fragment 1 rescale into this block's units (one MFMA, then 16 multiplies);
+  //  * after it (pair p + 1 has landed, `cur` is free): step 1's MFMAs; beside them the
+  //    next pair's step-0 fragment reads and the m-fragment 0 rescale into block p + 1's
+  //    units (behind that m-fragment's last MFMA of this block).
+  // U is zero before the first block, so its rescale is moot.
+  constexpr int kSchedMfma = 0x008, kSchedValu = 0x002, kSchedDsRead = 0x100;
   auto pair = [&](int p, uint8_t* cur, uint8_t* nxt) {
     const bool live = p < np;  // wave-uniform
     if (live) {
 #pragma unroll
-      for (int j = 0; j < FM; ++j)
+      for (int i = 0; i < FN; ++i) {
+        U[i][0] = mfma_scaled(wf[0][i], af[0][0], U[i][0], code[0]);
 #pragma unroll
-        for (int i = 0; i < FN; ++i) {
+        for (int r = 0; r < 16; ++r) U[i][1][r] *= ratio[1];
+      }
 #pragma unroll
-          for (int r = 0; r < 16; ++r) U[i][j][r] *= ratio[j];
-          U[i][j] = mfma_scaled(wf[0][i], af[0][j], U[i][j], code[j]);
-        }
+      for (int i = 0; i < FN; ++i) U[i][1] = mfma_scaled(wf[0][i], af[0][1], U[i][1], code[1]);
       read_frags(1, cur, 1);
 #pragma unroll
-      for (int i = 0; i < FN; ++i) U[i][0] = mfma_scaled(wf[1][i], af[1][0], U[i][0], code[0]);
+      for (int i = 0; i < FN; ++i) {
+        __builtin_amdgcn_sched_group_barrier(kSchedMfma, 1, 0);
+        __builtin_amdgcn_sched_group_barrier(kSchedValu, 16, 0);
+        __builtin_amdgcn_sched_group_barrier(kSchedDsRead, 1, 0);
+      }
+#pragma unroll
+      for (int i = 0; i < FN; ++i) {
+        __builtin_amdgcn_sched_group_barrier(kSchedMfma, 1, 0);
+        __builtin_amdgcn_sched_group_barrier(kSchedDsRead, 2, 0);
+      }
     }
-    const int code_tail = code[1];
+    const int code1 = code[1], code0 = code[0];
     __builtin_amdgcn_sched_barrier(0);
     wait_vmcnt<0>();  // pair p + 1 and its scales have landed
     lds_barrier();    // ... for every wavefront, and no wavefront reads `cur` any more
     __builtin_amdgcn_sched_barrier(0);
-    if (p + 1 < np) {
+    const bool more = p + 1 < np;
+    if (more) {
       prepare(s_next);
       if (p + 2 < np) {
         s_next = load_scales(p + 2);
         issue(p + 2, cur);
       }
-      read_frags(0, nxt, 0);
     }
+    const float ratio0 = more ? ratio[0] : 1.0f;  // after the last block the units stay
     if (live) {
 #pragma unroll
-      for (int i = 0; i < FN; ++i) U[i][1] = mfma_scaled(wf[1][i], af[1][1], U[i][1], code_tail);
+      for (int i = 0; i < FN; ++i) U[i][0] = mfma_scaled(wf[1][i], af[1][0], U[i][0], code0);
+      read_frags(0, nxt, 0);  // after the last pair: stale data, never used
+#pragma unroll
+      for (int i = 0; i < FN; ++i) {
+        U[i][1] = mfma_scaled(wf[1][i], af[1][1], U[i][1], code1);
+#pragma unroll
+        for (int r = 0; r < 16; ++r) U[i][0][r] *= ratio0;
+      }
+#pragma unroll
+      for (int i = 0; i < FN; ++i) {
+        __builtin_amdgcn_sched_group_barrier(kSchedMfma, 1, 0);
+        __builtin_amdgcn_sched_group_barrier(kSchedDsRead, 2, 0);
+      }
+#pragma unroll
+      for (int i = 0; i < FN; ++i) {
+        __builtin_amdgcn_sched_group_barrier(kSchedMfma, 1, 0);
+        __builtin_amdgcn_sched_group_barrier(kSchedValu, 16, 0);
+        __builtin_amdgcn_sched_group_barrier(kSchedDsRead, 1, 0);
+      }
+    } else {
+      read_frags(0, nxt, 0);
     }
   };
   for (int p = 0; p < npairs; p += 2) {
