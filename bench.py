@@ -1,29 +1,34 @@
 """Benchmark of the MI355X FP8 linear path (one JSON line on stdout).
 
-Headline (``value``): BASELINE.json configs[1] -- W8A16 rowwise decode GEMV on the
-four Llama-3-8B projections (qkv 6144x4096, o 4096x4096, gate_up 28672x4096,
-down 4096x14336) at M = 1. One step runs all four projections through
-``ayaka::fp8_weight_only_gemv`` exactly as ``FP8W8A16LinearMethod.apply`` calls it;
-``value`` is the step's algorithmic bytes (fp8 weights + fp32 row scales + bf16 x and
-out) divided by its wall time, in GB/s. Inputs are resident in HBM before timing;
-three independent weight/scale copies (654 MB) are rotated across steps so the
-256 MB MALL cannot serve them.
+Headline (``value``): BASELINE.json configs[1] -- W8A16 rowwise decode GEMV on the four
+Llama-3-8B projections (qkv 6144x4096, o 4096x4096, gate_up 28672x4096, down 4096x14336)
+at M = 1. One step runs all four projections through ``ayaka::fp8_weight_only_gemv`` as
+``FP8W8A16LinearMethod.apply`` calls it, replayed as one HIP graph; ``value`` is the
+step's algorithmic bytes (fp8 weights + fp32 row scales + bf16 x and out) over its wall
+time, in GB/s. Inputs are resident in HBM before timing; three weight copies (654 MB)
+rotate across steps so the 256 MB MALL cannot serve them.
 
-Each step is replayed as a HIP graph (the four launches of one decode step), as a
-serving loop runs decode; the eager per-op dispatch time is reported beside it.
-``roofline`` is the dominant kernel (the gate_up GEMV, the only launch of its op):
-a graph of back-to-back launches is replayed between two events on its stream and
-the elapsed time divided by the launch count. ``gemm`` adds the prefill
-GEMMs at M = 4096 (TFLOP/s against the 5.0 PFLOP/s dense fp8 peak) and
-``cpu_baseline`` times the reference's CPU path (the oracle restatement) on a
-bounded sample on this host's cores.
+``roofline`` is the dominant kernel (the gate_up GEMV): a graph of back-to-back launches
+replayed between two events on its stream, divided by the launch count.
 
-Usage: python bench.py [--gpus 1] [--steps K] [--warmup W] [--no-gemm] [--no-cpu] [--copy-probe]
+``configs`` times every point of BASELINE.json:configs (plus supplemental M = 4096
+points for the recipes whose configurations stop short of it: rowwise, per-tensor and
+MXFP8) through the drop-in layer API
+(``FP8Config`` -> ``LinearMethod.apply``: activation quant + GEMM/GEMV + epilogue), and
+the GEMM/GEMV kernel alone on pre-quantized operands: 100 calls captured in one HIP graph (replayed twice untimed, then three times between events),
+rotating weight copies for decode batches (M <= 64) so that every call streams its
+weights from HBM. ``gemm`` collects the M = 4096 line of each recipe.
+
+``cpu_baseline`` times the reference's CPU path (the oracle restatement) on a bounded
+sample on this host's cores; ``cpu_baseline_gemm`` does the same per GEMM recipe.
+
+Usage: python bench.py [--gpus 1] [--steps K] [--warmup W] [--no-gemm] [--no-cpu]
+                       [--copy-probe] [--list] [--only LABEL [--only-kind gemm|layer] [--reps R]]
 """
 
 import argparse
-import itertools
 import json
+import math
 import os
 import sys
 import time
@@ -33,19 +38,18 @@ sys.path[:0] = [os.path.join(ROOT, "ayaka-py_amd"), ROOT]
 
 import torch  # noqa: E402
 
+import workloads as wl  # noqa: E402
+
 HBM_PEAK_GBS = 8000.0
 FP8_PEAK_TFLOPS = 5000.0
 CFG2_SHAPES = [("qkv", 6144, 4096), ("o", 4096, 4096), ("gate_up", 28672, 4096), ("down", 4096, 14336)]
 COPIES = 3
+POINT_WARMUP, POINT_REPS = 25, 100
+ROTATE_BYTES = 640 << 20  # decode points rotate weight copies totalling at least this much
 
 
 def _gemv_bytes(n: int, k: int, m: int = 1) -> int:
     return n * k + 4 * n + 2 * m * k + 2 * m * n
-
-
-def _quant_rowwise(wf: torch.Tensor):
-    scale = wf.abs().amax(dim=1).clamp_min(1e-12) / 448.0
-    return (wf / scale[:, None]).clamp(-448, 448).to(torch.float8_e4m3fn), scale.float()
 
 
 def _make_cfg2(device, seed=0):
@@ -55,13 +59,10 @@ def _make_cfg2(device, seed=0):
         copies = []
         for _ in range(COPIES):
             wf = torch.randn(n, k, generator=g, device=device) * 0.02
-            copies.append(_quant_rowwise(wf))
+            copies.append(wl.quant_rows(wf))
             del wf
-        gx = torch.Generator(device=device).manual_seed(1)
-        x = torch.randn(k, generator=gx, device=device)
-        idx = torch.randperm(k, generator=gx, device=device)[: k // 100]
-        x[idx] *= 20.0
-        layers.append((name, n, k, copies, x.to(torch.bfloat16)))
+        x = wl.outlier_activations(1, k, device).reshape(k)
+        layers.append((name, n, k, copies, x))
     return layers
 
 
@@ -89,129 +90,307 @@ def _capture(fn):
     return graph
 
 
-def _time_dominant(layers, launches_per_graph=24, replays=5):
-    """Per-launch time of the gate_up GEMV: a graph of back-to-back launches (rotating
-    the weight copies) replayed between two events on the replay stream."""
-    from ayaka.kernel.hip import fp8_weight_only_gemv
-
-    name, n, k, copies, x = layers[2]
-    out = torch.empty(n, dtype=torch.bfloat16, device=x.device)
-
-    def launches():
-        for i in range(launches_per_graph):
-            w, s = copies[i % COPIES]
-            fp8_weight_only_gemv(x, w, s, 1, 1, k, "float32", out=out)
-
-    graph = _capture(launches)
+def _graph_per_launch(launch, count, replays=5):
+    """(mean, median) ms per launch of a graph of ``count`` back-to-back launches, timed
+    with events on the replay stream."""
+    graph = _capture(lambda: [launch(i) for i in range(count)])
     stream = torch.cuda.current_stream()
-    per_launch = []
+    times = []
     for _ in range(replays):
         start, end = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
         start.record(stream)
         graph.replay()
         end.record(stream)
         end.synchronize()
-        per_launch.append(start.elapsed_time(end) / launches_per_graph)
-    per_launch.sort()
-    return n, k, sum(per_launch) / len(per_launch), per_launch[len(per_launch) // 2]
+        times.append(start.elapsed_time(end) / count)
+    times.sort()
+    return sum(times) / len(times), times[len(times) // 2]
 
 
-def _bench_gemm(device, reps=20, warmup=5):
-    """Prefill GEMMs at M = 4096 on the config shapes (supplemental M for MXFP8). Each is
-    timed over `reps` launches after `warmup` untimed ones (the clocks settle over the
-    first few milliseconds of matrix-core load)."""
-    from ayaka.kernel.hip import fp8_blockwise_mm, fp8_scaled_mm, mxfp8_scaled_mm
+def _time_dominant(layers, launches_per_graph=24):
+    """Per-launch time of the gate_up GEMV (graph of launches rotating the weight copies)."""
+    from ayaka.kernel.hip import fp8_weight_only_gemv
 
-    g = torch.Generator(device=device).manual_seed(0)
-    m = 4096
+    name, n, k, copies, x = layers[2]
+    out = torch.empty(n, dtype=torch.bfloat16, device=x.device)
+
+    def launch(i):
+        w, s = copies[i % COPIES]
+        fp8_weight_only_gemv(x, w, s, 1, 1, k, "float32", out=out)
+
+    mean, med = _graph_per_launch(launch, launches_per_graph)
+    return n, k, mean, med
+
+
+def _cfg2_projections(layers, launches_per_graph=24):
+    """Per-projection M = 1 launch time and GB/s of the Cfg2 step."""
+    from ayaka.kernel.hip import fp8_weight_only_gemv
+
+    rows = {}
+    for name, n, k, copies, x in layers:
+        out = torch.empty(n, dtype=torch.bfloat16, device=x.device)
+
+        def launch(i, copies=copies, x=x, out=out, k=k):
+            w, s = copies[i % COPIES]
+            fp8_weight_only_gemv(x, w, s, 1, 1, k, "float32", out=out)
+
+        mean, _ = _graph_per_launch(launch, launches_per_graph)
+        gbs = _gemv_bytes(n, k) / (mean * 1e-3) / 1e9
+        rows[name] = {"N": n, "K": k, "us": round(mean * 1e3, 2), "GB/s": round(gbs, 1),
+                      "frac": round(gbs / HBM_PEAK_GBS, 4)}
+    return rows
+
+
+def _time_rotated(fns, reps: int, warmup: int) -> float:
+    """Average ms per call over ``reps`` calls cycling through ``fns``, after ``warmup``
+    untimed calls; events on the current stream."""
+    for i in range(warmup):
+        fns[i % len(fns)]()
+    torch.cuda.synchronize()
+    start, end = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+    start.record()
+    for i in range(reps):
+        fns[i % len(fns)]()
+    end.record()
+    torch.cuda.synchronize()
+    return start.elapsed_time(end) / reps
+
+
+def _time_graph(fns, reps: int, warmup_replays: int = 2, replays: int = 3) -> float:
+    """Average ms per call of a HIP graph of ``reps`` back-to-back calls cycling through
+    ``fns`` (no host dispatch inside the timed region, as a graph-captured serving loop
+    runs), replayed ``warmup_replays`` times untimed, then timed over ``replays`` replays
+    with events on the replay stream."""
+    graph = _capture(lambda: [fns[i % len(fns)]() for i in range(reps)])
+    for _ in range(warmup_replays):
+        graph.replay()
+    stream = torch.cuda.current_stream()
+    start, end = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+    start.record(stream)
+    for _ in range(replays):
+        graph.replay()
+    end.record(stream)
+    end.synchronize()
+    ms = start.elapsed_time(end) / (replays * reps)
+    del graph
+    return ms
+
+
+def _hbm_entry(ms: float, nbytes: int, **extra) -> dict:
+    gbs = nbytes / (ms * 1e-3) / 1e9
+    return {**extra, "us": round(ms * 1e3, 2), "bytes": nbytes, "GB/s": round(gbs, 1),
+            "frac": round(gbs / HBM_PEAK_GBS, 4)}
+
+
+# ------------------------------------------------------------------ config points
+RECIPE_CONFIG = {
+    "per_tensor_dynamic": {"quant_method": "fp8", "activation_scheme": "dynamic"},
+    "per_tensor_static": {"quant_method": "fp8", "activation_scheme": "static"},
+    "w8a16": {"quant_algo": "w8a16"},
+    "rowwise": {"fp8_recipe": "w8a8_rowwise"},
+    "block128": {"weight_block_size": [128, 128], "scale_format": "float32"},
+    "mxfp8": {"quant_algo": "mxfp8"},
+}
+
+
+def _points():
+    """(label, config name, recipe, projection, N, K, M) for every BASELINE config point
+    and the supplemental M = 4096 points."""
+    recipe_of = {"cfg1_per_tensor": "per_tensor_dynamic", "cfg2_w8a16": "w8a16", "cfg3_rowwise": "rowwise",
+                 "cfg4_block128": "block128", "cfg5_mxfp8": "mxfp8"}
+    pts = []
+    for cfg in wl.CONFIGS:
+        for proj, n, k in cfg["shapes"]:
+            for m in cfg["ms"]:
+                pts.append((f"{cfg['name']}/{proj}/M{m}", cfg["name"], recipe_of[cfg["name"]], proj, n, k, m))
+    for proj, n, k in wl.CFG3["shapes"]:
+        pts.append((f"supp_rowwise/{proj}/M4096", "cfg3_rowwise", "rowwise", proj, n, k, 4096))
+        pts.append((f"supp_per_tensor_static/{proj}/M4096", "cfg3_rowwise", "per_tensor_static", proj, n, k, 4096))
+    for proj, n, k in wl.CFG5["shapes"]:
+        pts.append((f"supp_mxfp8/{proj}/M4096", "cfg5_mxfp8", "mxfp8", proj, n, k, 4096))
+    return pts
+
+
+def _weights(cfg, recipe, n, k, device, seed):
+    if recipe == "per_tensor_static":
+        wf = torch.randn(n, k, generator=torch.Generator(device=device).manual_seed(seed), device=device) * 0.02
+        q, s = wl.quant_tensor(wf)
+        return q, s.expand(n).contiguous()
+    if cfg == "cfg1_per_tensor":
+        return wl.cfg1_weights(n, k, device, seed)
+    if cfg in ("cfg2_w8a16", "cfg3_rowwise"):
+        w, s = wl.cfg23_weights(n, k, device, seed)
+        return (w, s.reshape(n, 1)) if recipe == "w8a16" else (w, s)
+    if cfg == "cfg4_block128":
+        return wl.cfg4_weights(n, k, device, seed)
+    return wl.cfg5_weights(n, k, device, seed)
+
+
+def _activations(cfg, m, k, device):
+    if cfg in ("cfg2_w8a16", "cfg3_rowwise"):
+        return wl.outlier_activations(m, k, device)
+    if cfg == "cfg5_mxfp8":
+        return wl.student_t_activations(m, k, device)
+    return wl.normal_activations(m, k, device)
+
+
+def _layer(recipe, w, s, device, input_scale=None):
+    from torch import nn
+
+    from ayaka.layers.linear.fp8 import FP8Config
+
+    method = FP8Config.from_config(RECIPE_CONFIG[recipe]).get_quant_method(None, "model.layers.0.mlp.proj")
+    layer = nn.Module()
+    method.create_weights(layer, output_partition_sizes=[int(w.shape[0])], input_size_per_partition=int(w.shape[1]),
+                          device=device)
+    layer.weight.data.copy_(w)
+    param = layer.weight_scale_inv if recipe == "block128" else layer.weight_scale
+    param.weight_loader(layer, param, s)
+    if recipe == "per_tensor_static":
+        layer.input_scale.weight_loader(layer, layer.input_scale, input_scale)
+    method.process_weights_after_loading(layer)
+    return method, layer
+
+
+def _kernel_call(recipe, x, layer, out, bias):
+    """The GEMM / GEMV kernel alone on the layer's operands, activation quantized
+    beforehand (the layer call does the same plus the quantizer)."""
+    from ayaka.kernel.hip import (fp8_blockwise_mm, fp8_scaled_mm, fp8_weight_only_gemm, fp8_weight_only_gemv,
+                                  mxfp8_scaled_mm, per_token_group_quant_fp8, per_token_group_quant_mxfp8,
+                                  per_token_quant_fp8, static_quant_fp8)
+
+    m, k = x.shape
+    n = int(layer.weight.shape[0])
+    if recipe == "w8a16" or (m == 1 and recipe != "mxfp8"):
+        scale = layer.weight_scale_inv if recipe == "block128" else layer.weight_scale
+        by, bx, sdt = ((128, 128, "float32") if recipe == "block128" else (1, k, "float32"))
+        if m == 1:
+            return lambda w=None: fp8_weight_only_gemv(x.reshape(k), w if w is not None else layer.weight,
+                                                       scale, -(-k // bx), by, bx, sdt, out=out.reshape(n))
+        return lambda w=None: fp8_weight_only_gemm(x, w if w is not None else layer.weight, scale, 1, by, bx, sdt,
+                                                   out=out)
+    if recipe == "mxfp8":
+        q, c = per_token_group_quant_mxfp8(x, 32)
+        return lambda w=None: mxfp8_scaled_mm(q, c, w if w is not None else layer.weight, layer.weight_scale, out=out)
+    if recipe == "block128":
+        q, sa = per_token_group_quant_fp8(x, 128)
+        return lambda w=None: fp8_blockwise_mm(q, w if w is not None else layer.weight, sa, layer.weight_scale_inv,
+                                               out=out)
+    if recipe == "per_tensor_static":
+        q = static_quant_fp8(x, layer.input_scale)
+        s = layer.weight_scale[0]
+        return lambda w=None: fp8_scaled_mm(q, (w if w is not None else layer.weight).t(), layer.input_scale, s,
+                                            bias=bias, out=out)
+    q, sa = per_token_quant_fp8(x)
+    return lambda w=None: fp8_scaled_mm(q, (w if w is not None else layer.weight).t(), sa, layer.weight_scale,
+                                        bias=bias, out=out)
+
+
+def _kernel_bytes(recipe, m, n, k):
+    """Algorithmic HBM bytes of the kernel call: fp8 weights + weight scales + its
+    activation operand (fp8 quantized, bf16 for W8A16 / the M = 1 GEMV) + act scales +
+    bf16 output."""
+    wscale = {"block128": 4 * (-(-n // 128)) * (-(-k // 128)), "mxfp8": n * (k // 32)}.get(recipe, 4 * n)
+    if recipe == "w8a16" or (m == 1 and recipe != "mxfp8"):
+        act = 2 * m * k
+    else:
+        act = m * k + {"block128": 4 * m * (k // 128), "mxfp8": m * (k // 32)}.get(recipe, 4 * m)
+    return n * k + wscale + act + 2 * m * n
+
+
+def _bench_configs(device, only=None, only_kind="gemm", reps=POINT_REPS, warmup=POINT_WARMUP):
     results = {}
+    current = None  # (cfg, recipe, proj): weights built once per projection
+    for label, cfg, recipe, proj, n, k, m in _points():
+        if only is not None and label != only:
+            continue
+        key = (cfg, recipe, proj)
+        if current is None or current[0] != key:
+            current = None
+            torch.cuda.empty_cache()
+            w, s = _weights(cfg, recipe, n, k, device, seed=0)
+            current = (key, w, s, [])
+        _, w, s, extra = current
+        copies = 1
+        if m <= 64:  # decode batches: enough copies that every call streams from HBM
+            copies = min(16, max(1, math.ceil(ROTATE_BYTES / (n * k))))
+            while len(extra) < copies - 1:
+                extra.append(_weights(cfg, recipe, n, k, device, seed=len(extra) + 1)[0])
+        weights = [w] + extra[: copies - 1]
+        x = _activations(cfg, m, k, device)
+        bias = wl.bias_vector(n, device) if cfg == "cfg3_rowwise" else None
+        method, layer = _layer(recipe, w, s, device, input_scale=torch.full((), 0.05, device=device))
+        out = torch.empty(m, n, dtype=torch.bfloat16, device=device)
+        kernel = _kernel_call(recipe, x, layer, out, bias)
 
-    def run(label, n, k, fn, m=m):
-        for _ in range(warmup):
-            fn()
-        torch.cuda.synchronize()
-        start, end = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
-        start.record()
-        for _ in range(reps):
-            fn()
-        end.record()
-        torch.cuda.synchronize()
-        ms = start.elapsed_time(end) / reps
-        tflops = 2.0 * m * n * k / (ms * 1e-3) / 1e12
-        results[label] = {"M": m, "N": n, "K": k, "ms": round(ms, 4), "tflops": round(tflops, 1),
-                          "frac": round(tflops / FP8_PEAK_TFLOPS, 4)}
+        def layer_call(i, method=method, layer=layer, weights=weights):
+            layer.weight.data = weights[i % len(weights)]
+            method.apply(layer, x, bias)
 
-    fp8 = torch.float8_e4m3fn
-    # rowwise, Qwen2-7B gate_up (Cfg3 shape, M = 4096 between its 2048 and 8192 points)
-    n, k = 37888, 3584
-    a = (torch.randn(m, k, generator=g, device=device) * 50).clamp(-448, 448).to(fp8)
-    w = (torch.randn(n, k, generator=g, device=device) * 50).clamp(-448, 448).to(fp8)
-    sa = torch.rand(m, generator=g, device=device) * 1e-3
-    sb = torch.rand(n, generator=g, device=device) * 1e-3
-    out = torch.empty(m, n, dtype=torch.bfloat16, device=device)
-    run("rowwise_qwen2_gate_up", n, k, lambda: fp8_scaled_mm(a, w.t(), sa, sb, out=out))
-    run("per_tensor_qwen2_gate_up", n, k, lambda: fp8_scaled_mm(a, w.t(), sa[0], sb[0], out=out))
-    del a, w, out
-    # rowwise Qwen2 down (Cfg3) at M = 512 and 2048: few 256 x 256 tiles, so K splits.
-    # Weight-bound sizes: 5 rotated weight copies (340 MB) keep every launch on HBM.
-    n, k = 3584, 18944
-    wds = [(torch.randn(n, k, generator=g, device=device) * 50).clamp(-448, 448).to(fp8) for _ in range(5)]
-    sbd = torch.rand(n, generator=g, device=device) * 1e-3
-    for m_small in (512, 2048):
-        a_s = (torch.randn(m_small, k, generator=g, device=device) * 50).clamp(-448, 448).to(fp8)
-        sa_s = torch.rand(m_small, generator=g, device=device) * 1e-3
-        out_s = torch.empty(m_small, n, dtype=torch.bfloat16, device=device)
-        cyc = itertools.cycle(wds)
-        run(f"rowwise_qwen2_down_m{m_small}", n, k,
-            lambda: fp8_scaled_mm(a_s, next(cyc).t(), sa_s, sbd, out=out_s), m=m_small)
-    del wds, a_s, out_s
-    # block-128, DeepSeek-V3 dense (Cfg4, M = 4096)
-    n, k = 18432, 7168
-    a = (torch.randn(m, k, generator=g, device=device) * 50).clamp(-448, 448).to(fp8)
-    w = (torch.randn(n, k, generator=g, device=device) * 50).clamp(-448, 448).to(fp8)
-    sa = torch.rand(m, k // 128, generator=g, device=device)
-    sb = torch.rand(n // 128, k // 128, generator=g, device=device)
-    out = torch.empty(m, n, dtype=torch.bfloat16, device=device)
-    run("block128_dsv3_18432x7168", n, k, lambda: fp8_blockwise_mm(a, w, sa, sb, out=out))
-    # Cfg4's smaller batches: few tiles, so the K split applies (M = 32: 32-row tiles).
-    # Weight-bound sizes: 3 rotated weight copies (396 MB) keep every launch on HBM.
-    wbs = [w] + [(torch.randn(n, k, generator=g, device=device) * 50).clamp(-448, 448).to(fp8) for _ in range(2)]
-    for m_small in (32, 256):
-        a_s, sa_s = a[:m_small].contiguous(), sa[:m_small].contiguous()
-        out_s = torch.empty(m_small, n, dtype=torch.bfloat16, device=device)
-        cyc = itertools.cycle(wbs)
-        run(f"block128_dsv3_18432x7168_m{m_small}", n, k,
-            lambda: fp8_blockwise_mm(a_s, next(cyc), sa_s, sb, out=out_s), m=m_small)
-    del wbs
-    del a, w, out
-    # MXFP8, Llama-3-70B gate_up (Cfg5 shape, supplemental M = 4096)
-    n, k = 57344, 8192
-    a = (torch.randn(m, k, generator=g, device=device) * 50).clamp(-448, 448).to(fp8)
-    w = (torch.randn(n, k, generator=g, device=device) * 50).clamp(-448, 448).to(fp8)
-    ca = torch.randint(100, 130, (m, k // 32), generator=g, device=device, dtype=torch.uint8)
-    cw = torch.randint(100, 130, (n, k // 32), generator=g, device=device, dtype=torch.uint8)
-    out = torch.empty(m, n, dtype=torch.bfloat16, device=device)
-    run("mxfp8_llama70b_gate_up", n, k, lambda: mxfp8_scaled_mm(a, ca, w, cw, out=out))
-    del a, w, out
-    # INT8 rowwise scaled GEMM, on the Qwen2 gate_up shape
+        kernel_fns = [lambda wt=wt: kernel(wt) for wt in weights]
+        if only is not None:
+            fns = kernel_fns if only_kind == "gemm" else [lambda i=i: layer_call(i) for i in range(len(weights))]
+            ms = _time_rotated(fns, reps, warmup)
+            print(json.dumps({"only": label, "kind": only_kind, "ms": round(ms, 5), "reps": reps}), flush=True)
+            return {}
+        kernel_ms = _time_graph(kernel_fns, reps)
+        layer_ms = _time_graph([lambda i=i: layer_call(i) for i in range(len(weights))], reps)
+        layer.weight.data = w
+        flops = 2.0 * m * n * k
+        nbytes = _kernel_bytes(recipe, m, n, k)
+        tflops = flops / (kernel_ms * 1e-3) / 1e12
+        gbs = nbytes / (kernel_ms * 1e-3) / 1e9
+        bound = "hbm" if flops / nbytes < FP8_PEAK_TFLOPS / HBM_PEAK_GBS * 1e3 else "mfma"
+        results[label] = {
+            "recipe": recipe, "M": m, "N": n, "K": k, "weight_copies": len(weights),
+            "kernel_us": round(kernel_ms * 1e3, 2), "layer_us": round(layer_ms * 1e3, 2),
+            "TFLOP/s": round(tflops, 1), "GB/s": round(gbs, 1), "bound": bound,
+            "frac": round(tflops / FP8_PEAK_TFLOPS if bound == "mfma" else gbs / HBM_PEAK_GBS, 4),
+        }
+        del layer, method, out, x
+    torch.cuda.empty_cache()
+    return results
+
+
+def _gemm_summary(configs):
+    """The M = 4096 line of each recipe (Cfg4's config point; supplemental points for
+    rowwise, per-tensor and MXFP8)."""
+    picks = {"rowwise_qwen2_gate_up": "supp_rowwise/gate_up/M4096",
+             "rowwise_qwen2_down": "supp_rowwise/down/M4096",
+             "per_tensor_qwen2_gate_up": "supp_per_tensor_static/gate_up/M4096",
+             "block128_dsv3_18432x7168": "cfg4_block128/up/M4096",
+             "block128_dsv3_7168x18432": "cfg4_block128/down/M4096",
+             "mxfp8_llama70b_gate_up": "supp_mxfp8/gate_up/M4096",
+             "mxfp8_llama70b_down": "supp_mxfp8/down/M4096"}
+    out = {}
+    for name, label in picks.items():
+        if label in configs:
+            r = configs[label]
+            out[name] = {"M": r["M"], "N": r["N"], "K": r["K"], "us": r["kernel_us"], "tflops": r["TFLOP/s"],
+                         "frac": round(r["TFLOP/s"] / FP8_PEAK_TFLOPS, 4)}
+    return out
+
+
+def _bench_int8(device, reps=POINT_REPS, warmup=POINT_WARMUP):
     from ayaka.kernel.hip import int8_scaled_mm
 
-    n, k = 37888, 3584
+    g = torch.Generator(device=device).manual_seed(0)
+    m, n, k = 4096, 37888, 3584
     a = torch.randint(-128, 128, (m, k), generator=g, device=device, dtype=torch.int8)
     w = torch.randint(-128, 128, (n, k), generator=g, device=device, dtype=torch.int8)
     sa = torch.rand(m, generator=g, device=device) * 1e-4
     sb = torch.rand(n, generator=g, device=device) * 1e-4
     out = torch.empty(m, n, dtype=torch.bfloat16, device=device)
-    run("int8_rowwise_qwen2_gate_up", n, k, lambda: int8_scaled_mm(a, w.t(), sa, sb, out=out))
-    del a, w, out
-    torch.cuda.empty_cache()
-    return results
+    ms = _time_rotated([lambda: int8_scaled_mm(a, w.t(), sa, sb, out=out)], reps, warmup)
+    tops = 2.0 * m * n * k / (ms * 1e-3) / 1e12
+    return {"M": m, "N": n, "K": k, "us": round(ms * 1e3, 2), "tops": round(tops, 1), "frac": round(tops / 5000.0, 4)}
 
 
-def _bench_moe(device, reps=10, warmup=3):
+def _bench_moe(device, reps=20, warmup=5):
     """MoE FP8 block-128 grouped GEMM at the DeepSeek-V3 MoE gate_up shape: 256 experts,
     4096 tokens routed top-8 (32768 rows, per-expert counts from a seeded multinomial),
-    N = 2 x 2048, K = 7168. Useful FLOPs: 2 x rows x N x K."""
+    N = 2 x 2048, K = 7168. Useful FLOPs: 2 x rows x N x K; algorithmic bytes: expert
+    weights + activations + scales + bf16 output."""
     from ayaka.kernel.hip import fp8_blockwise_scaled_grouped_mm
 
     g = torch.Generator(device="cpu").manual_seed(0)
@@ -240,49 +419,23 @@ def _bench_moe(device, reps=10, warmup=3):
     def run():
         fp8_blockwise_scaled_grouped_mm(out, *ptrs, a, b, sa, sb, *strides, *lay, ps_d, off_d, ws)
 
-    for _ in range(warmup):
-        run()
-    torch.cuda.synchronize()
-    start, end = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
-    start.record()
-    for _ in range(reps):
-        run()
-    end.record()
-    torch.cuda.synchronize()
-    ms = start.elapsed_time(end) / reps
+    ms = _time_rotated([run], reps, warmup)
     tflops = 2.0 * rows * n * k / (ms * 1e-3) / 1e12
+    nbytes = experts * n * k + rows * k + 2 * rows * n + 4 * rows * (k // 128) + 4 * experts * (n // 128) * (k // 128)
+    gbs = nbytes / (ms * 1e-3) / 1e9
     result = {"experts": experts, "rows": rows, "N": n, "K": k, "max_rows_per_expert": int(counts.max()),
-              "ms": round(ms, 4), "tflops": round(tflops, 1), "frac": round(tflops / FP8_PEAK_TFLOPS, 4)}
+              "ms": round(ms, 4), "tflops": round(tflops, 1), "mfma_frac": round(tflops / FP8_PEAK_TFLOPS, 4),
+              "bytes": nbytes, "GB/s": round(gbs, 1), "hbm_frac": round(gbs / HBM_PEAK_GBS, 4),
+              "bound": "hbm" if 2.0 * rows * n * k / nbytes < FP8_PEAK_TFLOPS / HBM_PEAK_GBS * 1e3 else "mfma"}
     del a, b, out
     torch.cuda.empty_cache()
     return result
 
 
-def _time_rotated(fns, reps: int, warmup: int) -> float:
-    """Average ms per call over `reps` calls cycling through `fns` (input copies whose
-    total exceeds the 256 MB Infinity Cache, so each call streams from HBM)."""
-    for i in range(warmup):
-        fns[i % len(fns)]()
-    torch.cuda.synchronize()
-    start, end = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
-    start.record()
-    for i in range(reps):
-        fns[i % len(fns)]()
-    end.record()
-    torch.cuda.synchronize()
-    return start.elapsed_time(end) / reps
-
-
-def _hbm_entry(ms: float, nbytes: int, **extra) -> dict:
-    gbs = nbytes / (ms * 1e-3) / 1e9
-    return {**extra, "us": round(ms * 1e3, 2), "bytes": nbytes, "GB/s": round(gbs, 1),
-            "frac": round(gbs / HBM_PEAK_GBS, 4)}
-
-
-def _bench_kv_cache(device, reps=40, warmup=8, copies=4):
+def _bench_kv_cache(device, reps=POINT_REPS, warmup=POINT_WARMUP, copies=4):
     """FP8 KV-cache write (bf16 K/V -> e4m3 pages) and dequantizing gather (e4m3 -> bf16)
     for a 16384-token prefill chunk of Llama-3-8B (8 KV heads x 128) into a 65536-slot
-    cache at shuffled slots, rotating over `copies` sources and caches. Algorithmic bytes:
+    cache at shuffled slots, rotating over ``copies`` sources and caches. Algorithmic bytes:
     write 2 planes x (2 B read + 1 B written) per element + 8 B per slot; gather 1 B read
     + 2 B written per element + 8 B per slot."""
     from ayaka.kernel.hip import gather_cache, write_kv
@@ -312,21 +465,20 @@ def _bench_kv_cache(device, reps=40, warmup=8, copies=4):
     return results
 
 
-def _bench_quant(device, reps=40, warmup=8, copies=6):
+def _bench_quant(device, reps=POINT_REPS, warmup=POINT_WARMUP, copies=6):
     """Activation quantizers on bf16 prefill activations (M = 4096) at the config hidden
-    sizes, rotating over `copies` inputs. Algorithmic bytes: 2 B read + 1 B written per
+    sizes, rotating over ``copies`` inputs. Algorithmic bytes: 2 B read + 1 B written per
     element, plus the scales written."""
     from ayaka.kernel.hip import (per_token_group_quant_fp8, per_token_group_quant_mxfp8, per_token_quant_fp8,
                                   static_quant_fp8)
 
-    g = torch.Generator(device=device).manual_seed(0)
     m = 4096
     results = {}
 
-    def inputs(k):
-        return [torch.randn(m, k, generator=g, device=device).to(torch.bfloat16) for _ in range(copies)]
+    def inputs(k, make):
+        return [make(m, k, device, seed=1 + i) for i in range(copies)]
 
-    xs = inputs(3584)
+    xs = inputs(3584, wl.outlier_activations)
     results["per_token_qwen2_k3584"] = _hbm_entry(
         _time_rotated([lambda x=x: per_token_quant_fp8(x) for x in xs], reps, warmup), m * 3584 * 3 + m * 4, M=m, K=3584)
     scale = torch.full((), 0.05, device=device)
@@ -335,12 +487,12 @@ def _bench_quant(device, reps=40, warmup=8, copies=6):
         _time_rotated([lambda x=x, o=o: static_quant_fp8(x, scale, out=o) for x, o in zip(xs, outs)], reps, warmup),
         m * 3584 * 3, M=m, K=3584)
     del xs, outs
-    xs = inputs(7168)
+    xs = inputs(7168, wl.normal_activations)
     results["group128_dsv3_k7168"] = _hbm_entry(
         _time_rotated([lambda x=x: per_token_group_quant_fp8(x, 128) for x in xs], reps, warmup),
         m * 7168 * 3 + m * 56 * 4, M=m, K=7168)
     del xs
-    xs = inputs(8192)
+    xs = inputs(8192, wl.student_t_activations)
     results["mxfp8_llama70b_k8192"] = _hbm_entry(
         _time_rotated([lambda x=x: per_token_group_quant_mxfp8(x, 32) for x in xs], reps, warmup),
         m * 8192 * 3 + m * 256, M=m, K=8192)
@@ -349,46 +501,26 @@ def _bench_quant(device, reps=40, warmup=8, copies=6):
     return results
 
 
-def _bench_decode_m(layers, reps=20):
-    """W8A16 at the other Cfg2 decode batch sizes (M = 4, 16, 32): GB/s per projection
-    (algorithmic bytes: fp8 weights + scales + bf16 x and out), each launch timed in a
-    graph of back-to-back launches rotating the weight copies."""
-    from ayaka.kernel.hip import fp8_weight_only_gemm
-
-    out = {}
-    for m in (4, 16, 32):
-        row = {}
-        for name, n, k, copies, x in layers:
-            xm = x.reshape(1, k).repeat(m, 1).contiguous()
-            y = torch.empty(m, n, dtype=torch.bfloat16, device=x.device)
-
-            def launches():
-                for i in range(reps):
-                    w, s = copies[i % COPIES]
-                    fp8_weight_only_gemm(xm, w, s.reshape(n, 1), 1, 1, k, "float32", out=y)
-
-            graph = _capture(launches)
-            start, end = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
-            start.record()
-            graph.replay()
-            end.record()
-            end.synchronize()
-            us = start.elapsed_time(end) * 1e3 / reps
-            row[name] = {"us": round(us, 2), "gbs": round(_gemv_bytes(n, k, m) / (us * 1e-6) / 1e9, 1)}
-        out[f"M={m}"] = row
-    return out
+# ------------------------------------------------------------------ CPU baselines
+def _cpu_time(fn, reps=3):
+    fn()  # warmup
+    times = []
+    for _ in range(reps):
+        t0 = time.perf_counter()
+        fn()
+        times.append(time.perf_counter() - t0)
+    return sorted(times)[len(times) // 2]
 
 
 def _cpu_baseline():
     """The reference's CPU path (oracle restatement) on one Cfg2 M = 1 pass."""
     from oracle import fp8_oracle as ora
 
-    threads = os.cpu_count() or 1
-    torch.set_num_threads(threads)
+    torch.set_num_threads(os.cpu_count() or 1)
     g = torch.Generator().manual_seed(0)
     layers = []
     for _, n, k in CFG2_SHAPES:
-        w, s = _quant_rowwise(torch.randn(n, k, generator=g) * 0.02)
+        w, s = wl.quant_rows(torch.randn(n, k, generator=g) * 0.02)
         layers.append((n, k, w, s, torch.randn(1, k, generator=g).to(torch.bfloat16)))
     total_bytes = sum(_gemv_bytes(n, k) for n, k, *_ in layers)
 
@@ -396,24 +528,49 @@ def _cpu_baseline():
         for n, k, w, s, x in layers:
             ora.fp8_linear("w8a16", x, w, s.reshape(n, 1), weight_block=(1, k), scale_dtype="float32")
 
-    one_pass()  # warmup
-    reps = []
-    for _ in range(3):
-        t0 = time.perf_counter()
-        one_pass()
-        reps.append(time.perf_counter() - t0)
-    sec = sorted(reps)[1]
+    sec = _cpu_time(one_pass)
     return {"value": round(total_bytes / sec / 1e9, 3), "unit": "GB/s", "cores": torch.get_num_threads(),
             "kind": "port", "sample": "one Cfg2 M=1 pass (4 projections, 218 MB of fp8 weights), median of 3 after 1 warmup, "
             f"{sec:.2f} s per pass; oracle/fp8_oracle.fp8_linear('w8a16') on torch CPU"}
+
+
+def _cpu_baseline_gemm():
+    """The oracle's recipe composition (quant + GEMM) per GEMM recipe on a sample of each
+    recipe's M = 4096 shape -- 64 activation rows x the first 8192 weight rows -- on this
+    host's cores; TFLOP/s of that sample."""
+    from oracle import fp8_oracle as ora
+
+    torch.set_num_threads(os.cpu_count() or 1)
+    cpu = torch.device("cpu")
+    m = 64
+    out = {}
+    cases = [("rowwise", "cfg3_rowwise", 37888, 3584), ("per_tensor_static", "cfg3_rowwise", 37888, 3584),
+             ("block128", "cfg4_block128", 18432, 7168), ("mxfp8", "cfg5_mxfp8", 57344, 8192),
+             ("w8a16", "cfg2_w8a16", 28672, 4096)]
+    for recipe, cfg, n_full, k in cases:
+        n = min(n_full, 8192)
+        w, s = _weights(cfg, recipe, n, k, cpu, seed=0)
+        x = _activations(cfg, m, k, cpu)
+        name = {"rowwise": "w8a8_rowwise", "per_tensor_static": "w8a8_static_per_tensor",
+                "block128": "w8a8_block128"}.get(recipe, recipe)
+        kw = {"input_scale": torch.tensor(0.05)} if recipe == "per_tensor_static" else {}
+        if recipe == "w8a16":
+            kw = {"weight_block": (1, k), "scale_dtype": "float32"}
+        sec = _cpu_time(lambda: ora.fp8_linear(name, x, w, s, None, **kw), reps=1)
+        out[recipe] = {"value": round(2.0 * m * n * k / sec / 1e12, 4), "unit": "TFLOP/s",
+                       "cores": torch.get_num_threads(), "kind": "port",
+                       "sample": f"{m} x {n} of the {n_full} x {k} weight, {sec:.2f} s; oracle/fp8_oracle.fp8_linear('{name}')"}
+        del w, s, x
+    return out
 
 
 TRAFFIC_PROFILE = os.path.join(ROOT, "profiles", "gemv_gate_up_traffic.md")
 
 
 def _measured_traffic():
-    """HBM bytes per gate_up GEMV launch from the committed counter summary (FETCH_SIZE +
-    WRITE_SIZE, scaled by the copy-kernel calibration it records), or None."""
+    """HBM bytes per gate_up GEMV launch from the committed rocprofv3 counter summary
+    (FETCH_SIZE + WRITE_SIZE of the same launches, scaled by the copy-kernel calibration
+    it records), or None."""
     try:
         with open(TRAFFIC_PROFILE) as f:
             for line in f:
@@ -440,14 +597,22 @@ def main() -> int:
     ap.add_argument("--gpus", type=int, default=1)
     ap.add_argument("--steps", type=int, default=50)
     ap.add_argument("--warmup", type=int, default=10)
-    ap.add_argument("--no-gemm", action="store_true")
+    ap.add_argument("--no-gemm", action="store_true", help="skip the config sweep, MoE and INT8")
     ap.add_argument("--no-cpu", action="store_true")
     ap.add_argument("--copy-probe", action="store_true", help="only run a 256 MiB device copy (counter calibration)")
+    ap.add_argument("--list", action="store_true", help="print the config point labels")
+    ap.add_argument("--only", help="time one config point only (for profilers)")
+    ap.add_argument("--only-kind", choices=("gemm", "layer"), default="gemm")
+    ap.add_argument("--reps", type=int, default=POINT_REPS)
     args = ap.parse_args()
     if args.gpus != 1:
         print(f"bench.py measures one GPU only (got --gpus {args.gpus}); the FP8 linear path is "
               "single-device here and multi-GPU runs are not part of this build", file=sys.stderr)
         return 2
+    if args.list:
+        for label, *_ in _points():
+            print(label)
+        return 0
 
     import ayaka.kernel.hip  # noqa: F401  (registers the ops)
 
@@ -455,6 +620,9 @@ def main() -> int:
     torch.cuda.set_device(device)
     if args.copy_probe:
         _copy_probe(device)
+        return 0
+    if args.only:
+        _bench_configs(device, only=args.only, only_kind=args.only_kind, reps=args.reps)
         return 0
     layers = _make_cfg2(device)
     outs = [torch.empty(n, dtype=torch.bfloat16, device=device) for _, n, _, _, _ in layers]
@@ -507,15 +675,22 @@ def main() -> int:
                      "peak": HBM_PEAK_GBS, "unit": "GB/s", "frac": round(achieved / HBM_PEAK_GBS, 4),
                      "avg_launch_us": round(avg_ms * 1e3, 2), "median_launch_us": round(med_ms * 1e3, 2),
                      "bytes_per_launch": _gemv_bytes(n, k), "traffic": _measured_traffic()},
+        "cfg2_m1_projections": _cfg2_projections(layers),
     }
-    result["decode_w8a16"] = _bench_decode_m(layers)
+    del graphs, layers, outs
+    torch.cuda.empty_cache()
     if not args.no_gemm:
-        result["gemm"] = _bench_gemm(device)
+        configs = _bench_configs(device)
+        result["gemm"] = _gemm_summary(configs)
+        result["gemm"]["int8_rowwise_qwen2_gate_up"] = _bench_int8(device)
+        result["configs"] = configs
         result["moe_grouped_block128"] = _bench_moe(device)
     result["quant"] = _bench_quant(device)
     result["kv_cache"] = _bench_kv_cache(device)
     if not args.no_cpu:
         result["cpu_baseline"] = _cpu_baseline()
+        if not args.no_gemm:
+            result["cpu_baseline_gemm"] = _cpu_baseline_gemm()
     print(json.dumps(result), flush=True)
     return 0
 
