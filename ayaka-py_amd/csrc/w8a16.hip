@@ -509,6 +509,411 @@ int launch_skinny(const SkinnyPlan& p, SkinnyArgs a, size_t ws_bytes, hipStream_
   return AYK_OK;
 }
 
+// ------------------------------------------------------------ row-stream decode kernel
+// Decode batches (M <= 32, K split into whole 256-K stages). A workgroup of four
+// wavefronts owns R = 16 RT weight rows and streams them through LDS in stages of
+// R rows x 256 K bytes, together with the stage's 256 K of every activation row
+// (M rounded up to 8 rows): each direct-to-LDS load instruction moves 4 weight rows x
+// 256 contiguous bytes or 2 activation rows x 512 bytes (whole 128-byte lines), the
+// stages form a ring of D buffers, and one
+// workgroup barrier per stage makes a stage visible and frees the oldest buffer.
+// Wavefront w computes 64-K chunk w of every stage for all R rows, so its partial sums
+// cover a quarter of K and meet the others' in LDS at the end.
+//
+// MFMA v_mfma_f32_16x16x32_{bf16,f16}, weight as operand A. Lane (r = lane % 16,
+// g = lane / 16) reads 16 weight bytes of row r at K [16 g, 16 g + 16) of its chunk and
+// dequantizes them (w * s rounded to the activation dtype, the reference's numerics)
+// into two 8-element operands: the chunk's first MFMA sums K {16 g .. 16 g + 7}, the
+// second K {16 g + 8 .. 16 g + 15}; operand B takes the same K sets of x from the
+// stage (lane (m = lane % 16, g): 32 bytes of x row m at K 16 g). Weight LDS rows are 256 bytes apart, with logical 16-byte chunk c of row r stored at
+// physical chunk c ^ (r % 16): the 16 rows of a fragment read fall on distinct banks.
+constexpr int kRsWaves = 4;
+constexpr int kRsStageK = 256;           // K bytes per stage and row
+constexpr int kRsChunk = kRsStageK / kRsWaves;  // 64 K per wavefront per stage
+
+struct RsArgs {
+  const uint16_t* x;
+  int64_t ldx;
+  int64_t M;
+  const uint8_t* w;
+  int64_t ldw;
+  int64_t N, K;
+  const void* scale;
+  int scale_dtype;
+  int64_t srs, by, bx;
+  uint16_t* out;
+  int64_t ldo;
+  float* part;          // [split, M, N] when gridDim.y > 1
+  int64_t k_per_split;  // multiple of kRsStageK
+};
+
+typedef float v4f __attribute__((ext_vector_type(4)));
+// One 16-byte direct-to-LDS load per lane (a device function: the builtin inside a
+// lambda of a kernel template loses the kernel's host-side launch stub).
+__device__ inline void dma16(const uint8_t* src, uint8_t* lds_dst) {
+  __builtin_amdgcn_global_load_lds(src, (__attribute__((address_space(3))) void*)lds_dst, 16, 0, 0);
+}
+// One 4-byte direct-to-LDS load per lane (lane i writes lds_dst + 4 i).
+__device__ inline void dma4(const uint8_t* src, uint8_t* lds_dst) {
+  __builtin_amdgcn_global_load_lds(src, (__attribute__((address_space(3))) void*)lds_dst, 4, 0, 0);
+}
+__device__ inline uint32_t lds_addr(const uint8_t* p) {
+  return (uint32_t)(uintptr_t)(const __attribute__((address_space(3))) uint8_t*)p;
+}
+// All LDS reads of one stage in one assembly statement that ends with
+// s_waitcnt lgkmcnt(0): NB 16-byte reads into b, NS 4-byte reads into w. The compiler
+// cannot relate these reads to the direct-to-LDS loads in flight into other stage
+// buffers (it would otherwise wait for every one of them first), and every result
+// register is final when the statement ends.
+typedef uint32_t v4u __attribute__((ext_vector_type(4)));
+#define AYK_R128(o, i) "ds_read_b128 %" #o ", %" #i "\n\t"
+#define AYK_R32(o, i) "ds_read_b32 %" #o ", %" #i "\n\t"
+template <int NB, int NS>
+__device__ inline void stage_reads(v4u (&b)[NB], uint32_t (&w)[NS], const uint32_t (&ab)[NB], const uint32_t (&as)[NS]);
+template <>
+__device__ inline void stage_reads<4, 2>(v4u (&b)[4], uint32_t (&w)[2], const uint32_t (&ab)[4], const uint32_t (&as)[2]) {
+  asm volatile(AYK_R128(0, 6) AYK_R128(1, 7) AYK_R128(2, 8) AYK_R128(3, 9) AYK_R32(4, 10) AYK_R32(5, 11)
+               "s_waitcnt lgkmcnt(0)"
+               : "=&v"(b[0]), "=&v"(b[1]), "=&v"(b[2]), "=&v"(b[3]), "=&v"(w[0]), "=&v"(w[1])
+               : "v"(ab[0]), "v"(ab[1]), "v"(ab[2]), "v"(ab[3]), "v"(as[0]), "v"(as[1])
+               : "memory");
+}
+template <>
+__device__ inline void stage_reads<6, 2>(v4u (&b)[6], uint32_t (&w)[2], const uint32_t (&ab)[6], const uint32_t (&as)[2]) {
+  asm volatile(AYK_R128(0, 8) AYK_R128(1, 9) AYK_R128(2, 10) AYK_R128(3, 11) AYK_R128(4, 12) AYK_R128(5, 13)
+               AYK_R32(6, 14) AYK_R32(7, 15) "s_waitcnt lgkmcnt(0)"
+               : "=&v"(b[0]), "=&v"(b[1]), "=&v"(b[2]), "=&v"(b[3]), "=&v"(b[4]), "=&v"(b[5]), "=&v"(w[0]), "=&v"(w[1])
+               : "v"(ab[0]), "v"(ab[1]), "v"(ab[2]), "v"(ab[3]), "v"(ab[4]), "v"(ab[5]), "v"(as[0]), "v"(as[1])
+               : "memory");
+}
+template <>
+__device__ inline void stage_reads<6, 4>(v4u (&b)[6], uint32_t (&w)[4], const uint32_t (&ab)[6], const uint32_t (&as)[4]) {
+  asm volatile(AYK_R128(0, 10) AYK_R128(1, 11) AYK_R128(2, 12) AYK_R128(3, 13) AYK_R128(4, 14) AYK_R128(5, 15)
+               AYK_R32(6, 16) AYK_R32(7, 17) AYK_R32(8, 18) AYK_R32(9, 19) "s_waitcnt lgkmcnt(0)"
+               : "=&v"(b[0]), "=&v"(b[1]), "=&v"(b[2]), "=&v"(b[3]), "=&v"(b[4]), "=&v"(b[5]),
+                 "=&v"(w[0]), "=&v"(w[1]), "=&v"(w[2]), "=&v"(w[3])
+               : "v"(ab[0]), "v"(ab[1]), "v"(ab[2]), "v"(ab[3]), "v"(ab[4]), "v"(ab[5]),
+                 "v"(as[0]), "v"(as[1]), "v"(as[2]), "v"(as[3])
+               : "memory");
+}
+template <>
+__device__ inline void stage_reads<8, 4>(v4u (&b)[8], uint32_t (&w)[4], const uint32_t (&ab)[8], const uint32_t (&as)[4]) {
+  asm volatile(AYK_R128(0, 12) AYK_R128(1, 13) AYK_R128(2, 14) AYK_R128(3, 15) AYK_R128(4, 16) AYK_R128(5, 17)
+               AYK_R128(6, 18) AYK_R128(7, 19) AYK_R32(8, 20) AYK_R32(9, 21) AYK_R32(10, 22) AYK_R32(11, 23)
+               "s_waitcnt lgkmcnt(0)"
+               : "=&v"(b[0]), "=&v"(b[1]), "=&v"(b[2]), "=&v"(b[3]), "=&v"(b[4]), "=&v"(b[5]), "=&v"(b[6]), "=&v"(b[7]),
+                 "=&v"(w[0]), "=&v"(w[1]), "=&v"(w[2]), "=&v"(w[3])
+               : "v"(ab[0]), "v"(ab[1]), "v"(ab[2]), "v"(ab[3]), "v"(ab[4]), "v"(ab[5]), "v"(ab[6]), "v"(ab[7]),
+                 "v"(as[0]), "v"(as[1]), "v"(as[2]), "v"(as[3])
+               : "memory");
+}
+#undef AYK_R128
+#undef AYK_R32
+template <bool BF16>
+__device__ inline v4f mfma16x16(const v8s& a, const v8s& b, const v4f& c) {
+  if constexpr (BF16) {
+    return __builtin_amdgcn_mfma_f32_16x16x32_bf16(__builtin_bit_cast(v8bf, a), __builtin_bit_cast(v8bf, b), c, 0, 0, 0);
+  } else {
+    return __builtin_amdgcn_mfma_f32_16x16x32_f16(__builtin_bit_cast(v8h, a), __builtin_bit_cast(v8h, b), c, 0, 0, 0);
+  }
+}
+
+template <bool BF16, bool ROW_SCALE, int RT, int XJ, int D>
+__global__ __launch_bounds__(kRsWaves * kWave) void w8a16_rows_kernel(RsArgs a) {
+  constexpr int R = 16 * RT;
+  constexpr int MP = 8 * XJ;                 // activation rows staged (M rounded up to 8)
+  constexpr int MT = MP > 16 ? 2 : 1;        // 16-column MFMA tiles
+  constexpr int kWBytes = R * kRsStageK;     // weight part of a stage
+  constexpr int kXRow = 2 * kRsStageK;       // bytes of one activation row of a stage
+  constexpr int kXBytes = MP * kXRow;
+  // Per-stage scale words (block scales only): entry (row, 16-K group) of the stage.
+  constexpr int kSBytes = ROW_SCALE ? 0 : R * (kRsStageK / 16) * 4;
+  constexpr int kStageBytes = kWBytes + kXBytes + kSBytes;
+  constexpr int kDma = R / (4 * kRsWaves);   // weight load instructions per wavefront per stage
+  constexpr int kSDma = ROW_SCALE ? 0 : RT;  // scale load instructions per wavefront per stage
+  static_assert(R % (4 * kRsWaves) == 0, "whole load instructions per wavefront");
+  static_assert(R * (kRsStageK / 16) == kRsWaves * kSDma * kWave || ROW_SCALE, "scale entries per stage");
+  static_assert(D == 4, "four stage buffers");
+  // Four distinct LDS objects for the ring, and the per-row scale words (lane i of the
+  // one load writes word i).
+  __shared__ __attribute__((aligned(1024))) uint8_t B0[kStageBytes];
+  __shared__ __attribute__((aligned(1024))) uint8_t B1[kStageBytes];
+  __shared__ __attribute__((aligned(1024))) uint8_t B2[kStageBytes];
+  __shared__ __attribute__((aligned(1024))) uint8_t B3[kStageBytes];
+  __shared__ __attribute__((aligned(256))) uint8_t SROW[ROW_SCALE ? 4 * kWave : 4];
+  auto stage_buf = [&](int d) -> uint8_t* { return d == 0 ? B0 : (d == 1 ? B1 : (d == 2 ? B2 : B3)); };
+  const int lane = threadIdx.x & (kWave - 1);
+  const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x / kWave);
+  const int r16 = lane & 15, g = lane >> 4;
+  const int64_t n_base = (int64_t)blockIdx.x * R;
+  const int64_t kbeg = (int64_t)blockIdx.y * a.k_per_split;
+  const int64_t klen = a.K - kbeg < a.k_per_split ? a.K - kbeg : a.k_per_split;
+  const int ns = (int)(klen / kRsStageK);
+  const int ssize = a.scale_dtype == AYK_F32 ? 4 : (a.scale_dtype == AYK_U8 ? 1 : 2);
+  const uintptr_t sbase = reinterpret_cast<uintptr_t>(a.scale);
+  // Scale element i is read as the aligned dword that holds it (in the same page, so
+  // always readable) and shifted out after the read.
+  auto scale_word = [&](int64_t i) { return reinterpret_cast<const uint8_t*>((sbase + (uintptr_t)(i * ssize)) & ~(uintptr_t)3); };
+  auto scale_shift = [&](int64_t i) { return (uint32_t)((sbase + (uintptr_t)(i * ssize)) & 3) * 8; };
+
+  // Weight DMA: load instruction j (0 .. kDma - 1) of wavefront w covers rows
+  // 4 (w kDma + j) + lane / 16; lane fetches the logical chunk that lands at physical
+  // chunk lane % 16 of its row.
+  constexpr int kOps = kDma + XJ + kSDma;  // vector-memory instructions per stage and wavefront
+  const uint8_t* dsrc[kDma + XJ];
+  int dlds[kDma + XJ];
+#pragma unroll
+  for (int j = 0; j < kDma; ++j) {
+    const int row = 4 * (wave * kDma + j) + (lane >> 4);
+    const int64_t n = n_base + row < a.N ? n_base + row : a.N - 1;  // rows past N re-read row N - 1
+    const int chunk = (lane & 15) ^ (row & 15);
+    dsrc[j] = a.w + n * a.ldw + kbeg + chunk * 16;
+    dlds[j] = __builtin_amdgcn_readfirstlane(4 * (wave * kDma + j) * kRsStageK);
+  }
+  // Activation DMA: instruction j of wavefront w covers activation rows 2 (4 j + w) and
+  // 2 (4 j + w) + 1 (512 bytes each: 32 chunks of 16 bytes); logical chunk c of row m
+  // sits at physical chunk c ^ 2 (m % 16), so the 16 rows of a fragment read (32
+  // contiguous bytes each) fall on distinct banks. Rows past M re-read row M - 1.
+#pragma unroll
+  for (int j = 0; j < XJ; ++j) {
+    const int row = 2 * (4 * j + wave) + (lane >> 5);
+    const int64_t m = row < a.M ? row : a.M - 1;
+    const int chunk = (lane & 31) ^ ((row & 15) << 1);
+    dsrc[kDma + j] = reinterpret_cast<const uint8_t*>(a.x + m * a.ldx + kbeg + chunk * 8);
+    dlds[kDma + j] = __builtin_amdgcn_readfirstlane(kWBytes + 2 * (4 * j + wave) * kXRow);
+  }
+  // Per-stage scale DMA (block scales): instruction j of wavefront w loads entries
+  // e = 64 (w kSDma + j) + lane, i.e. row e / 16 and 16-K group e % 16 of the stage.
+  int64_t srow_idx[kSDma > 0 ? kSDma : 1];
+  int sgrp_k[kSDma > 0 ? kSDma : 1];
+#pragma unroll
+  for (int j = 0; j < kSDma; ++j) {
+    const int e = kWave * (wave * kSDma + j) + lane;
+    const int64_t n = n_base + e / 16 < a.N ? n_base + e / 16 : a.N - 1;
+    srow_idx[j] = (int64_t)((uint64_t)n / (uint64_t)a.by) * a.srs;
+    sgrp_k[j] = 16 * (e % 16);
+  }
+
+  // LDS read addresses (relative to the stage buffer) and scale decoding per row tile.
+  uint32_t xoff[2 * MT], woff[RT], soff[RT];
+#pragma unroll
+  for (int mt = 0; mt < MT; ++mt) {
+    const int m = 16 * mt + r16 < a.M ? 16 * mt + r16 : (int)a.M - 1;  // columns past M repeat row M - 1
+    const int c = 2 * (4 * wave + g);
+    xoff[2 * mt] = kWBytes + m * kXRow + ((c ^ ((m & 15) << 1)) << 4);
+    xoff[2 * mt + 1] = kWBytes + m * kXRow + (((c + 1) ^ ((m & 15) << 1)) << 4);
+  }
+  int64_t rowbase[RT];
+  uint32_t shift[RT];
+#pragma unroll
+  for (int rt = 0; rt < RT; ++rt) {
+    const int row = 16 * rt + r16;
+    woff[rt] = row * kRsStageK + (((4 * wave + g) ^ (row & 15)) << 4);
+    const int64_t n = n_base + row < a.N ? n_base + row : a.N - 1;
+    rowbase[rt] = (int64_t)((uint64_t)n / (uint64_t)a.by) * a.srs;
+    soff[rt] = ROW_SCALE ? 4 * row : kWBytes + kXBytes + 4 * (row * (kRsStageK / 16) + 4 * wave + g);
+    shift[rt] = scale_shift(rowbase[rt]);
+  }
+
+  if constexpr (ROW_SCALE) {
+    // One load by wavefront 0, older than every stage: the first stage's wait and
+    // barrier make it visible.
+    if (wave == 0) {
+      const int row = lane < R ? lane : R - 1;
+      const int64_t n = n_base + row < a.N ? n_base + row : a.N - 1;
+      dma4(scale_word((int64_t)((uint64_t)n / (uint64_t)a.by) * a.srs), SROW);
+    }
+  }
+
+  // Stage s (clamped to the last stage: the ring is always full; a clamped stage lands
+  // in a buffer that no later stage reads) into ring slot d.
+  auto issue = [&](int d, int s) {
+    const int sc = s < ns ? s : ns - 1;
+    const int64_t ks = (int64_t)sc * kRsStageK;
+#pragma unroll
+    for (int j = 0; j < kDma; ++j) dma16(dsrc[j] + ks, stage_buf(d) + dlds[j]);
+#pragma unroll
+    for (int j = 0; j < XJ; ++j) dma16(dsrc[kDma + j] + 2 * ks, stage_buf(d) + dlds[kDma + j]);
+#pragma unroll
+    for (int j = 0; j < kSDma; ++j) {
+      const int64_t i = srow_idx[j] + (uint32_t)(kbeg + ks + sgrp_k[j]) / (uint32_t)a.bx;
+      dma4(scale_word(i), stage_buf(d) + kWBytes + kXBytes + __builtin_amdgcn_readfirstlane(4 * kWave * (wave * kSDma + j)));
+    }
+  };
+
+  v4f acc[RT][MT];
+#pragma unroll
+  for (int rt = 0; rt < RT; ++rt)
+#pragma unroll
+    for (int mt = 0; mt < MT; ++mt) acc[rt][mt] = v4f{0.0f, 0.0f, 0.0f, 0.0f};
+  auto compute = [&](int d, int s) {
+    const uint32_t base = lds_addr(stage_buf(d));
+    const uint32_t sb = ROW_SCALE ? lds_addr(SROW) : base;
+    uint32_t ab[2 * MT + RT], as[RT];
+#pragma unroll
+    for (int i = 0; i < 2 * MT; ++i) ab[i] = base + xoff[i];
+#pragma unroll
+    for (int rt = 0; rt < RT; ++rt) {
+      ab[2 * MT + rt] = base + woff[rt];
+      as[rt] = sb + soff[rt];
+    }
+    v4u v[2 * MT + RT];
+    uint32_t sw[RT];
+    stage_reads<2 * MT + RT, RT>(v, sw, ab, as);
+    uint32_t sh[RT];
+    if constexpr (ROW_SCALE) {
+#pragma unroll
+      for (int rt = 0; rt < RT; ++rt) sh[rt] = shift[rt];
+    } else {
+      // 16 consecutive K of a lane share one scale (bx % 16 == 0, checked on the host)
+      const int64_t kidx = (uint32_t)(kbeg + (int64_t)s * kRsStageK + 16 * (4 * wave + g)) / (uint32_t)a.bx;
+#pragma unroll
+      for (int rt = 0; rt < RT; ++rt) sh[rt] = scale_shift(rowbase[rt] + kidx);
+    }
+#pragma unroll
+    for (int rt = 0; rt < RT; ++rt) {
+      const v4u wq = v[2 * MT + rt];
+      const float sc = bits_to_f32(RawBits{sw[rt], sh[rt]}, a.scale_dtype);
+      const v8s lo = convert8<BF16>(wq[0], wq[1], sc);
+      const v8s hi = convert8<BF16>(wq[2], wq[3], sc);
+#pragma unroll
+      for (int mt = 0; mt < MT; ++mt) {
+        acc[rt][mt] = mfma16x16<BF16>(lo, __builtin_bit_cast(v8s, v[2 * mt]), acc[rt][mt]);
+        acc[rt][mt] = mfma16x16<BF16>(hi, __builtin_bit_cast(v8s, v[2 * mt + 1]), acc[rt][mt]);
+      }
+    }
+  };
+
+  // Ring: stages 0 .. D - 2 in flight; at stage s, wait for it (D - 2 younger stages may
+  // still be in flight), barrier (stage s visible; nobody reads stage s - 1 any more),
+  // refill that buffer with stage s + D - 1, compute stage s.
+#pragma unroll
+  for (int d = 0; d < D - 1; ++d) issue(d, d);
+  for (int s0 = 0; s0 < ns; s0 += D) {
+#pragma unroll
+    for (int d = 0; d < D; ++d) {
+      const int s = s0 + d;
+      if (s < ns) {  // workgroup-uniform
+        wait_vmcnt<(D - 2) * kOps>();
+        __builtin_amdgcn_s_barrier();
+        issue((d + D - 1) % D, s + D - 1);
+        compute(d, s);
+      }
+    }
+  }
+  wait_vmcnt<0>();
+  __syncthreads();
+
+  // Partial sums of the four wavefronts meet in LDS (the ring is free: wavefront w
+  // writes stage buffer w); wavefront w finishes tile pairs w, w + 4, ... in a fixed
+  // order. D[n][m]: lane holds m = lane % 16 and n = 4 (lane / 16) + r of its 16 x 16 tile.
+  static_assert(RT * MT * 4 * kWave * 4 <= kStageBytes, "a wavefront's partials fit one stage buffer");
+  auto red_at = [&](int w, int slot) { return reinterpret_cast<float*>(stage_buf(w)) + (slot * kWave + lane); };
+#pragma unroll
+  for (int rt = 0; rt < RT; ++rt)
+#pragma unroll
+    for (int mt = 0; mt < MT; ++mt)
+#pragma unroll
+      for (int r = 0; r < 4; ++r) *red_at(wave, (rt * MT + mt) * 4 + r) = acc[rt][mt][r];
+  __syncthreads();
+  for (int p = wave; p < RT * MT; p += kRsWaves) {
+    const int rt = p / MT, mt = p % MT;
+    const int64_t m = 16 * mt + r16;
+    const int64_t n0 = n_base + 16 * rt + 4 * g;
+    if (m >= a.M) continue;
+#pragma unroll
+    for (int r = 0; r < 4; ++r) {
+      float v = *red_at(0, p * 4 + r);
+#pragma unroll
+      for (int w2 = 1; w2 < kRsWaves; ++w2) v += *red_at(w2, p * 4 + r);
+      const int64_t n = n0 + r;
+      if (n >= a.N) continue;
+      if (gridDim.y == 1) a.out[m * a.ldo + n] = round16<BF16>(v);
+      else a.part[((int64_t)blockIdx.y * a.M + m) * a.N + n] = v;
+    }
+  }
+}
+
+template <bool BF16>
+__global__ __launch_bounds__(256) void w8a16_rows_reduce(RsArgs a, int split) {
+  const int64_t i = (int64_t)blockIdx.x * 256 + threadIdx.x;
+  const int64_t mn = a.M * a.N;
+  if (i >= mn) return;
+  float v = 0.0f;
+  for (int s = 0; s < split; ++s) v += a.part[(int64_t)s * mn + i];
+  const int64_t m = i / a.N, n = i - m * a.N;
+  a.out[m * a.ldo + n] = round16<BF16>(v);
+}
+
+// Launch plan from the shapes alone (the workspace query reproduces it). R = 64 rows
+// per workgroup for M > 16 when that still gives >= 384 workgroups (the activation
+// stage is then shared by more rows), else 32. K is split across workgroups only while
+// each split keeps >= 4096 K and there are < 512 workgroups: a split costs a second
+// launch and fp32 partials, which measured slower than fewer workgroups at K = 4096
+// (Llama-3-8B qkv / o / gate_up) and faster at K = 14336 (down, split 2).
+struct RsPlan {
+  bool ok;
+  int rt, xj, split;  // xj: activation rows staged / 8
+  int64_t kps;
+};
+RsPlan rows_plan(int64_t M, int64_t N, int64_t K, int64_t bx) {
+  RsPlan p{};
+  const bool row_scale = bx >= K;
+  if (M < 2 || M > 32 || N < 1 || K < kRsStageK || K % kRsStageK || K >= (int64_t(1) << 31) || (!row_scale && bx % 16)) return p;
+  p.xj = (int)cdiv(M, 8);
+  p.rt = M > 16 && cdiv(N, 64) >= 384 ? 4 : 2;
+  const int64_t tiles = cdiv(N, 16 * p.rt);
+  int64_t split = 1;
+  while (tiles * split < 512 && K / (split * 2) >= 4096 && (K / kRsStageK) % (split * 2) == 0) split *= 2;
+  p.kps = K / split;
+  p.split = (int)split;
+  p.ok = cdiv(N, 16 * p.rt) <= 0x7FFFFFFF;
+  return p;
+}
+size_t rows_workspace(const RsPlan& p, int64_t M, int64_t N) {
+  return p.ok && p.split > 1 ? (size_t)p.split * (size_t)M * (size_t)N * sizeof(float) : 0;
+}
+
+template <bool BF16, bool ROW_SCALE>
+void launch_rows_kernel(const RsPlan& p, const RsArgs& a, hipStream_t st) {
+  const dim3 grid((unsigned)cdiv(a.N, 16 * p.rt), (unsigned)p.split), block(kRsWaves * kWave);
+  constexpr int D = 4;
+  if (p.rt == 4) {
+    switch (p.xj) {
+      case 1: hipLaunchKernelGGL((w8a16_rows_kernel<BF16, ROW_SCALE, 4, 1, D>), grid, block, 0, st, a); break;
+      case 2: hipLaunchKernelGGL((w8a16_rows_kernel<BF16, ROW_SCALE, 4, 2, D>), grid, block, 0, st, a); break;
+      case 3: hipLaunchKernelGGL((w8a16_rows_kernel<BF16, ROW_SCALE, 4, 3, D>), grid, block, 0, st, a); break;
+      default: hipLaunchKernelGGL((w8a16_rows_kernel<BF16, ROW_SCALE, 4, 4, D>), grid, block, 0, st, a); break;
+    }
+  } else {
+    switch (p.xj) {
+      case 1: hipLaunchKernelGGL((w8a16_rows_kernel<BF16, ROW_SCALE, 2, 1, D>), grid, block, 0, st, a); break;
+      case 2: hipLaunchKernelGGL((w8a16_rows_kernel<BF16, ROW_SCALE, 2, 2, D>), grid, block, 0, st, a); break;
+      case 3: hipLaunchKernelGGL((w8a16_rows_kernel<BF16, ROW_SCALE, 2, 3, D>), grid, block, 0, st, a); break;
+      default: hipLaunchKernelGGL((w8a16_rows_kernel<BF16, ROW_SCALE, 2, 4, D>), grid, block, 0, st, a); break;
+    }
+  }
+}
+
+template <bool BF16>
+int launch_rows(const RsPlan& p, RsArgs a, size_t ws_bytes, hipStream_t st) {
+  a.k_per_split = p.kps;
+  if (p.split > 1) {
+    const size_t need = rows_workspace(p, a.M, a.N);
+    if (a.part == nullptr || ws_bytes < need) {
+      return fail(AYK_EWORKSPACE, "fp8_weight_only_gemm: workspace of %zu bytes required, %zu given", need, ws_bytes);
+    }
+  }
+  if (a.bx >= a.K) launch_rows_kernel<BF16, true>(p, a, st);
+  else launch_rows_kernel<BF16, false>(p, a, st);
+  if (int rc = check_launch("fp8_weight_only_gemm")) return rc;
+  if (p.split > 1) {
+    hipLaunchKernelGGL((w8a16_rows_reduce<BF16>), dim3((unsigned)cdiv(a.M * a.N, 256)), dim3(256), 0, st, a, p.split);
+    return check_launch("fp8_weight_only_gemm");
+  }
+  return AYK_OK;
+}
+
 template <bool BF16, int BN, int BM, int WN, int WM>
 int launch_w16(W16Args g, hipStream_t st) {
   g.tiles_m = (int)cdiv(g.M, BM);
@@ -534,7 +939,10 @@ extern "C" {
 
 size_t ayk_fp8_weight_only_gemm_workspace_bytes(int64_t M, int64_t N, int64_t K, int64_t block_size_x) {
   if (M < 2) return 0;
-  return skinny_workspace(skinny_plan(M, N, K, block_size_x), M, N);
+  // An upper bound over the two decode kernels (alignment decides which one runs).
+  const size_t rs = rows_workspace(rows_plan(M, N, K, block_size_x), M, N);
+  const size_t sk = skinny_workspace(skinny_plan(M, N, K, block_size_x), M, N);
+  return rs > sk ? rs : sk;
 }
 
 int ayk_fp8_weight_only_gemm(const void* x, int x_dtype, int64_t ldx, int64_t M, const void* w,
@@ -570,8 +978,20 @@ int ayk_fp8_weight_only_gemm(const void* x, int x_dtype, int64_t ldx, int64_t M,
   g.out = static_cast<uint16_t*>(out);
   g.ldo = ldo;
   hipStream_t st = static_cast<hipStream_t>(stream);
-  // Decode batch sizes: the skinny streaming kernel (whole 128-K steps, scale blocks
-  // of >= 32 K, activation rows 16-byte aligned).
+  // Decode batch sizes: the row-stream kernel (whole 256-K stages, scale blocks of
+  // whole 16 K), else the skinny streaming kernel (whole 128-K steps, scale blocks of
+  // >= 32 K); both need 16-byte aligned activation rows.
+  if (M >= 2 && ldx % 8 == 0) {
+    const RsPlan rp = rows_plan(M, N, K, block_size_x);
+    if (rp.ok) {
+      RsArgs a{};
+      a.x = g.x; a.ldx = ldx; a.M = M; a.w = g.w; a.ldw = ldw; a.N = N; a.K = K;
+      a.scale = scale; a.scale_dtype = scale_dtype; a.srs = scale_row_stride; a.by = block_size_y; a.bx = block_size_x;
+      a.out = g.out; a.ldo = ldo; a.part = static_cast<float*>(workspace);
+      return x_dtype == AYK_BF16 ? launch_rows<true>(rp, a, workspace_bytes, st)
+                                 : launch_rows<false>(rp, a, workspace_bytes, st);
+    }
+  }
   if (M >= 2 && ldx % 8 == 0) {
     const SkinnyPlan p = skinny_plan(M, N, K, block_size_x);
     if (p.ok) {

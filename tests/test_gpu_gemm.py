@@ -437,6 +437,45 @@ def test_weight_only_gemm(gpu, m, case):
     assert_linear_close(y, ref, "weight_only_gemm")
 
 
+def _weight_only_operands(n, k, case, seed=10):
+    w = _fp8((n, k), seed=seed)
+    if case == "channel":
+        by, bx, sdt = 1, k, "float32"
+        scale = torch.rand(n, 1, generator=_gen(1)) * 0.01 + 1e-3
+    elif case == "channel_e8m0":
+        by, bx, sdt = 1, k, "e8m0"
+        scale = torch.randint(115, 125, (n, 1), generator=_gen(1), dtype=torch.uint8)
+    elif case == "block128":
+        by, bx, sdt = 128, 128, "bfloat16"
+        scale = (torch.rand(-(-n // 128), k // 128, generator=_gen(1)) * 0.01 + 1e-3).to(torch.bfloat16)
+    else:
+        by, bx, sdt = 1, 32, "e8m0"
+        scale = torch.randint(115, 125, (n, k // 32), generator=_gen(1), dtype=torch.uint8)
+    return w, scale, by, bx, sdt
+
+
+# Decode-batch launch plans: a K split of 2 and 4 (K >= 8192, few row tiles), 64-row
+# tiles (M > 16, N >= 384 * 64), activation rows padded to 8 (M = 5, 9, 13, 27), row
+# counts that are not a multiple of the tile, every scale dtype, fp16 activations.
+@pytest.mark.parametrize("m,n,k,case,xdt", [
+    (5, 600, 8192, "channel", torch.bfloat16),
+    (27, 24640, 512, "block128", torch.bfloat16),
+    (13, 100, 16384, "e8m0_32", torch.float16),
+    (9, 200, 768, "channel_e8m0", torch.bfloat16),
+    (32, 24576, 256, "channel", torch.float16),
+])
+def test_weight_only_gemm_decode_plans(gpu, m, n, k, case, xdt):
+    from ayaka.kernel.hip import fp8_weight_only_gemm
+
+    _say(f"fp8_weight_only_gemm decode plan m={m} n={n} k={k} case={case} x={xdt}")
+    w, scale, by, bx, sdt = _weight_only_operands(n, k, case)
+    x = torch.randn(m, k, generator=_gen(2)).to(xdt)
+    y = fp8_weight_only_gemm(x.to(gpu), w.to(gpu), scale.to(gpu), -(-k // bx), by, bx, sdt)
+    ref = ora.fp8_weight_only_gemm(x, w, scale, -(-k // bx), by, bx, sdt)
+    assert y.dtype == xdt
+    assert_linear_close(y, ref, "weight_only_gemm decode plan")
+
+
 # ------------------------------------------------------------------ linear entry points
 @pytest.mark.parametrize("m", [1, 8, 40])
 @pytest.mark.parametrize("recipe", ["w8a8_rowwise", "w8a8_dynamic_per_tensor", "w8a8_block128"])
