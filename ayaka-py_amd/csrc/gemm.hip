@@ -703,8 +703,8 @@ __global__ __launch_bounds__(kThreads, 1) void fp8_gemm_big_kernel(GemmArgs g) {
 // halves the L2 requests per byte (an L2-resident probe reads 57 B/cycle per compute
 // unit with the wide shape against 29 with the narrow one). Stage buffers therefore
 // hold a pair of steps: two 64 KB pair buffers, the second pair's loads in flight while
-// the first is multiplied. The fragment reads, the MFMA order and the epilogue are the
-// narrow kernel's.
+// the first is multiplied. The fragment layout, the MFMA order and the epilogue are the
+// narrow kernel's; the step schedule (one barrier per pair) is its own.
 template <int MODE>
 __global__ __launch_bounds__(kThreads, 1) void fp8_gemm_pair_kernel(GemmArgs gin) {
   // Rowwise / MX K split (as in the general kernel): blockIdx.y's K range, scaled fp32
@@ -876,7 +876,6 @@ __global__ __launch_bounds__(kThreads, 1) void fp8_gemm_pair_kernel(GemmArgs gin
         }
       }
   };
-  constexpr int kHead = 1;  // m-fragments multiplied before the step's barrier
 
   const BigScales scales = load_big_scales<MODE>(g, m_base, n_base);
   // Prologue: pairs 0 and 1 in flight (pair 0's codes between them), pair 0 visible,
@@ -889,20 +888,22 @@ __global__ __launch_bounds__(kThreads, 1) void fp8_gemm_pair_kernel(GemmArgs gin
   read_frags(0, P0, 0);
   read_codes(0, 0);
 
-  // Pair p in `cur`, pair p + 1 in flight into `nxt`. Its first step: the barrier (the
-  // whole pair has landed) certifies every wavefront has its step fragments, then the
-  // second step's fragments are read from the same buffer. Its second step: "pair p + 1
-  // has landed" (nothing else is in flight) and a barrier, after which no wavefront reads
-  // `cur` any more: pair p + 2 is issued into it and the next pair's first fragments are
-  // read from `nxt`.
+  // Pair p in `cur`, pair p + 1 in flight into `nxt`, one barrier per pair. Step 0: the
+  // 16 MFMAs of fragment set 0 interleaved one for one with the reads of step 1's
+  // fragments (set 1) from `cur`. Step 1: wait for pair p + 1 and for this wavefront's
+  // reads, barrier (pair p + 1 is visible and nobody reads `cur` any more), read the
+  // next pair's codes, issue pair p + 2 into `cur`, then the 16 MFMAs of set 1
+  // interleaved with the direct loads and with the reads of pair p + 1's step 0
+  // fragments from `nxt`. Left to itself the scheduler puts all reads after the MFMAs,
+  // and their latency then stalls the next step's first MFMA.
   auto pair = [&](int p, uint8_t* cur, uint8_t* nxt) {
-    mfmas(0, 0, kHead);
-    __builtin_amdgcn_sched_barrier(0);
-    lds_barrier();
-    __builtin_amdgcn_sched_barrier(0);
     read_frags(1, cur, 1);
-    mfmas(0, kHead, FM);
-    mfmas(1, 0, kHead);
+    mfmas(0, 0, FM);
+#pragma unroll
+    for (int i = 0; i < FN * FM; ++i) {
+      __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);  // one MFMA
+      __builtin_amdgcn_sched_group_barrier(0x100, 1, 0);  // one LDS read
+    }
     __builtin_amdgcn_sched_barrier(0);
     wait_vmcnt<0>();
     lds_barrier();
@@ -913,7 +914,14 @@ __global__ __launch_bounds__(kThreads, 1) void fp8_gemm_pair_kernel(GemmArgs gin
     issue(p + 2 < npairs ? p + 2 : npairs - 1, cur);
     if (MODE == MODE_MX && ((p + 2) & 3) == 0 && p + 2 < npairs) issue_codes((p + 2) >> 2);
     read_frags(0, nxt, 0);
-    mfmas(1, kHead, FM);
+    mfmas(1, 0, FM);
+#pragma unroll
+    for (int i = 0; i < FN * FM; ++i) {
+      __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);  // one MFMA
+      __builtin_amdgcn_sched_group_barrier(0x020, 1, 0);  // one direct load
+      __builtin_amdgcn_sched_group_barrier(0x100, 1, 0);  // one LDS read
+    }
+    __builtin_amdgcn_sched_barrier(0);
     next_codes();
   };
   for (int p = 0; p < npairs; p += 2) {
