@@ -182,6 +182,27 @@ def _hbm_entry(ms: float, nbytes: int, **extra) -> dict:
             "frac": round(gbs / HBM_PEAK_GBS, 4)}
 
 
+_COPY_FLOOR: dict = {}
+
+
+def _with_copy_floor(entry: dict, device) -> dict:
+    """Adds the rate of a plain device-to-device copy moving the same bytes (half read,
+    half written; torch's copy kernel, graph-timed, rotating over enough buffer pairs
+    that their sources span 1 GiB, past the 256 MB last-level cache): what a kernel of
+    this size can reach on this GPU, beside the 8 TB/s peak."""
+    nbytes = entry["bytes"]
+    if nbytes not in _COPY_FLOOR:
+        half = nbytes // 2
+        copies = max(4, -(-(1 << 30) // half))
+        src = [torch.empty(half, dtype=torch.uint8, device=device) for _ in range(copies)]
+        dst = [torch.empty(half, dtype=torch.uint8, device=device) for _ in range(copies)]
+        ms = _time_graph([lambda a=a, b=b: b.copy_(a) for a, b in zip(src, dst)], POINT_REPS)
+        _COPY_FLOOR[nbytes] = 2 * half / (ms * 1e-3) / 1e9
+        del src, dst
+    floor = _COPY_FLOOR[nbytes]
+    return {**entry, "copy_GB/s": round(floor, 1), "frac_of_copy": round(entry["GB/s"] / floor, 4)}
+
+
 # ------------------------------------------------------------------ config points
 RECIPE_CONFIG = {
     "per_tensor_dynamic": {"quant_method": "fp8", "activation_scheme": "dynamic"},
@@ -437,7 +458,7 @@ def _bench_kv_cache(device, reps=POINT_REPS, warmup=POINT_WARMUP, copies=4):
     for a 16384-token prefill chunk of Llama-3-8B (8 KV heads x 128) into a 65536-slot
     cache at shuffled slots, rotating over ``copies`` sources and caches. Algorithmic bytes:
     write 2 planes x (2 B read + 1 B written) per element + 8 B per slot; gather 1 B read
-    + 2 B written per element + 8 B per slot."""
+    + 2 B written per element + 8 B per slot. Graph-timed (kernel time, no host dispatch)."""
     from ayaka.kernel.hip import gather_cache, write_kv
 
     g = torch.Generator(device=device).manual_seed(0)
@@ -455,20 +476,20 @@ def _bench_kv_cache(device, reps=POINT_REPS, warmup=POINT_WARMUP, copies=4):
     writes = [lambda s=s: write_kv(s[0], s[1], s[2], s[3], s[4], 0.5, 0.5) for s in sets]
     gathers = [lambda s=s: gather_cache(s[2], s[4], s[5], 2.0, True) for s in sets]
     results = {
-        "write_kv_bf16_to_e4m3": _hbm_entry(_time_rotated(writes, reps, warmup), 2 * n * width * 3 + 8 * n,
+        "write_kv_bf16_to_e4m3": _hbm_entry(_time_graph(writes, reps), 2 * n * width * 3 + 8 * n,
                                             tokens=n, width=width),
-        "gather_e4m3_to_bf16": _hbm_entry(_time_rotated(gathers, reps, warmup), n * width * 3 + 8 * n,
+        "gather_e4m3_to_bf16": _hbm_entry(_time_graph(gathers, reps), n * width * 3 + 8 * n,
                                           tokens=n, width=width),
     }
     del sets, writes, gathers
     torch.cuda.empty_cache()
-    return results
+    return {k: _with_copy_floor(v, device) for k, v in results.items()}
 
 
 def _bench_quant(device, reps=POINT_REPS, warmup=POINT_WARMUP, copies=6):
     """Activation quantizers on bf16 prefill activations (M = 4096) at the config hidden
     sizes, rotating over ``copies`` inputs. Algorithmic bytes: 2 B read + 1 B written per
-    element, plus the scales written."""
+    element, plus the scales written. Graph-timed (kernel time, no host dispatch)."""
     from ayaka.kernel.hip import (per_token_group_quant_fp8, per_token_group_quant_mxfp8, per_token_quant_fp8,
                                   static_quant_fp8)
 
@@ -480,25 +501,25 @@ def _bench_quant(device, reps=POINT_REPS, warmup=POINT_WARMUP, copies=6):
 
     xs = inputs(3584, wl.outlier_activations)
     results["per_token_qwen2_k3584"] = _hbm_entry(
-        _time_rotated([lambda x=x: per_token_quant_fp8(x) for x in xs], reps, warmup), m * 3584 * 3 + m * 4, M=m, K=3584)
+        _time_graph([lambda x=x: per_token_quant_fp8(x) for x in xs], reps), m * 3584 * 3 + m * 4, M=m, K=3584)
     scale = torch.full((), 0.05, device=device)
     outs = [torch.empty(m, 3584, dtype=torch.float8_e4m3fn, device=device) for _ in xs]
     results["static_qwen2_k3584"] = _hbm_entry(
-        _time_rotated([lambda x=x, o=o: static_quant_fp8(x, scale, out=o) for x, o in zip(xs, outs)], reps, warmup),
+        _time_graph([lambda x=x, o=o: static_quant_fp8(x, scale, out=o) for x, o in zip(xs, outs)], reps),
         m * 3584 * 3, M=m, K=3584)
     del xs, outs
     xs = inputs(7168, wl.normal_activations)
     results["group128_dsv3_k7168"] = _hbm_entry(
-        _time_rotated([lambda x=x: per_token_group_quant_fp8(x, 128) for x in xs], reps, warmup),
+        _time_graph([lambda x=x: per_token_group_quant_fp8(x, 128) for x in xs], reps),
         m * 7168 * 3 + m * 56 * 4, M=m, K=7168)
     del xs
     xs = inputs(8192, wl.student_t_activations)
     results["mxfp8_llama70b_k8192"] = _hbm_entry(
-        _time_rotated([lambda x=x: per_token_group_quant_mxfp8(x, 32) for x in xs], reps, warmup),
+        _time_graph([lambda x=x: per_token_group_quant_mxfp8(x, 32) for x in xs], reps),
         m * 8192 * 3 + m * 256, M=m, K=8192)
     del xs
     torch.cuda.empty_cache()
-    return results
+    return {k: _with_copy_floor(v, device) for k, v in results.items()}
 
 
 # ------------------------------------------------------------------ CPU baselines

@@ -230,3 +230,28 @@ def test_write_every_16bit_pattern(gpu, src_dtype, cache_dtype):
     write_kv(x.to(gpu), x.to(gpu), kg, vg, slots.to(gpu), 1.0, 0.3)
     assert torch.equal(_bytes(kg.cpu()), _bytes(k_ref))
     assert torch.equal(_bytes(vg.cpu()), _bytes(v_ref))
+
+
+@pytest.mark.parametrize("cache_dtype", [torch.float8_e4m3fn, torch.float8_e5m2])
+@pytest.mark.parametrize("dest_dtype", [torch.bfloat16, torch.float16])
+@pytest.mark.parametrize("n,heads,dim", [(37, 2, 128), (5000, 8, 128)])
+def test_gather_fp8_to_16bit_rows_of_16(gpu, cache_dtype, dest_dtype, n, heads, dim):
+    """fp8 cache into a 16-bit destination with rows of whole 16-element chunks (the
+    16-byte-chunk gather), with out-of-range slots (zero rows), dequantized and plain."""
+    from ayaka.kernel.hip import gather_cache
+
+    _say(f"gather_cache wide n={n} width={heads * dim} {cache_dtype} -> {dest_dtype}")
+    pages, page_size = 64, 16
+    g = torch.Generator().manual_seed(21)
+    cache = (torch.randn(pages, page_size, heads, dim, generator=g) * 30).to(cache_dtype)
+    slots = torch.randint(0, pages * page_size, (n,), generator=g)
+    slots[3] = -1
+    slots[n // 2] = pages * page_size + 5
+    cg, sg = cache.to(gpu), slots.to(gpu)
+    for deq, scale in ((True, 0.75), (False, 1.0)):
+        dest = torch.full((n, heads, dim), 7.0, dtype=dest_dtype, device=gpu)
+        gather_cache(cg, sg, dest, scale, deq)
+        valid = (slots >= 0) & (slots < pages * page_size)
+        ref = ora.kv_gather(cache, torch.where(valid, slots, 0), dest_dtype, scale, deq).reshape(n, heads, dim)
+        ref[~valid] = 0  # the kernel's contract for slots outside the cache: a zero row
+        assert _same(dest, ref), f"dequantize={deq}"
