@@ -271,11 +271,12 @@ __global__ __launch_bounds__(kQuantThreads) void group_quant_vec_kernel(
     live[u] = gi < rows * gpr;
     row[u] = live[u] ? gi / gpr : 0;
     g[u] = live[u] ? gi % gpr : 0;
+    // Loaded unconditionally (a slot past the end re-reads group 0 of row 0 and is
+    // never stored): a load inside a branch makes the compiler wait for it before the
+    // next slot's, which serializes the slots' latencies.
     const uint4* xg = reinterpret_cast<const uint4*>(x + row[u] * ldx + g[u] * group);
 #pragma unroll
-    for (int j = 0; j < VPL; ++j) {
-      if (live[u]) cache[u][j] = xg[lig + j * GL];
-    }
+    for (int j = 0; j < VPL; ++j) cache[u][j] = xg[lig + j * GL];
   }
   float f[V];
 #pragma unroll
