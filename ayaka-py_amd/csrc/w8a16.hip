@@ -12,6 +12,8 @@
 // LDS with double buffering, 64 K elements per step.
 #include "ayk_common.h"
 
+#include <utility>
+
 namespace ayk {
 namespace {
 
@@ -914,6 +916,377 @@ int launch_rows(const RsPlan& p, RsArgs a, size_t ws_bytes, hipStream_t st) {
   return AYK_OK;
 }
 
+// ------------------------------------------------------------ stream decode kernel
+// Decode batches (2 <= M <= 32). Every wavefront streams its own RW = 16 TW weight rows
+// over the whole K range through a private LDS ring of D stages (16 TW rows x 256 K
+// bytes, filled by direct loads of 4 rows x 256 contiguous bytes each), with no
+// workgroup barrier per stage: a stage is complete for a wavefront once its own loads
+// have retired. The activations are shared: the workgroup stages them into LDS in
+// chunks of G stages (MP rows x 256 G elements, double-buffered), each wavefront
+// loading a quarter of every chunk together with the first stage of that chunk; one
+// workgroup barrier at every chunk boundary makes a chunk visible (and, G >= D - 1,
+// proves the buffer it refills has been read by everyone). Activation bytes thus pass
+// the vector-memory path once per workgroup, not once per wavefront.
+//
+// MFMA v_mfma_f32_16x16x32_{bf16,f16}, weight as operand A, in the row-stream kernel's
+// K order (lane (r, g): 16 weight bytes of row r at K [16 g, 16 g + 16) of a 64-K
+// window, two 8-element operands; the same K of activation row r (+ 16) as operand B).
+// Logical 16-byte chunk c of an LDS row (weights or activations) sits at physical chunk
+// c ^ (row % 16), so the 16 rows of a fragment read fall on distinct banks.
+constexpr int kStWaves = 4;
+constexpr int kStK = 256;  // K per stage
+
+// Calls f(std::integral_constant<int, i>{}) for i = 0 .. N - 1 (an unrolled loop whose
+// index is a compile-time constant in the body).
+template <typename F, int... I>
+__device__ inline void static_for_impl(F&& f, std::integer_sequence<int, I...>) {
+  (f(std::integral_constant<int, I>{}), ...);
+}
+template <int N, typename F>
+__device__ inline void static_for(F&& f) {
+  static_for_impl(f, std::make_integer_sequence<int, N>{});
+}
+
+template <int NB>
+__device__ inline void window_reads(v4u (&b)[NB], const uint32_t (&ab)[NB]);
+#define AYK_WR128(o, i) "ds_read_b128 %" #o ", %" #i "\n\t"
+template <>
+__device__ inline void window_reads<3>(v4u (&b)[3], const uint32_t (&ab)[3]) {
+  asm volatile(AYK_WR128(0, 3) AYK_WR128(1, 4) AYK_WR128(2, 5) "s_waitcnt lgkmcnt(0)"
+               : "=&v"(b[0]), "=&v"(b[1]), "=&v"(b[2])
+               : "v"(ab[0]), "v"(ab[1]), "v"(ab[2])
+               : "memory");
+}
+template <>
+__device__ inline void window_reads<4>(v4u (&b)[4], const uint32_t (&ab)[4]) {
+  asm volatile(AYK_WR128(0, 4) AYK_WR128(1, 5) AYK_WR128(2, 6) AYK_WR128(3, 7) "s_waitcnt lgkmcnt(0)"
+               : "=&v"(b[0]), "=&v"(b[1]), "=&v"(b[2]), "=&v"(b[3])
+               : "v"(ab[0]), "v"(ab[1]), "v"(ab[2]), "v"(ab[3])
+               : "memory");
+}
+template <>
+__device__ inline void window_reads<5>(v4u (&b)[5], const uint32_t (&ab)[5]) {
+  asm volatile(AYK_WR128(0, 5) AYK_WR128(1, 6) AYK_WR128(2, 7) AYK_WR128(3, 8) AYK_WR128(4, 9) "s_waitcnt lgkmcnt(0)"
+               : "=&v"(b[0]), "=&v"(b[1]), "=&v"(b[2]), "=&v"(b[3]), "=&v"(b[4])
+               : "v"(ab[0]), "v"(ab[1]), "v"(ab[2]), "v"(ab[3]), "v"(ab[4])
+               : "memory");
+}
+template <>
+__device__ inline void window_reads<6>(v4u (&b)[6], const uint32_t (&ab)[6]) {
+  asm volatile(AYK_WR128(0, 6) AYK_WR128(1, 7) AYK_WR128(2, 8) AYK_WR128(3, 9) AYK_WR128(4, 10) AYK_WR128(5, 11) "s_waitcnt lgkmcnt(0)"
+               : "=&v"(b[0]), "=&v"(b[1]), "=&v"(b[2]), "=&v"(b[3]), "=&v"(b[4]), "=&v"(b[5])
+               : "v"(ab[0]), "v"(ab[1]), "v"(ab[2]), "v"(ab[3]), "v"(ab[4]), "v"(ab[5])
+               : "memory");
+}
+#undef AYK_WR128
+
+// One 16-byte direct-to-LDS load per lane with the nontemporal hint: weights are read
+// once, so they stream past the caches (measured 3-7% faster than the default policy).
+__device__ inline void dma16_nt(const uint8_t* src, uint8_t* lds_dst) {
+  __builtin_amdgcn_global_load_lds(src, (__attribute__((address_space(3))) void*)lds_dst, 16, 0, 2);
+}
+
+template <bool BF16, bool ROW_SCALE, int MP, int TW, int G, int D>
+__global__ __launch_bounds__(kStWaves * kWave) void w8a16_stream_kernel(RsArgs a) {
+  constexpr int MT = MP > 16 ? 2 : 1;        // 16-column MFMA tiles
+  constexpr int RW = 16 * TW;                // rows per wavefront
+  constexpr int R = kStWaves * RW;           // rows per workgroup
+  constexpr int kWStage = RW * kStK;         // weight bytes of one wavefront stage
+  constexpr int kWIns = kWStage / 1024;      // direct loads per wavefront stage
+  constexpr int kXRow = 2 * G * kStK;        // bytes of one activation row of a chunk
+  constexpr int kXChunk = MP * kXRow;
+  constexpr int kXIns = kXChunk / (1024 * kStWaves);  // activation loads per wavefront and chunk
+  constexpr int kSOps = ROW_SCALE ? 0 : 4 * TW;       // block-scale words per stage
+  constexpr int kOpsW = kWIns + kSOps;
+  constexpr int U = G % D == 0 ? G : (D % G == 0 ? D : G * D);  // a multiple of G and D
+  static_assert(kXChunk % (1024 * kStWaves) == 0, "whole activation loads per wavefront");
+  static_assert(D >= 2 && D - 1 <= G, "an activation buffer is refilled only after a barrier past its last read");
+  static_assert(R <= kWStage, "the row-scale words fit one stage slot");
+  // Loads issued after stage s and before its wait (stages s + 1 .. s + D - 2).
+  constexpr auto wait_after = [](int u) {
+    int n = 0;
+    for (int t = u + 1; t <= u + D - 2; ++t) n += kOpsW + (t % G == 0 ? kXIns : 0);
+    return n;
+  };
+  static_assert(wait_after(0) <= 63 && wait_after(G - 1) <= 63, "vmcnt range");
+
+  __shared__ __attribute__((aligned(1024))) uint8_t wring[kStWaves * D * kWStage];
+  __shared__ __attribute__((aligned(1024))) uint8_t xbuf[2 * kXChunk];
+  const int lane = threadIdx.x & (kWave - 1);
+  const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x / kWave);
+  const int r16 = lane & 15, g = lane >> 4;
+  uint8_t* myring = wring + wave * D * kWStage;
+  const int64_t n_wave = (int64_t)blockIdx.x * R + wave * RW;
+  const int64_t kbeg = (int64_t)blockIdx.y * a.k_per_split;
+  const int64_t klen = a.K - kbeg < a.k_per_split ? a.K - kbeg : a.k_per_split;
+  const int ns = (int)(klen / kStK);  // a multiple of G (host plan)
+
+  // Weight loads: load j of a stage covers rows 4 j .. 4 j + 3 of the wavefront, lane l
+  // row 4 j + l / 16 at physical chunk l % 16; rows past N re-read row N - 1.
+  const uint8_t* wsrc[kWIns];
+#pragma unroll
+  for (int j = 0; j < kWIns; ++j) {
+    const int row = 4 * j + (lane >> 4);
+    const int64_t n = n_wave + row < a.N ? n_wave + row : a.N - 1;
+    wsrc[j] = a.w + n * a.ldw + kbeg + 16 * ((lane & 15) ^ (row & 15));
+  }
+  // Activation loads: load j of wavefront w fills chunk bytes 1024 (w kXIns + j) ..:
+  // row m, physical chunk p of that row; rows past M repeat row M - 1.
+  const uint16_t* xsrc[kXIns];
+  uint32_t xdst[kXIns];
+#pragma unroll
+  for (int j = 0; j < kXIns; ++j) {
+    const int byte = 1024 * (wave * kXIns + j) + 16 * lane;
+    const int m = byte / kXRow;
+    const int p = (byte % kXRow) / 16;
+    const int64_t mm = m < a.M ? m : a.M - 1;
+    xsrc[j] = a.x + mm * a.ldx + kbeg + 8 * (p ^ (m & 15));
+    xdst[j] = __builtin_amdgcn_readfirstlane(1024 * (wave * kXIns + j));
+  }
+  // Fragment read offsets: weights (row 16 tt + r, window chunk 4 win + g) within a stage
+  // slot; activations (row m = 16 mt + r, clamped to the staged rows) within a chunk.
+  uint32_t woff[TW][4], xoff[MT][4][2];
+#pragma unroll
+  for (int tt = 0; tt < TW; ++tt)
+#pragma unroll
+    for (int win = 0; win < 4; ++win) {
+      const int row = 16 * tt + r16;
+      woff[tt][win] = row * kStK + 16 * ((4 * win + g) ^ (row & 15));
+    }
+  int64_t rowbase[TW];
+#pragma unroll
+  for (int tt = 0; tt < TW; ++tt) {
+    const int64_t n = n_wave + 16 * tt + r16 < a.N ? n_wave + 16 * tt + r16 : a.N - 1;
+    rowbase[tt] = (int64_t)((uint64_t)n / (uint64_t)a.by) * a.srs;
+  }
+
+  // Per-row scales: wavefront 0 copies the workgroup's raw scale words into its last
+  // ring slot (free until the first stage's refill) ahead of everything else.
+  uint32_t* srow_lds = reinterpret_cast<uint32_t*>(wring + (D - 1) * kWStage);
+  constexpr int kSrowIns = ROW_SCALE ? (R + kWave - 1) / kWave : 0;
+  const int ssize = a.scale_dtype == AYK_F32 ? 4 : (a.scale_dtype == AYK_U8 ? 1 : 2);
+  if constexpr (ROW_SCALE) {
+    if (wave == 0) {
+#pragma unroll
+      for (int i = 0; i < kSrowIns; ++i) {
+        const int row = kWave * i + lane < R ? kWave * i + lane : R - 1;
+        const int64_t n = (int64_t)blockIdx.x * R + row < a.N ? (int64_t)blockIdx.x * R + row : a.N - 1;
+        const uintptr_t p = reinterpret_cast<uintptr_t>(a.scale) + (uintptr_t)(((int64_t)((uint64_t)n / (uint64_t)a.by) * a.srs) * ssize);
+        dma4(reinterpret_cast<const uint8_t*>(p & ~(uintptr_t)3), reinterpret_cast<uint8_t*>(srow_lds) + 4 * kWave * i);
+      }
+    }
+  }
+
+  RawBits sr[D][ROW_SCALE ? 1 : TW][ROW_SCALE ? 1 : 4];
+  // Stage t (clamped to the last stage; a clamped stage only rewrites data no later
+  // stage reads, or the same data) into slot t % D; the chunk's activations with the
+  // chunk's first stage (XL: t % G == 0, known at compile time at every call site).
+  auto issue = [&](int slot, int t, bool xl) {
+    const int tc = t < ns ? t : ns - 1;
+    const int64_t k = (int64_t)tc * kStK;
+#pragma unroll
+    for (int j = 0; j < kWIns; ++j) dma16_nt(wsrc[j] + k, myring + slot * kWStage + 1024 * j);
+    if constexpr (!ROW_SCALE) {
+#pragma unroll
+      for (int win = 0; win < 4; ++win) {
+        const int64_t kidx = (uint32_t)(kbeg + k + 64 * win + 16 * g) / (uint32_t)a.bx;
+#pragma unroll
+        for (int tt = 0; tt < TW; ++tt) sr[slot][tt][win] = load_bits(a.scale, a.scale_dtype, rowbase[tt] + kidx);
+      }
+    }
+    if (xl) {
+      const int c = tc / G;
+      uint8_t* xb = xbuf + (c & 1) * kXChunk;
+#pragma unroll
+      for (int j = 0; j < kXIns; ++j) dma16(reinterpret_cast<const uint8_t*>(xsrc[j] + (int64_t)c * G * kStK), xb + xdst[j]);
+    }
+  };
+
+  v4f acc[TW][MT];
+#pragma unroll
+  for (int tt = 0; tt < TW; ++tt)
+#pragma unroll
+    for (int mt = 0; mt < MT; ++mt) acc[tt][mt] = v4f{0.0f, 0.0f, 0.0f, 0.0f};
+  float srowf[TW];
+  // Stage s from slot `slot`; its activations at window base `wb` (K within the chunk)
+  // of chunk buffer `xb`.
+  auto compute = [&](int slot, int s, int wb) {
+    const uint32_t wbase = lds_addr(myring + slot * kWStage);
+    const uint32_t xbase = lds_addr(xbuf + ((s / G) & 1) * kXChunk);
+#pragma unroll
+    for (int win = 0; win < 4; ++win) {
+      constexpr int NB = TW + 2 * MT;
+      uint32_t ab[NB];
+      v4u v[NB];
+#pragma unroll
+      for (int tt = 0; tt < TW; ++tt) ab[tt] = wbase + woff[tt][win];
+#pragma unroll
+      for (int mt = 0; mt < MT; ++mt) {
+        const int m = 16 * mt + r16 < MP ? 16 * mt + r16 : MP - 1;
+#pragma unroll
+        for (int h = 0; h < 2; ++h) {
+          const int lc = wb / 8 + 8 * win + 2 * g + h;
+          ab[TW + 2 * mt + h] = xbase + m * kXRow + 16 * (lc ^ (m & 15));
+        }
+      }
+      window_reads<NB>(v, ab);
+#pragma unroll
+      for (int tt = 0; tt < TW; ++tt) {
+        float sc;
+        if constexpr (ROW_SCALE) sc = srowf[tt];
+        else sc = bits_to_f32(sr[slot][tt][win], a.scale_dtype);
+        const v8s lo = convert8<BF16>(v[tt][0], v[tt][1], sc);
+        const v8s hi = convert8<BF16>(v[tt][2], v[tt][3], sc);
+#pragma unroll
+        for (int mt = 0; mt < MT; ++mt) {
+          acc[tt][mt] = mfma16x16<BF16>(lo, __builtin_bit_cast(v8s, v[TW + 2 * mt]), acc[tt][mt]);
+          acc[tt][mt] = mfma16x16<BF16>(hi, __builtin_bit_cast(v8s, v[TW + 2 * mt + 1]), acc[tt][mt]);
+        }
+      }
+    }
+  };
+
+#pragma unroll
+  for (int d = 0; d < D - 1; ++d) issue(d, d, d % G == 0);
+  if constexpr (ROW_SCALE) {
+    // Everything older than the ring: wavefront 0's row-scale copy.
+    if (wave == 0) {
+      constexpr int kRing = [] {
+        int n = 0;
+        for (int t = 0; t < D - 1; ++t) n += kOpsW + (t % G == 0 ? kXIns : 0);
+        return n;
+      }();
+      wait_vmcnt<(kRing < 63 ? kRing : 63)>();
+    }
+    __builtin_amdgcn_s_barrier();
+#pragma unroll
+    for (int tt = 0; tt < TW; ++tt) {
+      const int row = wave * RW + 16 * tt + r16;
+      uint32_t word;
+      asm volatile("ds_read_b32 %0, %1\n\ts_waitcnt lgkmcnt(0)" : "=v"(word) : "v"(lds_addr(reinterpret_cast<const uint8_t*>(srow_lds)) + 4 * row) : "memory");
+      const uint32_t shift = (uint32_t)((reinterpret_cast<uintptr_t>(a.scale) + (uintptr_t)(rowbase[tt] * ssize)) & 3) * 8;
+      srowf[tt] = bits_to_f32(RawBits{word, shift}, a.scale_dtype);
+    }
+  }
+  // Step s: wait for stage s (its activation chunk too), at a chunk start a barrier,
+  // refill slot (s - 1) % D with stage s + D - 1, compute stage s. The main loop runs
+  // whole rounds of U steps with no exit inside; the remainder runs after it.
+  auto step = [&](auto uc, int s) {
+    constexpr int u = decltype(uc)::value;
+    wait_vmcnt<wait_after(u % G)>();
+    if (u % G == 0) __builtin_amdgcn_s_barrier();
+    issue((u + D - 1) % D, s + D - 1, (u + D - 1) % G == 0);
+    compute(u % D, s, (u % G) * kStK);
+  };
+  int s0 = 0;
+  for (; s0 + U <= ns; s0 += U) {
+    static_for<U>([&](auto uc) { step(uc, s0 + decltype(uc)::value); });
+  }
+  static_for<U - 1>([&](auto uc) {
+    if (s0 + decltype(uc)::value < ns) step(uc, s0 + decltype(uc)::value);  // workgroup-uniform
+  });
+  wait_vmcnt<0>();  // no direct load may still be writing LDS when the workgroup ends
+
+  // D[n][m]: lane holds m = lane % 16 (+ 16 mt) and n = 4 (lane / 16) + r of its tile.
+#pragma unroll
+  for (int tt = 0; tt < TW; ++tt)
+#pragma unroll
+    for (int mt = 0; mt < MT; ++mt) {
+      const int64_t m = 16 * mt + r16;
+      if (m >= a.M) continue;
+#pragma unroll
+      for (int r = 0; r < 4; ++r) {
+        const int64_t n = n_wave + 16 * tt + 4 * g + r;
+        if (n >= a.N) continue;
+        if (gridDim.y == 1) a.out[m * a.ldo + n] = round16<BF16>(acc[tt][mt][r]);
+        else a.part[((int64_t)blockIdx.y * a.M + m) * a.N + n] = acc[tt][mt][r];
+      }
+    }
+}
+
+// Launch plan from the shapes alone (the workspace query reproduces it). The kernel
+// serves wide projections (N >= kStMinRows: >= 384 wavefront tiles of 64 rows);
+// narrower ones keep the row-stream kernel, which measured as fast or faster there.
+constexpr int64_t kStMinRows = 24576;
+struct StPlan {
+  bool ok;
+  int mp, tw, g, d, split;
+  int64_t kps;
+};
+StPlan stream_plan(int64_t M, int64_t N, int64_t K, int64_t bx) {
+  StPlan p{};
+  const bool row_scale = bx >= K;
+  if (M < 2 || M > 32 || N < kStMinRows || K % kStK || K >= (int64_t(1) << 31) || (!row_scale && bx % 16)) return p;
+  p.mp = M <= 4 ? 4 : (M <= 8 ? 8 : (M <= 16 ? 16 : 32));
+  // Up to 8 activation rows: one 16-row tile per wavefront, 32 KB of activation
+  // buffers, two workgroups per CU. Above: two tiles per wavefront (the activation
+  // bytes a workgroup reads are half its weight bytes at M = 32), 64 KB of activation
+  // buffers, one workgroup per CU.
+  p.tw = p.mp <= 8 ? 1 : 2;
+  p.g = (p.tw == 1 ? 32 : 64) / p.mp;
+  if (p.g > 8) p.g = 8;
+  while (p.g > 2 && K % (kStK * p.g)) p.g /= 2;
+  if (K % (kStK * p.g)) return StPlan{};
+  p.d = 3;
+  p.split = 1;
+  p.kps = K;
+  p.ok = cdiv(N, 16 * kStWaves * p.tw) <= 0x7FFFFFFF;
+  return p;
+}
+size_t stream_workspace(const StPlan& p, int64_t M, int64_t N) {
+  return p.ok && p.split > 1 ? (size_t)p.split * (size_t)M * (size_t)N * sizeof(float) : 0;
+}
+
+template <bool BF16, bool ROW_SCALE, int MP, int TW>
+bool launch_stream_g(const StPlan& p, const RsArgs& a, hipStream_t st) {
+  const dim3 grid((unsigned)cdiv(a.N, 16 * kStWaves * TW), (unsigned)p.split), block(kStWaves * kWave);
+#define AYK_ST(G, D)                                                                                  \
+  if (p.g == G && p.d == D) {                                                                         \
+    hipLaunchKernelGGL((w8a16_stream_kernel<BF16, ROW_SCALE, MP, TW, G, D>), grid, block, 0, st, a); \
+    return true;                                                                                      \
+  }
+  // LDS: 4 D TW 4 KB of weight rings + 2 MP 512 G bytes of activation chunks
+  if constexpr (64 / MP >= 8) { AYK_ST(8, 3) }
+  if constexpr (64 / MP >= 4) { AYK_ST(4, 3) }
+  AYK_ST(2, 3)
+#undef AYK_ST
+  return false;
+}
+
+template <bool BF16, bool ROW_SCALE>
+bool launch_stream_kernel(const StPlan& p, const RsArgs& a, hipStream_t st) {
+  switch (p.mp * 10 + p.tw) {
+    case 41: return launch_stream_g<BF16, ROW_SCALE, 4, 1>(p, a, st);
+    case 42: return launch_stream_g<BF16, ROW_SCALE, 4, 2>(p, a, st);
+    case 81: return launch_stream_g<BF16, ROW_SCALE, 8, 1>(p, a, st);
+    case 82: return launch_stream_g<BF16, ROW_SCALE, 8, 2>(p, a, st);
+    case 161: return launch_stream_g<BF16, ROW_SCALE, 16, 1>(p, a, st);
+    case 162: return launch_stream_g<BF16, ROW_SCALE, 16, 2>(p, a, st);
+    case 321: return launch_stream_g<BF16, ROW_SCALE, 32, 1>(p, a, st);
+    case 322: return launch_stream_g<BF16, ROW_SCALE, 32, 2>(p, a, st);
+    default: return false;
+  }
+}
+
+template <bool BF16>
+int launch_stream(const StPlan& p, RsArgs a, size_t ws_bytes, hipStream_t st) {
+  a.k_per_split = p.kps;
+  if (p.split > 1) {
+    const size_t need = stream_workspace(p, a.M, a.N);
+    if (a.part == nullptr || ws_bytes < need) {
+      return fail(AYK_EWORKSPACE, "fp8_weight_only_gemm: workspace of %zu bytes required, %zu given", need, ws_bytes);
+    }
+  }
+  const bool launched = a.bx >= a.K ? launch_stream_kernel<BF16, true>(p, a, st) : launch_stream_kernel<BF16, false>(p, a, st);
+  if (!launched) return fail(AYK_EINVAL, "fp8_weight_only_gemm: no stream kernel for this plan");
+  if (int rc = check_launch("fp8_weight_only_gemm")) return rc;
+  if (p.split > 1) {
+    hipLaunchKernelGGL((w8a16_rows_reduce<BF16>), dim3((unsigned)cdiv(a.M * a.N, 256)), dim3(256), 0, st, a, p.split);
+    return check_launch("fp8_weight_only_gemm");
+  }
+  return AYK_OK;
+}
+
 template <bool BF16, int BN, int BM, int WN, int WM>
 int launch_w16(W16Args g, hipStream_t st) {
   g.tiles_m = (int)cdiv(g.M, BM);
@@ -939,10 +1312,11 @@ extern "C" {
 
 size_t ayk_fp8_weight_only_gemm_workspace_bytes(int64_t M, int64_t N, int64_t K, int64_t block_size_x) {
   if (M < 2) return 0;
-  // An upper bound over the two decode kernels (alignment decides which one runs).
+  // An upper bound over the decode kernels (alignment decides which one runs).
+  const size_t st = stream_workspace(stream_plan(M, N, K, block_size_x), M, N);
   const size_t rs = rows_workspace(rows_plan(M, N, K, block_size_x), M, N);
   const size_t sk = skinny_workspace(skinny_plan(M, N, K, block_size_x), M, N);
-  return rs > sk ? rs : sk;
+  return st > rs ? (st > sk ? st : sk) : (rs > sk ? rs : sk);
 }
 
 int ayk_fp8_weight_only_gemm(const void* x, int x_dtype, int64_t ldx, int64_t M, const void* w,
@@ -978,9 +1352,21 @@ int ayk_fp8_weight_only_gemm(const void* x, int x_dtype, int64_t ldx, int64_t M,
   g.out = static_cast<uint16_t*>(out);
   g.ldo = ldo;
   hipStream_t st = static_cast<hipStream_t>(stream);
-  // Decode batch sizes: the row-stream kernel (whole 256-K stages, scale blocks of
-  // whole 16 K), else the skinny streaming kernel (whole 128-K steps, scale blocks of
-  // >= 32 K); both need 16-byte aligned activation rows.
+  // Decode batch sizes (all three need 16-byte aligned activation rows): wide
+  // projections take the stream kernel (K a multiple of 512, scale blocks of whole
+  // 16 K), the others the row-stream kernel (whole 256-K stages, scale blocks of whole
+  // 16 K), else the skinny streaming kernel (whole 128-K steps, scale blocks of >= 32 K).
+  if (M >= 2 && ldx % 8 == 0) {
+    const StPlan sp = stream_plan(M, N, K, block_size_x);
+    if (sp.ok) {
+      RsArgs a{};
+      a.x = g.x; a.ldx = ldx; a.M = M; a.w = g.w; a.ldw = ldw; a.N = N; a.K = K;
+      a.scale = scale; a.scale_dtype = scale_dtype; a.srs = scale_row_stride; a.by = block_size_y; a.bx = block_size_x;
+      a.out = g.out; a.ldo = ldo; a.part = static_cast<float*>(workspace);
+      return x_dtype == AYK_BF16 ? launch_stream<true>(sp, a, workspace_bytes, st)
+                                 : launch_stream<false>(sp, a, workspace_bytes, st);
+    }
+  }
   if (M >= 2 && ldx % 8 == 0) {
     const RsPlan rp = rows_plan(M, N, K, block_size_x);
     if (rp.ok) {

@@ -476,6 +476,30 @@ def test_weight_only_gemm_decode_plans(gpu, m, n, k, case, xdt):
     assert_linear_close(y, ref, "weight_only_gemm decode plan")
 
 
+# Wide decode projections (N >= 24576) take the stream kernel: every staged activation
+# row count (4, 8, 16, 32), ragged N (not a multiple of 64, nor of 16), every scale
+# layout, fp16, K whose stage count leaves a remainder after the unrolled loop (3584:
+# 14 stages in rounds of 6) or runs the remainder only (512: 2 stages).
+@pytest.mark.parametrize("m,n,k,case,xdt", [
+    (4, 24576, 4096, "channel", torch.bfloat16),
+    (5, 24640, 1536, "e8m0_32", torch.bfloat16),
+    (13, 24600, 2048, "block128", torch.float16),
+    (32, 24576, 3584, "channel_e8m0", torch.bfloat16),
+    (2, 28672, 512, "channel", torch.float16),
+    (17, 24704, 2560, "block128", torch.bfloat16),
+])
+def test_weight_only_gemm_stream(gpu, m, n, k, case, xdt):
+    from ayaka.kernel.hip import fp8_weight_only_gemm
+
+    _say(f"fp8_weight_only_gemm stream m={m} n={n} k={k} case={case} x={xdt}")
+    w, scale, by, bx, sdt = _weight_only_operands(n, k, case)
+    x = torch.randn(m, k, generator=_gen(2)).to(xdt)
+    y = fp8_weight_only_gemm(x.to(gpu), w.to(gpu), scale.to(gpu), -(-k // bx), by, bx, sdt)
+    ref = ora.fp8_weight_only_gemm(x, w, scale, -(-k // bx), by, bx, sdt)
+    assert y.dtype == xdt and y.shape == (m, n)
+    assert_linear_close(y, ref, "weight_only_gemm stream")
+
+
 # ------------------------------------------------------------------ linear entry points
 @pytest.mark.parametrize("m", [1, 8, 40])
 @pytest.mark.parametrize("recipe", ["w8a8_rowwise", "w8a8_dynamic_per_tensor", "w8a8_block128"])
