@@ -79,6 +79,111 @@ __device__ inline void store_quant(uint8_t* dst, const float* f, const Divisor& 
   }
 }
 
+// ------------------------------------------------------------ finite fast path
+// The magnitude bits of a non-negative float (or NaN) order like the values as
+// unsigned integers, NaN above infinity: the amax of a row or group is an integer max
+// over |x|'s bits, and it is NaN exactly when the row or group holds a NaN. Rows and
+// groups whose amax is finite (the rule; infinity and NaN are the exception) take a
+// path with no per-element special cases; the others keep the exact element-wise one.
+typedef unsigned short u16x2 __attribute__((ext_vector_type(2)));
+
+// Running max of |x| bits over one 16-byte vector (16-bit floats: two lanes of packed
+// 16-bit magnitudes; fp32: one 32-bit magnitude).
+template <typename T>
+__device__ inline uint32_t absbits_max(const uint4& v, uint32_t acc);
+template <>
+__device__ inline uint32_t absbits_max<BF16T>(const uint4& v, uint32_t acc) {
+  u16x2 m = __builtin_bit_cast(u16x2, acc);
+  const uint32_t w[4] = {v.x, v.y, v.z, v.w};
+#pragma unroll
+  for (int i = 0; i < 4; ++i) m = __builtin_elementwise_max(m, __builtin_bit_cast(u16x2, w[i] & 0x7FFF7FFFu));
+  return __builtin_bit_cast(uint32_t, m);
+}
+template <>
+__device__ inline uint32_t absbits_max<F16T>(const uint4& v, uint32_t acc) {
+  return absbits_max<BF16T>(v, acc);  // the same packed 16-bit magnitudes
+}
+template <>
+__device__ inline uint32_t absbits_max<F32T>(const uint4& v, uint32_t acc) {
+  const uint32_t w[4] = {v.x, v.y, v.z, v.w};
+#pragma unroll
+  for (int i = 0; i < 4; ++i) acc = max(acc, w[i] & 0x7FFFFFFFu);
+  return acc;
+}
+// The accumulated magnitude bits as the fp32 bit pattern of the amax (whose integer
+// order is the value order, NaN above infinity).
+template <typename T>
+__device__ inline uint32_t absbits_f32(uint32_t acc);
+template <>
+__device__ inline uint32_t absbits_f32<BF16T>(uint32_t acc) {
+  const uint32_t lo = acc & 0xFFFFu, hi = acc >> 16;
+  return (lo > hi ? lo : hi) << 16;
+}
+template <>
+__device__ inline uint32_t absbits_f32<F16T>(uint32_t acc) {
+  const uint32_t lo = acc & 0xFFFFu, hi = acc >> 16;
+  return f2u(f16_bits_to_f32((uint16_t)(lo > hi ? lo : hi)));
+}
+template <>
+__device__ inline uint32_t absbits_f32<F32T>(uint32_t acc) {
+  return acc;
+}
+template <int WIDTH>
+__device__ inline uint32_t wave_max_u32(uint32_t v) {
+#pragma unroll
+  for (int off = WIDTH / 2; off > 0; off >>= 1) v = max(v, (uint32_t)__shfl_xor((int)v, off, WIDTH));
+  return v;
+}
+constexpr uint32_t kInfBits = 0x7F800000u;
+
+// Quantize N floats of a row or group with a finite amax by scale s (r = RN(1 / s),
+// s and r normal): |x| / s by Markstein's correction (see Divisor), which here needs no
+// special case -- |x| <= amax keeps every quotient finite, and the sign, applied
+// afterwards, keeps a zero's -- clamped to 448 and encoded without the NaN patch.
+template <int N>
+__device__ inline void store_quant_finite(uint8_t* dst, const float* f, float s, float r) {
+  static_assert(N % 4 == 0, "16-byte vectors hold 4 or 8 elements");
+  float q[N];
+#pragma unroll
+  for (int i = 0; i < N; ++i) {
+    const float ax = fabsf(f[i]);
+    const float q0 = ax * r;
+    const float qa = fminf(fmaf(fmaf(-s, q0, ax), r, q0), kE4M3Max);
+    q[i] = __builtin_copysignf(qa, f[i]);
+  }
+  uint32_t w[N / 4];
+#pragma unroll
+  for (int i = 0; i < N / 4; ++i) {
+    w[i] = (uint32_t)__builtin_amdgcn_cvt_pk_fp8_f32(q[4 * i], q[4 * i + 1], 0, false);
+    w[i] = (uint32_t)__builtin_amdgcn_cvt_pk_fp8_f32(q[4 * i + 2], q[4 * i + 3], (int)w[i], true);
+  }
+  if constexpr (N == 8) {
+    *reinterpret_cast<uint2*>(dst) = make_uint2(w[0], w[1]);
+  } else {
+    *reinterpret_cast<uint32_t*>(dst) = w[0];
+  }
+}
+// MX: |x| times the power of two inv (exact but for fp32 subnormals, which round as
+// the reference's division by the same power of two), clamped to 448 (the fp32 log2
+// can round the exponent one short), sign restored; finite groups only.
+template <int N>
+__device__ inline void store_mx_finite(uint8_t* dst, const float* f, float inv) {
+  float q[N];
+#pragma unroll
+  for (int i = 0; i < N; ++i) q[i] = __builtin_copysignf(fminf(fabsf(f[i]) * inv, kE4M3Max), f[i]);
+  uint32_t w[N / 4];
+#pragma unroll
+  for (int i = 0; i < N / 4; ++i) {
+    w[i] = (uint32_t)__builtin_amdgcn_cvt_pk_fp8_f32(q[4 * i], q[4 * i + 1], 0, false);
+    w[i] = (uint32_t)__builtin_amdgcn_cvt_pk_fp8_f32(q[4 * i + 2], q[4 * i + 3], (int)w[i], true);
+  }
+  if constexpr (N == 8) {
+    *reinterpret_cast<uint2*>(dst) = make_uint2(w[0], w[1]);
+  } else {
+    *reinterpret_cast<uint32_t*>(dst) = w[0];
+  }
+}
+
 // Block-wide NaN-propagating max over 256 threads; every thread gets the result.
 __device__ inline float block_max256(float v, float* red) {
   v = wave_max<kWave>(v);
@@ -88,6 +193,18 @@ __device__ inline float block_max256(float v, float* red) {
   float r = red[0];
 #pragma unroll
   for (int i = 1; i < kQuantThreads / kWave; ++i) r = nanmax(r, red[i]);
+  return r;
+}
+
+// The same over magnitude bits (unsigned max, NaN above infinity).
+__device__ inline uint32_t block_max256_u32(uint32_t v, uint32_t* red) {
+  v = wave_max_u32<kWave>(v);
+  const int wave = threadIdx.x / kWave;
+  if ((threadIdx.x % kWave) == 0) red[wave] = v;
+  __syncthreads();
+  uint32_t r = red[0];
+#pragma unroll
+  for (int i = 1; i < kQuantThreads / kWave; ++i) r = max(r, red[i]);
   return r;
 }
 
@@ -113,18 +230,30 @@ __global__ __launch_bounds__(kQuantThreads) void per_token_quant_vec_kernel(
   float f[V];
   if constexpr (VPT > 0) {
     uint4 cache[VPT];
+    uint32_t bits = 0;
 #pragma unroll
     for (int i = 0; i < VPT; ++i) {
       const int64_t v = threadIdx.x + (int64_t)i * kQuantThreads;
       if (v < nvec) {
         cache[i] = xr[v];
-        unpack16<T>(cache[i], f);
-        amax = absmax_n<V>(f, amax);
+        bits = absbits_max<T>(cache[i], bits);
       }
     }
-    amax = floor_amax(block_max256(amax, red));
-    const float s = amax / kE4M3Max;
+    bits = block_max256_u32(absbits_f32<T>(bits), reinterpret_cast<uint32_t*>(red));
+    const float s = floor_amax(u2f(bits)) / kE4M3Max;
     if (threadIdx.x == 0) scale[row] = s;
+    if (bits < kInfBits) {  // workgroup-uniform
+      const float r = 1.0f / s;
+#pragma unroll
+      for (int i = 0; i < VPT; ++i) {
+        const int64_t v = threadIdx.x + (int64_t)i * kQuantThreads;
+        if (v < nvec) {
+          unpack16<T>(cache[i], f);
+          store_quant_finite<V>(qr + v * V, f, s, r);
+        }
+      }
+      return;
+    }
     const Divisor dv = make_divisor(s);
 #pragma unroll
     for (int i = 0; i < VPT; ++i) {
@@ -171,17 +300,27 @@ __global__ __launch_bounds__(kQuantThreads) void per_token_quant_wave_kernel(
     if (v < nvec) cache[i] = xr[v];
   }
   float f[V];
-  float amax = 0.0f;
+  uint32_t bits = 0;
 #pragma unroll
   for (int i = 0; i < VPT; ++i) {
-    if (lane + (int64_t)i * kWave < nvec) {
-      unpack16<T>(cache[i], f);
-      amax = absmax_n<V>(f, amax);
-    }
+    if (lane + (int64_t)i * kWave < nvec) bits = absbits_max<T>(cache[i], bits);
   }
-  amax = floor_amax(wave_max<kWave>(amax));
+  bits = wave_max_u32<kWave>(absbits_f32<T>(bits));
+  const float amax = floor_amax(u2f(bits));
   const float sc = amax / kE4M3Max;
   if (lane == 0) scale[row] = sc;
+  if (bits < kInfBits) {  // wavefront-uniform
+    const float r = 1.0f / sc;
+#pragma unroll
+    for (int i = 0; i < VPT; ++i) {
+      const int64_t v = lane + (int64_t)i * kWave;
+      if (v < nvec) {
+        unpack16<T>(cache[i], f);
+        store_quant_finite<V>(qr + v * V, f, sc, r);
+      }
+    }
+    return;
+  }
   const Divisor dv = make_divisor(sc);
 #pragma unroll
   for (int i = 0; i < VPT; ++i) {
@@ -218,7 +357,7 @@ __global__ __launch_bounds__(kQuantThreads) void per_token_quant_scalar_kernel(
 // only inputs where rounding decides the ceiling are r just above a power of two,
 // where log2(r) lies within half an fp32 ulp of an integer.
 struct MxScale {
-  float inv;     // 2^-e (exact, e <= 120 for every finite fp32 amax)
+  float inv;     // 2^-e (e <= 120 for every finite fp32 amax); NaN for a NaN group
   uint8_t code;  // 0 for an all-zero group, else e + 127
   bool zero;
 };
@@ -237,6 +376,14 @@ __device__ inline float mx_ceil_log2(float ratio) {
 }
 __device__ inline MxScale mx_scale(float amax) {
   MxScale r;
+  if (amax != amax) {
+    // A NaN group: the reference's NaN exponent converts to code 0 and every quotient
+    // by its NaN scale is NaN.
+    r.zero = false;
+    r.code = 0;
+    r.inv = amax;
+    return r;
+  }
   float ratio = amax / kE4M3Max;
   ratio = ratio < 1e-38f ? 1e-38f : ratio;
   float e = mx_ceil_log2(ratio);
@@ -244,7 +391,9 @@ __device__ inline MxScale mx_scale(float amax) {
   const int ei = (int)e;
   r.zero = (amax == 0.0f);
   r.code = r.zero ? (uint8_t)0 : (uint8_t)(ei + 127);
-  r.inv = u2f((uint32_t)(127 - ei) << 23);
+  // 2^-e; 2^-127 (e = 127, only for an infinite amax) is the subnormal 2^-127, so an
+  // infinite element still divides to infinity and clamps to 448 as in the reference.
+  r.inv = ei <= 126 ? u2f((uint32_t)(127 - ei) << 23) : u2f(0x00400000u);
   return r;
 }
 
@@ -281,20 +430,28 @@ __global__ __launch_bounds__(kQuantThreads) void group_quant_vec_kernel(
   float f[V];
 #pragma unroll
   for (int u = 0; u < kGroupSlots; ++u) {
-    float amax = 0.0f;
+    uint32_t bits = 0;
 #pragma unroll
-    for (int j = 0; j < VPL; ++j) {
-      if (live[u]) {
-        unpack16<T>(cache[u][j], f);
-        amax = absmax_n<V>(f, amax);
-      }
-    }
-    amax = wave_max<GL>(amax);  // every lane of the group takes part (GL divides 64)
+    for (int j = 0; j < VPL; ++j) bits = absbits_max<T>(cache[u][j], bits);
+    bits = absbits_f32<T>(bits);
+    // every lane of the group takes part (GL divides 64); a slot past the end is
+    // reduced like the others and then left
+    bits = wave_max_u32<GL>(live[u] ? bits : 0u);
     if (!live[u]) continue;
+    const float amax = u2f(bits);
+    const bool finite = bits < kInfBits;
     uint8_t* qg = q + row[u] * ldq + g[u] * group;
     if constexpr (MX) {
       const MxScale ms = mx_scale(amax);
       if (lig == 0) reinterpret_cast<uint8_t*>(scale_out)[row[u] * gpr + g[u]] = ms.code;
+      if (finite && !ms.zero) {  // an all-zero group is written as +0 codes below
+#pragma unroll
+        for (int j = 0; j < VPL; ++j) {
+          unpack16<T>(cache[u][j], f);
+          store_mx_finite<V>(qg + (int64_t)(lig + j * GL) * V, f, ms.inv);
+        }
+        continue;
+      }
 #pragma unroll
       for (int j = 0; j < VPL; ++j) {
         unpack16<T>(cache[u][j], f);
@@ -316,9 +473,16 @@ __global__ __launch_bounds__(kQuantThreads) void group_quant_vec_kernel(
     } else {
       const float sc = floor_amax(amax) / kE4M3Max;
       if (lig == 0) reinterpret_cast<float*>(scale_out)[row[u] * gpr + g[u]] = sc;
-      // IEEE division here: with one scale per 8-16 lanes the reciprocal form measured
-      // slower (37 against 28 us at DSv3 K = 7168), unlike the per-row kernels.
-      const Divisor dv{sc, 0.0f, false};
+      if (finite) {
+        const float r = 1.0f / sc;
+#pragma unroll
+        for (int j = 0; j < VPL; ++j) {
+          unpack16<T>(cache[u][j], f);
+          store_quant_finite<V>(qg + (int64_t)(lig + j * GL) * V, f, sc, r);
+        }
+        continue;
+      }
+      const Divisor dv{sc, 0.0f, false};  // IEEE division for infinite / NaN groups
 #pragma unroll
       for (int j = 0; j < VPL; ++j) {
         unpack16<T>(cache[u][j], f);

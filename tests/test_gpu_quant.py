@@ -125,6 +125,44 @@ def test_mx_quant_exponent_boundaries(gpu):
     assert _bits_equal(q, rq)
 
 
+def _nan_aware_equal(a: torch.Tensor, b: torch.Tensor) -> bool:
+    """Same NaN positions, identical bits elsewhere (a NaN's payload and sign are not
+    part of the contract)."""
+    a, b = a.cpu(), b.cpu()
+    af, bf = a.float(), b.float()
+    nan_a, nan_b = torch.isnan(af), torch.isnan(bf)
+    if not torch.equal(nan_a, nan_b):
+        return False
+    view = torch.uint8 if a.dtype in (torch.float8_e4m3fn, torch.uint8) else torch.int32
+    return torch.equal(a.view(view)[~nan_a], b.view(view)[~nan_b])
+
+
+@pytest.mark.parametrize("dtype", DTYPES)
+def test_dynamic_quant_nan_and_inf(gpu, dtype):
+    """Rows and groups holding NaN or +-inf take the exact element-wise path; their
+    neighbours the finite one. Codes, scales and MX exponents against the oracle."""
+    from ayaka.kernel.hip import per_token_group_quant_fp8, per_token_group_quant_mxfp8, per_token_quant_fp8
+
+    _say(f"dynamic quant NaN / inf dtype={dtype}")
+    k = 1024 if dtype == torch.float32 else 9216  # 16-bit rows past 1024 vectors: one workgroup per row
+    x = _activation(8, k, dtype, seed=11).float()
+    x[0, 5] = float("nan")
+    x[3, 700] = float("inf")
+    x[4, 129] = -float("inf")
+    x[4, 900] = float("nan")
+    x[5, 0] = -0.0
+    x = x.to(dtype)
+    q, s = per_token_quant_fp8(x.to(gpu))
+    rq, rs = ora.per_token_quant(x)
+    assert _nan_aware_equal(s, rs) and _nan_aware_equal(q, rq), "per-token"
+    q, s = per_token_group_quant_fp8(x.to(gpu), 128)
+    rq, rs = ora.per_token_group_quant(x, 128)
+    assert _nan_aware_equal(s, rs) and _nan_aware_equal(q, rq), "group-128"
+    q, c = per_token_group_quant_mxfp8(x.to(gpu), 32)
+    rq, rc = ora.per_token_group_quant_mxfp8(x, 32)
+    assert torch.equal(c.cpu(), rc) and _nan_aware_equal(q, rq), "mxfp8"
+
+
 @pytest.mark.parametrize("dtype", DTYPES)
 @pytest.mark.parametrize("shape", [(1,), (5, 7), (64, 1024), (3, 4, 333)])
 def test_static_quant_bit_exact(gpu, dtype, shape):
