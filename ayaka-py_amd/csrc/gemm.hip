@@ -1312,107 +1312,6 @@ size_t block_split_workspace(int64_t M, int64_t N, int64_t K) {
   return split > 1 ? (size_t)split * (size_t)M * (size_t)N * sizeof(float) : 0;
 }
 
-// ------------------------------------------------------------ MoE grouped block-128 GEMM
-// Expert e owns activation rows [off_e, off_e + M_e) of a [M_total, K] and weights
-// b[e] = [N, K] (memory [E][N][K]); scales are fp32, [M_total, K/128] per row and
-// 128-K block for the activations, [E][N/128][K/128] for the weights. Each workgroup
-// takes one 128 x 128 tile of one expert: the launch is an upper bound on the tile
-// count (no host synchronisation), workgroups past the real count exit at once.
-struct GroupedBlockArgs {
-  const uint8_t* a;
-  const uint8_t* b;
-  const float* sa;
-  const float* sb;
-  void* out;
-  int out_dtype;
-  const int32_t* problem_sizes;   // [E, 3]: M_e, N_e, K_e
-  const int32_t* expert_offsets;  // [E]: first row of expert e
-  int num_experts;
-  int64_t m_total, n, k;
-};
-
-// Expert e's problem, clamped to what the operands hold (rows past M_total, N_e > n,
-// K_e > k), so device-side metadata can never address outside the tensors.
-struct ExpertProblem {
-  int64_t off, m, n, k;
-};
-__device__ inline ExpertProblem expert_problem(const GroupedBlockArgs& ga, int e) {
-  ExpertProblem p;
-  const int64_t off = ga.expert_offsets[e];
-  p.off = off < 0 ? 0 : (off > ga.m_total ? ga.m_total : off);
-  const int64_t m = ga.problem_sizes[3 * e], n = ga.problem_sizes[3 * e + 1], k = ga.problem_sizes[3 * e + 2];
-  p.m = m < 0 ? 0 : (m > ga.m_total - p.off ? ga.m_total - p.off : m);
-  p.n = n < 0 ? 0 : (n > ga.n ? ga.n : n);
-  p.k = k < 0 ? 0 : ((k > ga.k ? ga.k : k) / 128) * 128;  // whole 128-K blocks, as the reference's K // 128
-  return p;
-}
-__device__ inline int64_t expert_tiles(const ExpertProblem& p) { return cdiv(p.m, kBlkTile) * cdiv(p.n, kBlkTile); }
-
-__global__ __launch_bounds__(kBlkThreads, 1) void fp8_grouped_block_kernel(GroupedBlockArgs ga) {
-  AYK_BLOCK_LDS;
-  // Locate this workgroup's expert: lane l sums the tiles of experts [l * per, l * per
-  // + per), a wave scan turns the sums into prefixes, the first lane whose inclusive
-  // prefix passes the tile index owns the expert, and that lane's range is walked.
-  const int lane = threadIdx.x & 63;
-  const int E = ga.num_experts, per = (E + 63) / 64;
-  // Workgroup b runs on XCD b % 8. Logical tiles 2x and 2x + 1 of each block of 16 go to
-  // workgroups 8 apart (one XCD, dispatched together): with the row tiles of an expert
-  // enumerated first, an expert's two 128-row tiles of one weight panel then share that
-  // XCD's L2 instead of each reading the panel from HBM. The grid is a multiple of 16.
-  const int64_t b = blockIdx.x;
-  const int64_t pid = (b & ~(int64_t)15) + 2 * (b & 7) + ((b >> 3) & 1);
-  int64_t mine = 0;
-  for (int i = 0; i < per; ++i) {
-    const int e = lane * per + i;
-    if (e < E) mine += expert_tiles(expert_problem(ga, e));
-  }
-  int64_t incl = mine;
-#pragma unroll
-  for (int d = 1; d < 64; d <<= 1) {
-    const int64_t v = __shfl_up(incl, d, 64);
-    if (lane >= d) incl += v;
-  }
-  const uint64_t owners = __ballot(incl > pid);
-  if (owners == 0) return;  // past the real tile count (uniform: the ballot is)
-  const int owner = __ffsll((unsigned long long)owners) - 1;
-  int64_t start = __shfl(incl - mine, owner, 64);
-  int e = owner * per;
-  ExpertProblem p = expert_problem(ga, e);
-  for (int64_t t = expert_tiles(p); pid >= start + t; t = expert_tiles(p)) {
-    start += t;
-    p = expert_problem(ga, ++e);
-  }
-  const int64_t local = pid - start;
-  const int64_t tiles_m = cdiv(p.m, kBlkTile);
-  const int tm = (int)(local % tiles_m), tn = (int)(local / tiles_m);
-  const int64_t kb_total = ga.k / 128;
-  const int eb = ga.out_dtype == AYK_F32 ? 4 : 2;
-  if (p.k == 0) {  // no whole 128-K block: the sum is empty, the tile is zeros
-    for (int idx = threadIdx.x; idx < kBlkTile * kBlkTile; idx += kBlkThreads) {
-      const int64_t gm = (int64_t)tm * kBlkTile + idx / kBlkTile, gn = (int64_t)tn * kBlkTile + idx % kBlkTile;
-      if (gm < p.m && gn < p.n) store_f32(ga.out, ga.out_dtype, (p.off + gm) * ga.n + gn, 0.0f);
-    }
-    return;
-  }
-  GemmArgs g{};
-  g.a = ga.a + p.off * ga.k;
-  g.lda = ga.k;
-  g.w = ga.b + (int64_t)e * ga.n * ga.k;
-  g.ldw = ga.k;
-  g.M = p.m;
-  g.N = p.n;
-  g.K = p.k;
-  g.sa = ga.sa + p.off * kb_total;
-  g.sa_dtype = AYK_F32;
-  g.sb = ga.sb + (int64_t)e * (ga.n / 128) * kb_total;
-  g.sb_dtype = AYK_F32;
-  g.out = static_cast<uint8_t*>(ga.out) + p.off * ga.n * eb;
-  g.out_dtype = ga.out_dtype;
-  g.ldo = ga.n;
-  g.tiles_m = (int)tiles_m;
-  block_gemm_tile(g, tm, tn, L0, L1, L2, L3);
-}
-
 // MXFP8 large-tile kernel with 128-K stages: two 64 KB LDS stages, one code dword (four
 // UE8M0 codes) per fragment row and stage. The 64-K-stage kernel above would need one
 // code load per row and stage, which doubles its L2 request count; until its codes
@@ -1825,6 +1724,12 @@ int ayk_fp8_blockwise_mm(const void* a, int64_t lda, const void* b, int64_t ldb,
   return launch_gemm<MODE_BLOCK>(g, static_cast<hipStream_t>(stream), op);
 }
 
+// MoE grouped block-128 GEMM: expert e owns activation rows [off_e, off_e + M_e) of
+// a [M_total, K] and weights b[e] = [N, K] (memory [E][N][K]); scales are fp32,
+// [M_total, K/128] per row and 128-K block for the activations, [E][N/128][K/128] for
+// the weights. The 256 x 256 block-128 kernel's grouped form (gemm_block.hip) takes one
+// tile of one expert per workgroup; the launch is an upper bound on the tile count (no
+// host synchronisation).
 int ayk_fp8_grouped_blockwise_mm(const void* a, const void* b, const float* scales_a, const float* scales_b,
                                  const int32_t* problem_sizes, const int32_t* expert_offsets, int64_t num_experts,
                                  int64_t m_total, int64_t n, int64_t k, void* out, int out_dtype,
@@ -1843,26 +1748,21 @@ int ayk_fp8_grouped_blockwise_mm(const void* a, const void* b, const float* scal
       (reinterpret_cast<uintptr_t>(scales_b) & 3))
     return fail(AYK_EINVAL, "%s: operands must be 16-byte aligned (scales 4-byte)", op);
   if (k > 0x7FFFFFFF || n * k > ((int64_t)1 << 31)) return fail(AYK_EINVAL, "%s: expert weight too large", op);
-  // Upper bound on the tiles: every expert adds at most one partial M tile.
-  const int64_t bound = cdiv((cdiv(m_total, kBlkTile) + num_experts) * cdiv(n, kBlkTile), 16) * 16;
-  if (bound > 0x7FFFFFFF) return fail(AYK_EINVAL, "%s: problem too large", op);
   if (int rc = check_device()) return rc;
-  GroupedBlockArgs ga{};
-  ga.a = static_cast<const uint8_t*>(a);
-  ga.b = static_cast<const uint8_t*>(b);
-  ga.sa = scales_a;
-  ga.sb = scales_b;
-  ga.out = out;
-  ga.out_dtype = out_dtype;
-  ga.problem_sizes = problem_sizes;
-  ga.expert_offsets = expert_offsets;
-  ga.num_experts = (int)num_experts;
-  ga.m_total = m_total;
-  ga.n = n;
-  ga.k = k;
-  hipLaunchKernelGGL(fp8_grouped_block_kernel, dim3((unsigned)bound), dim3(kBlkThreads), 0,
-                     static_cast<hipStream_t>(stream), ga);
-  return check_launch(op);
+  Grouped256Args gb{};
+  gb.a = static_cast<const uint8_t*>(a);
+  gb.b = static_cast<const uint8_t*>(b);
+  gb.sa = scales_a;
+  gb.sb = scales_b;
+  gb.out = out;
+  gb.out_dtype = out_dtype;
+  gb.problem_sizes = problem_sizes;
+  gb.expert_offsets = expert_offsets;
+  gb.num_experts = (int)num_experts;
+  gb.m_total = m_total;
+  gb.n = n;
+  gb.k = k;
+  return grouped_block256_launch(gb, static_cast<hipStream_t>(stream), op);
 }
 
 size_t ayk_mxfp8_scaled_mm_workspace_bytes(int64_t M, int64_t N, int64_t K) {

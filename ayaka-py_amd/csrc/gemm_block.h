@@ -30,11 +30,31 @@ struct Block256Args {
   size_t ws_bytes;
 };
 
+// Grouped (MoE) problem: expert e owns activation rows [expert_offsets[e], + M_e) of
+// a [m_total, k] and weights b[e] = [n, k]; scales sa [m_total, k / 128], sb[e]
+// [n / 128, k / 128] fp32; out [m_total, n]. problem_sizes [E, 3] = (M_e, N_e, K_e) and
+// expert_offsets [E] are read on the device.
+struct Grouped256Args {
+  const uint8_t* a;
+  const uint8_t* b;
+  const float* sa;
+  const float* sb;
+  void* out;
+  int out_dtype;
+  const int32_t* problem_sizes;
+  const int32_t* expert_offsets;
+  int num_experts;
+  int64_t m_total, n, k;
+};
+
 // Whether the 256 x 256 kernel takes this problem (shape, alignment and dtype rules).
 bool block256_supported(const Block256Args& g);
 // K splits the 256 x 256 kernel uses (1: none); a function of the shape only.
 int64_t block256_split(int64_t M, int64_t N, int64_t K);
 // Launch (the kernel and, with a K split, the reduce). Returns an ayk_status.
 int block256_launch(const Block256Args& g, hipStream_t st, const char* op);
+// Grouped launch (n and k multiples of 128, 16-byte aligned operands, checked by the
+// caller). Returns an ayk_status.
+int grouped_block256_launch(const Grouped256Args& ga, hipStream_t st, const char* op);
 
 }  // namespace ayk

@@ -136,8 +136,19 @@ __device__ __attribute__((always_inline)) inline void block256_epilogue(const Bl
       const uint4 val = *reinterpret_cast<const uint4*>(region + rr * kRowBytes + ((cc ^ (rr & (kChunks - 1) & 15)) * 16));
       if (gm < g.M && gn < g.N) {
         uint8_t* out = static_cast<uint8_t*>(g.out) + (gm * g.ldo + gn) * EB;
-        if (gn + 16 / EB <= g.N) *reinterpret_cast<uint4*>(out) = val;
-        else *reinterpret_cast<uint2*>(out) = make_uint2(val.x, val.y);  // N % 4 == 0
+        if (gn + 16 / EB <= g.N) {
+          *reinterpret_cast<uint4*>(out) = val;
+        } else {  // the row's last columns, element by element (an expert's N need not be a multiple of 4)
+          const uint32_t vw[4] = {val.x, val.y, val.z, val.w};
+          const int64_t left = g.N - gn;
+#pragma unroll
+          for (int c = 0; c < 16 / EB - 1; ++c) {
+            if (c < left) {
+              if constexpr (EB == 4) reinterpret_cast<uint32_t*>(out)[c] = vw[c];
+              else reinterpret_cast<uint16_t*>(out)[c] = (uint16_t)(vw[c / 2] >> (16 * (c % 2)));
+            }
+          }
+        }
       }
     }
     asm volatile("s_waitcnt lgkmcnt(0)" ::: "memory");
@@ -152,29 +163,14 @@ __device__ __attribute__((always_inline)) inline void block256_epilogue_out(cons
   else block256_epilogue<OUT, false>(g, U, mu, m_tile, n_tile, region);
 }
 
-// blockIdx.x: tile (XCD-aware order); blockIdx.y: K split (kps > 0: K range
-// [y kps, (y + 1) kps), fp32 partial to ws[y], no bias).
-__global__ __launch_bounds__(kThreads, 1) void fp8_block256_kernel(Block256Args gin, int tiles_m, int64_t kps) {
-  __shared__ __attribute__((aligned(1024))) uint8_t P0[kPairBytes];
-  __shared__ __attribute__((aligned(1024))) uint8_t P1[kPairBytes];
-
-  Block256Args g = gin;
-  int64_t k0 = 0, klen = gin.K;
-  if (kps > 0) {
-    k0 = (int64_t)blockIdx.y * kps;
-    klen = gin.K - k0 < kps ? gin.K - k0 : kps;
-    g.bias = nullptr;
-    g.out = gin.ws + (int64_t)blockIdx.y * gin.M * gin.N;
-    g.out_dtype = AYK_F32;
-    g.ldo = gin.N;
-  }
-
+// One 256 x 256 output tile (tm, tn) over the K range [k0, k0 + klen) (whole 128-K
+// blocks), written to g.out; P0 / P1 are the workgroup's two pair buffers.
+__device__ __attribute__((always_inline)) inline void block256_tile(const Block256Args& g, int tm, int tn, int64_t k0,
+                                                                    int64_t klen, uint8_t* P0, uint8_t* P1) {
   const int tid = threadIdx.x, lane = tid & 63;
   const int wave_u = __builtin_amdgcn_readfirstlane(tid >> 6);
   const int wn = wave_u >> 2, wm = wave_u & 3;
   const int h = lane >> 5, frow = lane & 31;
-  int tm, tn;
-  big_tile_coords(blockIdx.x, tiles_m, (int)cdiv(g.N, kTile), tm, tn);
   const int64_t n_base = (int64_t)tn * kTile, m_base = (int64_t)tm * kTile;
   const int np = (int)(klen / kPairK);   // K blocks of this range (>= 1)
   const int npairs = (np + 1) & ~1;      // the loop runs pairs two at a time
@@ -391,6 +387,125 @@ __global__ __launch_bounds__(kThreads, 1) void fp8_block256_kernel(Block256Args 
   else block256_epilogue_out<AYK_F32>(g, U, mu, m_base, n_base, region);
 }
 
+// blockIdx.x: tile (XCD-aware order); blockIdx.y: K split (kps > 0: K range
+// [y kps, (y + 1) kps), fp32 partial to ws[y], no bias).
+__global__ __launch_bounds__(kThreads, 1) void fp8_block256_kernel(Block256Args gin, int tiles_m, int64_t kps) {
+  __shared__ __attribute__((aligned(1024))) uint8_t P0[kPairBytes];
+  __shared__ __attribute__((aligned(1024))) uint8_t P1[kPairBytes];
+  Block256Args g = gin;
+  int64_t k0 = 0, klen = gin.K;
+  if (kps > 0) {
+    k0 = (int64_t)blockIdx.y * kps;
+    klen = gin.K - k0 < kps ? gin.K - k0 : kps;
+    g.bias = nullptr;
+    g.out = gin.ws + (int64_t)blockIdx.y * gin.M * gin.N;
+    g.out_dtype = AYK_F32;
+    g.ldo = gin.N;
+  }
+  int tm, tn;
+  big_tile_coords(blockIdx.x, tiles_m, (int)cdiv(g.N, kTile), tm, tn);
+  block256_tile(g, tm, tn, k0, klen, P0, P1);
+}
+
+// Expert e's problem, clamped to what the operands hold (rows past M_total, N_e > n,
+// K_e > k, K in whole 128-K blocks as the reference's K // 128), so device-side
+// metadata can never address outside the tensors.
+struct Expert256 {
+  int64_t off, m, n, k;
+};
+__device__ inline Expert256 expert256(const Grouped256Args& ga, int e) {
+  Expert256 p;
+  const int64_t off = ga.expert_offsets[e];
+  p.off = off < 0 ? 0 : (off > ga.m_total ? ga.m_total : off);
+  const int64_t m = ga.problem_sizes[3 * e], n = ga.problem_sizes[3 * e + 1], k = ga.problem_sizes[3 * e + 2];
+  p.m = m < 0 ? 0 : (m > ga.m_total - p.off ? ga.m_total - p.off : m);
+  p.n = n < 0 ? 0 : (n > ga.n ? ga.n : n);
+  p.k = k < 0 ? 0 : ((k > ga.k ? ga.k : k) / kPairK) * kPairK;
+  return p;
+}
+__device__ inline int64_t expert256_tiles(const Expert256& p) { return cdiv(p.m, kTile) * cdiv(p.n, kTile); }
+
+// Grouped (MoE) form: workgroup b takes logical tile pid of the concatenation of every
+// expert's tiles (row tiles first within a column tile). Workgroup b runs on XCD b % 8;
+// pid maps the 16 logical tiles 16 x .. 16 x + 15 to workgroups 8 apart (one XCD,
+// dispatched together), so an expert's column tiles share its activation rows in that
+// XCD's L2 while each reads its own weight panel once. The grid is an upper bound (a
+// multiple of 128); workgroups past the real tile count leave at once.
+__global__ __launch_bounds__(kThreads, 1) void fp8_grouped_block256_kernel(Grouped256Args ga) {
+  __shared__ __attribute__((aligned(1024))) uint8_t P0[kPairBytes];
+  __shared__ __attribute__((aligned(1024))) uint8_t P1[kPairBytes];
+  const int lane = threadIdx.x & 63;
+  const int E = ga.num_experts, per = (E + 63) / 64;
+  const int64_t b = blockIdx.x;
+  const int64_t pid = (b & ~(int64_t)127) + 16 * (b & 7) + ((b >> 3) & 15);
+  // Locate the expert: lane l sums the tiles of experts [l per, l per + per), a wave
+  // scan makes prefixes, the first lane whose inclusive prefix passes pid owns it.
+  int64_t mine = 0;
+  for (int i = 0; i < per; ++i) {
+    const int e = lane * per + i;
+    if (e < E) mine += expert256_tiles(expert256(ga, e));
+  }
+  int64_t incl = mine;
+#pragma unroll
+  for (int d = 1; d < 64; d <<= 1) {
+    const int64_t v = __shfl_up(incl, d, 64);
+    if (lane >= d) incl += v;
+  }
+  const uint64_t owners = __ballot(incl > pid);
+  if (owners == 0) return;  // past the real tile count (uniform: the ballot is)
+  const int owner = __ffsll((unsigned long long)owners) - 1;
+  int64_t start = __shfl(incl - mine, owner, 64);
+  int e = owner * per;
+  Expert256 p = expert256(ga, e);
+  for (int64_t t = expert256_tiles(p); pid >= start + t; t = expert256_tiles(p)) {
+    start += t;
+    p = expert256(ga, ++e);
+  }
+  // Everything below is wavefront-uniform: keep it in scalar registers.
+  auto uni64 = [](int64_t v) {
+    const uint32_t lo = (uint32_t)__builtin_amdgcn_readfirstlane((int)(uint32_t)v);
+    const uint32_t hi = (uint32_t)__builtin_amdgcn_readfirstlane((int)(uint32_t)((uint64_t)v >> 32));
+    return (int64_t)(((uint64_t)hi << 32) | lo);
+  };
+  e = __builtin_amdgcn_readfirstlane(e);
+  p.off = uni64(p.off);
+  p.m = uni64(p.m);
+  p.n = uni64(p.n);
+  p.k = uni64(p.k);
+  const int64_t local = uni64(pid - start);
+  const int64_t tiles_m = cdiv(p.m, kTile);
+  const int tm = __builtin_amdgcn_readfirstlane((int)(local % tiles_m));
+  const int tn = __builtin_amdgcn_readfirstlane((int)(local / tiles_m));
+  const int eb = ga.out_dtype == AYK_F32 ? 4 : 2;
+  if (p.k == 0) {  // no whole 128-K block: the sum is empty, the tile is zeros
+    for (int idx = threadIdx.x; idx < kTile * kTile; idx += kThreads) {
+      const int64_t gm = (int64_t)tm * kTile + idx / kTile, gn = (int64_t)tn * kTile + idx % kTile;
+      if (gm < p.m && gn < p.n) store_f32(ga.out, ga.out_dtype, (p.off + gm) * ga.n + gn, 0.0f);
+    }
+    return;
+  }
+  const int64_t kb_total = ga.k / kPairK;
+  Block256Args g{};
+  g.a = ga.a + p.off * ga.k;
+  g.lda = ga.k;
+  g.w = ga.b + (int64_t)e * ga.n * ga.k;
+  g.ldw = ga.k;
+  g.M = p.m;
+  g.N = p.n;
+  g.K = p.k;
+  g.sa = ga.sa + p.off * kb_total;
+  g.ld_sa = kb_total;
+  g.sa_col_major = 0;
+  g.sb = ga.sb + (int64_t)e * (ga.n / kPairK) * kb_total;
+  g.sb_dtype = AYK_F32;
+  g.ld_sb = kb_total;
+  g.bias = nullptr;
+  g.out = static_cast<uint8_t*>(ga.out) + p.off * ga.n * eb;
+  g.out_dtype = ga.out_dtype;
+  g.ldo = ga.n;
+  block256_tile(g, tm, tn, 0, p.k, P0, P1);
+}
+
 // Fixed-order sum of the K-split partials, bias, one rounding.
 __global__ __launch_bounds__(256) void block256_reduce(const float* __restrict__ part, int64_t M, int64_t N, int split,
                                                        const void* __restrict__ bias, int bias_dtype, void* __restrict__ out,
@@ -440,6 +555,14 @@ int block256_launch(const Block256Args& g, hipStream_t st, const char* op) {
   if (int rc = check_launch(op)) return rc;
   hipLaunchKernelGGL(block256_reduce, dim3((unsigned)cdiv(g.M * g.N, 256)), dim3(256), 0, st, g.ws, g.M, g.N, (int)split,
                      g.bias, g.bias_dtype, g.out, g.out_dtype, g.ldo);
+  return check_launch(op);
+}
+
+int grouped_block256_launch(const Grouped256Args& ga, hipStream_t st, const char* op) {
+  // Upper bound on the tiles: every expert adds at most one partial 256-row tile.
+  const int64_t bound = cdiv((cdiv(ga.m_total, kTile) + ga.num_experts) * cdiv(ga.n, kTile), 128) * 128;
+  if (bound > 0x7FFFFFFF) return fail(AYK_EINVAL, "%s: problem too large", op);
+  hipLaunchKernelGGL(fp8_grouped_block256_kernel, dim3((unsigned)bound), dim3(kThreads), 0, st, ga);
   return check_launch(op);
 }
 
