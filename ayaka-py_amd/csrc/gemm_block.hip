@@ -493,12 +493,14 @@ __global__ __launch_bounds__(kThreads, 1) void fp8_grouped_block256_kernel(Group
   g.M = p.m;
   g.N = p.n;
   g.K = p.k;
+  // The reference's pointer tables: expert e's scales start at row off_e of sa and at
+  // block row e (n / 128) of sb, both with row stride K_e / 128.
   g.sa = ga.sa + p.off * kb_total;
-  g.ld_sa = kb_total;
+  g.ld_sa = p.k / kPairK;
   g.sa_col_major = 0;
   g.sb = ga.sb + (int64_t)e * (ga.n / kPairK) * kb_total;
   g.sb_dtype = AYK_F32;
-  g.ld_sb = kb_total;
+  g.ld_sb = p.k / kPairK;
   g.bias = nullptr;
   g.out = static_cast<uint8_t*>(ga.out) + p.off * ga.n * eb;
   g.out_dtype = ga.out_dtype;

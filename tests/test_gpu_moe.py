@@ -90,6 +90,23 @@ def test_grouped_mm_matches_oracle(gpu, case, out_dtype):
         assert_linear_close(got[owned], ref[owned], f"case {case}")
 
 
+def test_grouped_mm_partial_experts(gpu):
+    """Experts narrower and shorter than the operands: N_e < N (one not a multiple of 4,
+    which the store tail writes element by element), K_e < K, with the
+    scales addressed with row stride K_e / 128 as the reference's tables."""
+    counts, n, k = [70, 3, 200], 512, 1024
+    _say("grouped mm partial experts")
+    a, b, sa, sb, _, off = _problem(counts, n, k, seed=21)
+    ps = torch.tensor([[70, 510, 640], [3, 256, 1024], [200, 300, 896]], dtype=torch.int32)
+    out, _ = _run(gpu, a, b, sa, sb, ps, off, torch.bfloat16)
+    sentinel = torch.full((a.shape[0], n), 3.0, dtype=torch.bfloat16)
+    ref = ora.grouped_blockwise_mm(a, b, sa, sb, ps, off, sentinel.float())
+    got = out.cpu()
+    for (m_e, n_e, _), o in zip(ps.tolist(), off.tolist()):
+        assert torch.equal(got[o:o + m_e, n_e:], sentinel[o:o + m_e, n_e:]), "columns past N_e were written"
+        assert_linear_close(got[o:o + m_e, :n_e], ref[o:o + m_e, :n_e], f"expert at {o}")
+
+
 @pytest.mark.parametrize("swap_ab", [False, True])
 def test_pointer_tables_and_transposed_weight_view(gpu, swap_ab):
     counts, n, k = [4, 0, 9], 256, 384
