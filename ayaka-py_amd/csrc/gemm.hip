@@ -71,6 +71,10 @@ struct GemmArgs {
   float* ws;       // split-K partials (block-scaled GEMM), ws_bytes long
   size_t ws_bytes;
   int64_t kps;     // general kernel, block mode: K per split (0: no split; blockIdx.y = split)
+  // 256 x 256 pair kernel, tail split (tail_split > 1): workgroups past dp_tiles take
+  // K piece (b - dp_tiles) % tail_split of tile dp_tiles + (b - dp_tiles) / tail_split.
+  int dp_tiles;
+  int tail_split;
 };
 
 __device__ inline v16f mfma(const v8i& wa, const v8i& ab, const v16f& c, int sw, int sa) {
@@ -707,13 +711,32 @@ __global__ __launch_bounds__(kThreads, 1) void fp8_gemm_big_kernel(GemmArgs g) {
 // narrow kernel's; the step schedule (one barrier per pair) is its own.
 template <int MODE>
 __global__ __launch_bounds__(kThreads, 1) void fp8_gemm_pair_kernel(GemmArgs gin) {
-  // Rowwise / MX K split (as in the general kernel): blockIdx.y's K range, scaled fp32
-  // partials to ws[y].
+  // The tile (XCD-aware order) and K range of this workgroup:
+  //  * a K split of every tile (gin.kps > 0, launches short of one round): blockIdx.y's
+  //    K range, scaled fp32 partials to ws[y] ([M, N]);
+  //  * a tail split (gin.tail_split > 1): the last, mostly empty round of tiles is
+  //    split over K across the CUs that round would leave idle; workgroup
+  //    b >= dp_tiles takes piece (b - dp_tiles) % tail_split of tile
+  //    dp_tiles + (b - dp_tiles) / tail_split, a 256 x 256 scaled fp32 partial in the
+  //    compact workspace [tail_split][tail tiles][256][256];
+  //  * otherwise tile blockIdx.x over all of K.
   GemmArgs g = gin;
+  int tile_id = blockIdx.x, piece = blockIdx.y;
+  int64_t kps = gin.kps;
+  bool tail = false;
+  if (gin.tail_split > 1 && (int)blockIdx.x >= gin.dp_tiles) {
+    const int u = (int)blockIdx.x - gin.dp_tiles;
+    tile_id = gin.dp_tiles + u / gin.tail_split;
+    piece = u % gin.tail_split;
+    kps = gin.K / gin.tail_split;  // whole pairs (MX: whole 512-K chunks), by the plan
+    tail = true;
+  }
+  int tm, tn;
+  big_tile_coords(tile_id, g.tiles_m, (int)cdiv(g.N, kBigTile), tm, tn);
   if constexpr (MODE == MODE_SCALED || MODE == MODE_MX || MODE == MODE_INT8) {
-    if (gin.kps > 0) {
-      const int64_t k0 = (int64_t)blockIdx.y * gin.kps;  // MX: kps % 512 == 0 keeps the code rows 16-byte aligned
-      g.K = gin.K - k0 < gin.kps ? gin.K - k0 : gin.kps;
+    if (kps > 0) {
+      const int64_t k0 = (int64_t)piece * kps;  // MX: kps % 512 == 0 keeps the code rows 16-byte aligned
+      g.K = gin.K - k0 < kps ? gin.K - k0 : kps;
       g.a = gin.a + k0;
       g.w = gin.w + k0;
       if constexpr (MODE == MODE_MX) {
@@ -721,9 +744,18 @@ __global__ __launch_bounds__(kThreads, 1) void fp8_gemm_pair_kernel(GemmArgs gin
         g.sb = static_cast<const uint8_t*>(gin.sb) + k0 / 32;
       }
       g.bias = nullptr;
-      g.out = gin.ws + (int64_t)blockIdx.y * gin.M * gin.N;
       g.out_dtype = AYK_F32;
-      g.ldo = gin.N;
+      if (tail) {
+        // The epilogue addresses out + (m * ldo + n) with the tile's global (m, n): the
+        // base is moved back by the tile origin so that the tile lands at its slot.
+        const int tail_tiles = (int)(cdiv(gin.M, kBigTile) * cdiv(gin.N, kBigTile)) - gin.dp_tiles;
+        const int64_t slot = (int64_t)piece * tail_tiles + (tile_id - gin.dp_tiles);
+        g.out = gin.ws + slot * kBigTile * kBigTile - ((int64_t)tm * kBigTile * kBigTile + (int64_t)tn * kBigTile);
+        g.ldo = kBigTile;
+      } else {
+        g.out = gin.ws + (int64_t)piece * gin.M * gin.N;
+        g.ldo = gin.N;
+      }
     }
   }
   static_assert(row_scaled(MODE) || MODE == MODE_MX, "per-row / per-tensor scales or MX codes");
@@ -745,8 +777,6 @@ __global__ __launch_bounds__(kThreads, 1) void fp8_gemm_pair_kernel(GemmArgs gin
   const int wave_u = __builtin_amdgcn_readfirstlane(tid >> 6);  // keep descriptors in SGPRs
   const int wn = wave_u >> 1, wm = wave_u & 1;
   const int h = lane >> 5, frow = lane & 31;
-  int tm, tn;
-  big_tile_coords(blockIdx.x, g.tiles_m, (int)cdiv(g.N, kBigTile), tm, tn);
   const int64_t n_base = (int64_t)tn * kBigTile, m_base = (int64_t)tm * kBigTile;
   const int np = (int)(g.K / kPairK);    // real pairs
   const int npairs = (np + 1) & ~1;      // padded to the unroll (a padded pair computes zeros)
@@ -1235,6 +1265,36 @@ __global__ __launch_bounds__(kBlkThreads, 1) void fp8_gemm_block_split_kernel(Ge
   block_gemm_tile(s, tm, tn, L0, L1, L2, L3);
 }
 
+// Tail split of the 256 x 256 pair kernel: tile t (0 .. tail_tiles - 1) of the tail is
+// tile dp_tiles + t of the XCD-aware order; its tail_split partials sit at
+// part[(y tail_tiles + t) 65536 ..]. Summed in piece order, bias added, rounded once;
+// four consecutive columns per thread (N % 4 == 0 on this path).
+__global__ __launch_bounds__(256) void tail_split_reduce(const float* __restrict__ part, int tail_tiles, int split,
+                                                         int dp_tiles, int tiles_m, int tiles_n, int64_t M, int64_t N,
+                                                         const void* __restrict__ bias, int bias_dtype,
+                                                         void* __restrict__ out, int out_dtype, int64_t ldo) {
+  constexpr int kTileElems = kBigTile * kBigTile;
+  const int64_t i = ((int64_t)blockIdx.x * 256 + threadIdx.x) * 4;
+  if (i >= (int64_t)tail_tiles * kTileElems) return;
+  const int t = (int)(i / kTileElems), within = (int)(i % kTileElems);
+  const int r = within / kBigTile, c = within % kBigTile;
+  int tm, tn;
+  big_tile_coords(dp_tiles + t, tiles_m, tiles_n, tm, tn);
+  const int64_t m = (int64_t)tm * kBigTile + r, n = (int64_t)tn * kBigTile + c;
+  if (m >= M || n >= N) return;
+  float4 v = *reinterpret_cast<const float4*>(part + i);
+  for (int y = 1; y < split; ++y) {
+    const float4 p = *reinterpret_cast<const float4*>(part + ((int64_t)y * tail_tiles + t) * kTileElems + within);
+    v.x += p.x; v.y += p.y; v.z += p.z; v.w += p.w;
+  }
+  float o[4] = {v.x, v.y, v.z, v.w};
+#pragma unroll
+  for (int q = 0; q < 4; ++q) {
+    if (bias) o[q] += load_f32(bias, bias_dtype, n + q);
+    store_f32(out, out_dtype, m * ldo + n + q, o[q]);
+  }
+}
+
 __global__ __launch_bounds__(256) void block_split_reduce(const float* __restrict__ part, int64_t M, int64_t N, int split,
                                                           const void* __restrict__ bias, int bias_dtype, void* __restrict__ out,
                                                           int out_dtype, int64_t ldo) {
@@ -1289,6 +1349,40 @@ int64_t scaled_split(int64_t M, int64_t N, int64_t K, int bm, int bn) {
   return cdiv(K, kps);
 }
 int64_t scaled_kps(int64_t K, int64_t split) { return cdiv(K / 128, split) * 128; }
+
+// Tail split of the 256 x 256 pair kernel (launches of more than one round): when the
+// last round would hold at most a third of a round of tiles, those tiles are split over
+// K into the largest number of pieces (at least three) that still fits in one round
+// (256 workgroups), each of at least 512 K, dividing K into whole 128-K pairs (MXFP8:
+// whole 512-K code chunks). The first rounds run whole tiles. A piece pays a tile's
+// prologue and a 256 KB fp32 epilogue, and the partials a reduce: measured on Qwen2
+// gate_up (K = 3584), M = 512 went 115 -> 105 us and M = 4096 649 -> 638 us, while a
+// two-way split (M = 8192) broke even. A function of the shape only (the workspace
+// query reproduces it). split = 1: no tail split.
+struct TailPlan {
+  int dp_tiles, split, tail_tiles;
+};
+TailPlan tail_plan(int64_t M, int64_t N, int64_t K, bool mx) {
+  TailPlan p{0, 1, 0};
+  const int64_t tiles = cdiv(M, kBigTile) * cdiv(N, kBigTile);
+  const int64_t unit = mx ? 512 : 128;
+  if (tiles <= 256 || tiles > 0x7FFFFFFF / 2 || K % unit) return p;
+  const int64_t rem = tiles % 256;
+  if (rem == 0 || rem > 256 / 3) return p;
+  for (int64_t s = 256 / rem; s >= 3; --s) {
+    if ((K / unit) % s == 0 && K / s >= 512) {
+      p.dp_tiles = (int)(tiles - rem);
+      p.split = (int)s;
+      p.tail_tiles = (int)rem;
+      return p;
+    }
+  }
+  return p;
+}
+size_t tail_workspace(const TailPlan& p) {
+  return p.split > 1 ? (size_t)p.split * (size_t)p.tail_tiles * kBigTile * kBigTile * sizeof(float) : 0;
+}
+
 size_t scaled_split_workspace(int64_t M, int64_t N, int64_t K) {
   const int bm = M <= 32 ? 32 : (M <= 64 ? 64 : 128);
   int64_t split = scaled_split(M, N, K, bm, 128);
@@ -1468,6 +1562,31 @@ __global__ __launch_bounds__(kThreads, 1) void fp8_gemm_mx128_kernel(GemmArgs g)
   big_epilogue<MODE>(g, acc, BigScales{}, m_base, n_base, lds0);
 }
 
+// The pair kernel over all K, with the tail split when the plan has one (whole rounds
+// of tiles, then the last round's tiles in K pieces and their fixed-order reduce).
+template <int MODE>
+int launch_pair_tail(GemmArgs g, int64_t tiles, hipStream_t st, const char* op) {
+  const TailPlan tp = tail_plan(g.M, g.N, g.K, MODE == MODE_MX);
+  g.kps = 0;
+  g.dp_tiles = tp.dp_tiles;
+  g.tail_split = tp.split;
+  if (tp.split == 1) {
+    hipLaunchKernelGGL((fp8_gemm_pair_kernel<MODE>), dim3((unsigned)tiles), dim3(kThreads), 0, st, g);
+    return check_launch(op);
+  }
+  const size_t need = tail_workspace(tp);
+  if (g.ws == nullptr || g.ws_bytes < need)
+    return fail(AYK_EWORKSPACE, "%s: workspace of %zu bytes required, %zu given", op, need, g.ws_bytes);
+  const int64_t grid = (int64_t)tp.dp_tiles + (int64_t)tp.tail_tiles * tp.split;
+  hipLaunchKernelGGL((fp8_gemm_pair_kernel<MODE>), dim3((unsigned)grid), dim3(kThreads), 0, st, g);
+  if (int rc = check_launch(op)) return rc;
+  const int64_t threads = (int64_t)tp.tail_tiles * kBigTile * kBigTile / 4;
+  hipLaunchKernelGGL(tail_split_reduce, dim3((unsigned)cdiv(threads, 256)), dim3(256), 0, st, g.ws, tp.tail_tiles,
+                     tp.split, tp.dp_tiles, g.tiles_m, (int)cdiv(g.N, kBigTile), g.M, g.N, g.bias, g.bias_dtype, g.out,
+                     g.out_dtype, g.ldo);
+  return check_launch(op);
+}
+
 template <int MODE>
 int launch_big(GemmArgs g, hipStream_t st, const char* op) {
   static_assert(MODE != MODE_BLOCK, "block scales use the general kernel");
@@ -1486,12 +1605,11 @@ int launch_big(GemmArgs g, hipStream_t st, const char* op) {
         if (g.ws == nullptr || g.ws_bytes < need)
           return fail(AYK_EWORKSPACE, "%s: workspace of %zu bytes required, %zu given", op, need, g.ws_bytes);
       }
+      if (split == 1) return launch_pair_tail<MODE>(g, tiles, st, op);
       hipLaunchKernelGGL((fp8_gemm_pair_kernel<MODE>), dim3((unsigned)tiles, (unsigned)split), dim3(kThreads), 0, st, g);
-      if (split > 1) {
-        if (int rc = check_launch(op)) return rc;
-        hipLaunchKernelGGL(block_split_reduce, dim3((unsigned)cdiv(g.M * g.N, 256)), dim3(256), 0, st, g.ws, g.M, g.N,
-                           (int)split, g.bias, g.bias_dtype, g.out, g.out_dtype, g.ldo);
-      }
+      if (int rc = check_launch(op)) return rc;
+      hipLaunchKernelGGL(block_split_reduce, dim3((unsigned)cdiv(g.M * g.N, 256)), dim3(256), 0, st, g.ws, g.M, g.N,
+                         (int)split, g.bias, g.bias_dtype, g.out, g.out_dtype, g.ldo);
     } else {
       hipLaunchKernelGGL((fp8_gemm_mx128_kernel<MODE>), dim3((unsigned)tiles), dim3(kThreads), 0, st, g);
     }
@@ -1505,6 +1623,7 @@ int launch_big(GemmArgs g, hipStream_t st, const char* op) {
         return fail(AYK_EWORKSPACE, "%s: workspace of %zu bytes required, %zu given", op, need, g.ws_bytes);
       g.kps = scaled_kps(g.K, split);
     }
+    if (split == 1 && MODE == MODE_SCALED) return launch_pair_tail<MODE>(g, tiles, st, op);
     hipLaunchKernelGGL((fp8_gemm_pair_kernel<MODE>), dim3((unsigned)tiles, (unsigned)split), dim3(kThreads), 0, st, g);
     if (split > 1) {
       if (int rc = check_launch(op)) return rc;
@@ -1640,7 +1759,9 @@ extern "C" {
 
 size_t ayk_fp8_scaled_mm_workspace_bytes(int64_t M, int64_t N, int64_t K) {
   if (M < 1 || N < 1 || K < 1) return 0;
-  return scaled_split_workspace(M, N, K);
+  const size_t split = scaled_split_workspace(M, N, K);
+  const size_t tail = M >= kBigTile && N >= kBigTile ? tail_workspace(tail_plan(M, N, K, false)) : 0;
+  return split > tail ? split : tail;
 }
 
 int ayk_fp8_scaled_mm(const void* a, int64_t lda, const void* b, int64_t ldb, int64_t M, int64_t N,
@@ -1767,7 +1888,9 @@ int ayk_fp8_grouped_blockwise_mm(const void* a, const void* b, const float* scal
 
 size_t ayk_mxfp8_scaled_mm_workspace_bytes(int64_t M, int64_t N, int64_t K) {
   if (M < 1 || N < 1 || K < 1) return 0;
-  return scaled_split_workspace(M, N, K);
+  const size_t split = scaled_split_workspace(M, N, K);
+  const size_t tail = M >= kBigTile && N >= kBigTile ? tail_workspace(tail_plan(M, N, K, true)) : 0;
+  return split > tail ? split : tail;
 }
 
 int ayk_mxfp8_scaled_mm(const void* a, int64_t lda, const uint8_t* a_scale, int64_t ld_as,

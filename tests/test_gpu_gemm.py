@@ -164,6 +164,47 @@ def test_mxfp8_scaled_mm_split_k(gpu, m, n, k):
     assert_linear_close(y, ref, "mxfp8_scaled_mm split-K")
 
 
+# 276 tiles of 256 x 256: one whole round, then a last round of 20 tiles that the pair
+# kernel splits over K (three 512-K pieces each) into the workspace, ragged M and N.
+TAIL_MNK = (1300, 11712, 1536)
+
+
+@pytest.mark.parametrize("rowwise,out_dtype", [(True, torch.bfloat16), (False, torch.float16), (True, torch.float32)])
+def test_fp8_scaled_mm_tail_split(gpu, rowwise, out_dtype):
+    from ayaka.kernel.hip import _lib, fp8_scaled_mm
+
+    m, n, k = TAIL_MNK
+    _say(f"fp8_scaled_mm tail split m={m} n={n} k={k} rowwise={rowwise} out={out_dtype}")
+    assert _lib.query("ayk_fp8_scaled_mm_workspace_bytes", m, n, k) == 3 * 20 * 256 * 256 * 4, "tail split expected"
+    a = _fp8((m, k), seed=41, scale=40)
+    w = _fp8((n, k), seed=42, scale=40)
+    sa = (torch.rand(m, generator=_gen(43)) * 0.01 + 1e-3) if rowwise else torch.tensor(0.004)
+    sb = (torch.rand(n, generator=_gen(44)) * 0.01 + 1e-3) if rowwise else torch.tensor(0.002)
+    bias = (torch.randn(n, generator=_gen(45)) * 30).to(torch.bfloat16)
+    ref = ora.fp8_scaled_mm(a, w, sa, sb, bias)
+    out = torch.empty(m, n, dtype=out_dtype, device=gpu)
+    fp8_scaled_mm(a.to(gpu), w.to(gpu).t(), sa.to(gpu), sb.to(gpu), bias.to(gpu), out=out)
+    assert_linear_close(out, ref, "fp8_scaled_mm tail split")
+
+
+def test_mxfp8_scaled_mm_tail_split(gpu):
+    from ayaka.kernel.hip import _lib, mxfp8_scaled_mm
+
+    m, n, k = TAIL_MNK
+    _say(f"mxfp8_scaled_mm tail split m={m} n={n} k={k}")
+    assert _lib.query("ayk_mxfp8_scaled_mm_workspace_bytes", m, n, k) == 3 * 20 * 256 * 256 * 4, "tail split expected"
+    torch.manual_seed(46)
+    x = torch.distributions.StudentT(3.0).sample((m, k))
+    wf = torch.randn(n, k, generator=_gen(47))
+    qa, ca = ora.per_token_group_quant_mxfp8(x, 32)
+    qw, cw = ora.per_token_group_quant_mxfp8(wf, 32)
+    bias = (torch.randn(n, generator=_gen(48)) * 10).to(torch.bfloat16)
+    ref = ora.mxfp8_scaled_mm(qa, ca, qw, cw, bias)
+    y = mxfp8_scaled_mm(qa.to(gpu), ca.to(gpu), qw.to(gpu), cw.to(gpu), bias.to(gpu),
+                        out=torch.empty(m, n, dtype=torch.bfloat16, device=gpu))
+    assert_linear_close(y, ref, "mxfp8_scaled_mm tail split")
+
+
 @pytest.mark.parametrize("out_dtype", [torch.float16, torch.bfloat16, torch.float32])
 def test_fp8_scaled_mm_big_tile_strided_out(gpu, out_dtype):
     """256x256-tile kernel: every output dtype, a padded output row stride, M/N tails."""

@@ -324,7 +324,10 @@ def test_c_abi_rejects_bad_arguments_without_a_gpu():
     assert lib.ayk_fp8_weight_only_gemv_workspace_bytes(28672, 4096) == 0
     # GEMM split-K plans: too few tiles split K, a full round does not
     assert lib.ayk_fp8_scaled_mm_workspace_bytes(512, 3584, 18944) > 0
-    assert lib.ayk_fp8_scaled_mm_workspace_bytes(4096, 37888, 3584) == 0
+    assert lib.ayk_fp8_scaled_mm_workspace_bytes(4096, 28672, 4096) == 0  # seven whole rounds of tiles
+    # 2368 tiles: a last round of 64 tiles split four ways over K (256 x 256 fp32 each)
+    assert lib.ayk_fp8_scaled_mm_workspace_bytes(4096, 37888, 3584) == 4 * 64 * 256 * 256 * 4
+    assert lib.ayk_fp8_scaled_mm_workspace_bytes(8192, 37888, 3584) == 0  # a two-way tail split does not pay
     assert lib.ayk_int8_scaled_mm_workspace_bytes(512, 768, 8192) == 0  # INT8 never splits K
     # block-128 size query mirrors the launch: N < 128 at M <= 64 still splits K
     assert lib.ayk_fp8_blockwise_mm_workspace_bytes(16, 64, 4096) > 0
