@@ -986,15 +986,17 @@ __device__ inline void dma16_nt(const uint8_t* src, uint8_t* lds_dst) {
   __builtin_amdgcn_global_load_lds(src, (__attribute__((address_space(3))) void*)lds_dst, 16, 0, 2);
 }
 
-template <bool BF16, bool ROW_SCALE, int MP, int TW, int G, int D>
+template <bool BF16, bool ROW_SCALE, int MP, int TW, int G, int D, int KS>
 __global__ __launch_bounds__(kStWaves * kWave) void w8a16_stream_kernel(RsArgs a) {
   constexpr int MT = MP > 16 ? 2 : 1;        // 16-column MFMA tiles
   constexpr int RW = 16 * TW;                // rows per wavefront
-  constexpr int R = kStWaves * RW;           // rows per workgroup
+  constexpr int RG = kStWaves / KS;          // row groups per workgroup (KS K parts each)
+  constexpr int R = RG * RW;                 // rows per workgroup
   constexpr int kWStage = RW * kStK;         // weight bytes of one wavefront stage
   constexpr int kWIns = kWStage / 1024;      // direct loads per wavefront stage
-  constexpr int kXRow = 2 * G * kStK;        // bytes of one activation row of a chunk
-  constexpr int kXChunk = MP * kXRow;
+  constexpr int kXRow = 2 * G * kStK;        // bytes of one activation row of a chunk (one K part)
+  constexpr int kXPart = MP * kXRow;         // one K part's rows of a chunk
+  constexpr int kXChunk = KS * kXPart;
   constexpr int kXIns = kXChunk / (1024 * kStWaves);  // activation loads per wavefront and chunk
   constexpr int kSOps = ROW_SCALE ? 0 : 4 * TW;       // block-scale words per stage
   constexpr int kOpsW = kWIns + kSOps;
@@ -1016,10 +1018,15 @@ __global__ __launch_bounds__(kStWaves * kWave) void w8a16_stream_kernel(RsArgs a
   const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x / kWave);
   const int r16 = lane & 15, g = lane >> 4;
   uint8_t* myring = wring + wave * D * kWStage;
-  const int64_t n_wave = (int64_t)blockIdx.x * R + wave * RW;
+  // With KS > 1 the wavefronts of a row group take the KS parts of the K range (sums
+  // meet in LDS at the end): wavefront w is part w / RG of row group w % RG.
+  const int part = wave / RG, rg = wave % RG;
+  const int64_t n_wave = (int64_t)blockIdx.x * R + rg * RW;
   const int64_t kbeg = (int64_t)blockIdx.y * a.k_per_split;
   const int64_t klen = a.K - kbeg < a.k_per_split ? a.K - kbeg : a.k_per_split;
-  const int ns = (int)(klen / kStK);  // a multiple of G (host plan)
+  const int64_t plen = klen / KS;            // K per part
+  const int64_t kpart = kbeg + part * plen;
+  const int ns = (int)(plen / kStK);  // a multiple of G (host plan)
 
   // Weight loads: load j of a stage covers rows 4 j .. 4 j + 3 of the wavefront, lane l
   // row 4 j + l / 16 at physical chunk l % 16; rows past N re-read row N - 1.
@@ -1028,24 +1035,25 @@ __global__ __launch_bounds__(kStWaves * kWave) void w8a16_stream_kernel(RsArgs a
   for (int j = 0; j < kWIns; ++j) {
     const int row = 4 * j + (lane >> 4);
     const int64_t n = n_wave + row < a.N ? n_wave + row : a.N - 1;
-    wsrc[j] = a.w + n * a.ldw + kbeg + 16 * ((lane & 15) ^ (row & 15));
+    wsrc[j] = a.w + n * a.ldw + kpart + 16 * ((lane & 15) ^ (row & 15));
   }
   // Activation loads: load j of wavefront w fills chunk bytes 1024 (w kXIns + j) ..:
-  // row m, physical chunk p of that row; rows past M repeat row M - 1.
+  // K part q, row m, physical chunk p of that row; rows past M repeat row M - 1.
   const uint16_t* xsrc[kXIns];
   uint32_t xdst[kXIns];
 #pragma unroll
   for (int j = 0; j < kXIns; ++j) {
     const int byte = 1024 * (wave * kXIns + j) + 16 * lane;
-    const int m = byte / kXRow;
+    const int q = byte / kXPart;
+    const int m = (byte % kXPart) / kXRow;
     const int p = (byte % kXRow) / 16;
     const int64_t mm = m < a.M ? m : a.M - 1;
-    xsrc[j] = a.x + mm * a.ldx + kbeg + 8 * (p ^ (m & 15));
+    xsrc[j] = a.x + mm * a.ldx + kbeg + q * plen + 8 * (p ^ (m & 15));
     xdst[j] = __builtin_amdgcn_readfirstlane(1024 * (wave * kXIns + j));
   }
   // Fragment read offsets: weights (row 16 tt + r, window chunk 4 win + g) within a stage
   // slot; activations (row m = 16 mt + r, clamped to the staged rows) within a chunk.
-  uint32_t woff[TW][4], xoff[MT][4][2];
+  uint32_t woff[TW][4];
 #pragma unroll
   for (int tt = 0; tt < TW; ++tt)
 #pragma unroll
@@ -1069,7 +1077,7 @@ __global__ __launch_bounds__(kStWaves * kWave) void w8a16_stream_kernel(RsArgs a
     if (wave == 0) {
 #pragma unroll
       for (int i = 0; i < kSrowIns; ++i) {
-        const int row = kWave * i + lane < R ? kWave * i + lane : R - 1;
+        const int row = kWave * i + lane < R ? kWave * i + lane : R - 1;  // row of the workgroup
         const int64_t n = (int64_t)blockIdx.x * R + row < a.N ? (int64_t)blockIdx.x * R + row : a.N - 1;
         const uintptr_t p = reinterpret_cast<uintptr_t>(a.scale) + (uintptr_t)(((int64_t)((uint64_t)n / (uint64_t)a.by) * a.srs) * ssize);
         dma4(reinterpret_cast<const uint8_t*>(p & ~(uintptr_t)3), reinterpret_cast<uint8_t*>(srow_lds) + 4 * kWave * i);
@@ -1089,7 +1097,7 @@ __global__ __launch_bounds__(kStWaves * kWave) void w8a16_stream_kernel(RsArgs a
     if constexpr (!ROW_SCALE) {
 #pragma unroll
       for (int win = 0; win < 4; ++win) {
-        const int64_t kidx = (uint32_t)(kbeg + k + 64 * win + 16 * g) / (uint32_t)a.bx;
+        const int64_t kidx = (uint32_t)(kpart + k + 64 * win + 16 * g) / (uint32_t)a.bx;
 #pragma unroll
         for (int tt = 0; tt < TW; ++tt) sr[slot][tt][win] = load_bits(a.scale, a.scale_dtype, rowbase[tt] + kidx);
       }
@@ -1112,7 +1120,7 @@ __global__ __launch_bounds__(kStWaves * kWave) void w8a16_stream_kernel(RsArgs a
   // of chunk buffer `xb`.
   auto compute = [&](int slot, int s, int wb) {
     const uint32_t wbase = lds_addr(myring + slot * kWStage);
-    const uint32_t xbase = lds_addr(xbuf + ((s / G) & 1) * kXChunk);
+    const uint32_t xbase = lds_addr(xbuf + ((s / G) & 1) * kXChunk + part * kXPart);
 #pragma unroll
     for (int win = 0; win < 4; ++win) {
       constexpr int NB = TW + 2 * MT;
@@ -1161,7 +1169,7 @@ __global__ __launch_bounds__(kStWaves * kWave) void w8a16_stream_kernel(RsArgs a
     __builtin_amdgcn_s_barrier();
 #pragma unroll
     for (int tt = 0; tt < TW; ++tt) {
-      const int row = wave * RW + 16 * tt + r16;
+      const int row = rg * RW + 16 * tt + r16;
       uint32_t word;
       asm volatile("ds_read_b32 %0, %1\n\ts_waitcnt lgkmcnt(0)" : "=v"(word) : "v"(lds_addr(reinterpret_cast<const uint8_t*>(srow_lds)) + 4 * row) : "memory");
       const uint32_t shift = (uint32_t)((reinterpret_cast<uintptr_t>(a.scale) + (uintptr_t)(rowbase[tt] * ssize)) & 3) * 8;
@@ -1187,6 +1195,35 @@ __global__ __launch_bounds__(kStWaves * kWave) void w8a16_stream_kernel(RsArgs a
   });
   wait_vmcnt<0>();  // no direct load may still be writing LDS when the workgroup ends
 
+  if constexpr (KS > 1) {
+    // The K parts of a row group meet in LDS (the rings are free once every wavefront
+    // is past its last stage): wavefront w writes its sums at slot w, and part 0 adds
+    // the parts in order.
+    constexpr int kSlots = TW * MT * 4;
+    static_assert(kStWaves * kSlots * kWave * 4 <= kStWaves * D * kWStage, "the sums fit the rings");
+    float* red = reinterpret_cast<float*>(wring);
+    __syncthreads();
+#pragma unroll
+    for (int tt = 0; tt < TW; ++tt)
+#pragma unroll
+      for (int mt = 0; mt < MT; ++mt)
+#pragma unroll
+        for (int r = 0; r < 4; ++r) red[(wave * kSlots + (tt * MT + mt) * 4 + r) * kWave + lane] = acc[tt][mt][r];
+    __syncthreads();
+    if (part != 0) return;
+#pragma unroll
+    for (int tt = 0; tt < TW; ++tt)
+#pragma unroll
+      for (int mt = 0; mt < MT; ++mt)
+#pragma unroll
+        for (int r = 0; r < 4; ++r) {
+          float v = 0.0f;
+#pragma unroll
+          for (int q = 0; q < KS; ++q) v += red[((q * RG + rg) * kSlots + (tt * MT + mt) * 4 + r) * kWave + lane];
+          acc[tt][mt][r] = v;
+        }
+  }
+
   // D[n][m]: lane holds m = lane % 16 (+ 16 mt) and n = 4 (lane / 16) + r of its tile.
 #pragma unroll
   for (int tt = 0; tt < TW; ++tt)
@@ -1204,50 +1241,68 @@ __global__ __launch_bounds__(kStWaves * kWave) void w8a16_stream_kernel(RsArgs a
     }
 }
 
-// Launch plan from the shapes alone (the workspace query reproduces it). The kernel
-// serves wide projections (N >= kStMinRows: >= 384 wavefront tiles of 64 rows);
-// narrower ones keep the row-stream kernel, which measured as fast or faster there.
+// Launch plan from the shapes alone (the workspace query reproduces it).
+//  * Wide projections (N >= kStMinRows: >= 384 wavefront tiles of 64 rows), any M:
+//    each wavefront owns its rows over all of K (KS = 1).
+//  * Narrower projections at M <= 8: a workgroup's four wavefronts take the four K
+//    quarters of 16 rows (KS = 4), so that N / 16 workgroups cover the CUs; the
+//    activation chunk holds all four quarters (2 stages each).
+// Narrow projections at M > 8 keep the row-stream kernel: a 16-row workgroup would read
+// 2 M bytes of activations per weight byte.
 constexpr int64_t kStMinRows = 24576;
 struct StPlan {
   bool ok;
-  int mp, tw, g, d, split;
+  int mp, tw, g, d, ks, split;
   int64_t kps;
 };
 StPlan stream_plan(int64_t M, int64_t N, int64_t K, int64_t bx) {
   StPlan p{};
   const bool row_scale = bx >= K;
-  if (M < 2 || M > 32 || N < kStMinRows || K % kStK || K >= (int64_t(1) << 31) || (!row_scale && bx % 16)) return p;
+  if (M < 2 || M > 32 || N < 1 || K % kStK || K >= (int64_t(1) << 31) || (!row_scale && bx % 16)) return p;
   p.mp = M <= 4 ? 4 : (M <= 8 ? 8 : (M <= 16 ? 16 : 32));
-  // Up to 8 activation rows: one 16-row tile per wavefront, 32 KB of activation
-  // buffers, two workgroups per CU. Above: two tiles per wavefront (the activation
-  // bytes a workgroup reads are half its weight bytes at M = 32), 64 KB of activation
-  // buffers, one workgroup per CU.
-  p.tw = p.mp <= 8 ? 1 : 2;
-  p.g = (p.tw == 1 ? 32 : 64) / p.mp;
-  if (p.g > 8) p.g = 8;
-  while (p.g > 2 && K % (kStK * p.g)) p.g /= 2;
-  if (K % (kStK * p.g)) return StPlan{};
   p.d = 3;
   p.split = 1;
   p.kps = K;
-  p.ok = cdiv(N, 16 * kStWaves * p.tw) <= 0x7FFFFFFF;
+  if (N >= kStMinRows) {
+    // Up to 8 activation rows: one 16-row tile per wavefront, 32 KB of activation
+    // buffers, two workgroups per CU. Above: two tiles per wavefront (the activation
+    // bytes a workgroup reads are half its weight bytes at M = 32), 64 KB of activation
+    // buffers, one workgroup per CU.
+    p.ks = 1;
+    p.tw = p.mp <= 8 ? 1 : 2;
+    p.g = (p.tw == 1 ? 32 : 64) / p.mp;
+    if (p.g > 8) p.g = 8;
+    while (p.g > 2 && K % (kStK * p.g)) p.g /= 2;
+    if (K % (kStK * p.g)) return StPlan{};
+  } else if (p.mp <= 8 && N >= 512 && cdiv(N, 16) <= (p.mp == 4 ? 512 : 256)) {
+    // One round of resident workgroups: 80 KB of LDS at M <= 4 (two per CU), 112 KB at
+    // M <= 8 (one per CU); past it the row-stream kernel measured faster (qkv at M = 8:
+    // 384 workgroups, 13.1 against 9.9 us).
+    p.ks = 4;
+    p.tw = 1;
+    p.g = 2;
+    if (K % (4 * kStK * p.g)) return StPlan{};
+  } else {
+    return StPlan{};
+  }
+  p.ok = cdiv(N, 16 * p.tw * (kStWaves / p.ks)) <= 0x7FFFFFFF;
   return p;
 }
 size_t stream_workspace(const StPlan& p, int64_t M, int64_t N) {
   return p.ok && p.split > 1 ? (size_t)p.split * (size_t)M * (size_t)N * sizeof(float) : 0;
 }
 
-template <bool BF16, bool ROW_SCALE, int MP, int TW>
+template <bool BF16, bool ROW_SCALE, int MP, int TW, int KS>
 bool launch_stream_g(const StPlan& p, const RsArgs& a, hipStream_t st) {
-  const dim3 grid((unsigned)cdiv(a.N, 16 * kStWaves * TW), (unsigned)p.split), block(kStWaves * kWave);
-#define AYK_ST(G, D)                                                                                  \
-  if (p.g == G && p.d == D) {                                                                         \
-    hipLaunchKernelGGL((w8a16_stream_kernel<BF16, ROW_SCALE, MP, TW, G, D>), grid, block, 0, st, a); \
-    return true;                                                                                      \
+  const dim3 grid((unsigned)cdiv(a.N, 16 * TW * (kStWaves / KS)), (unsigned)p.split), block(kStWaves * kWave);
+#define AYK_ST(G, D)                                                                                      \
+  if (p.g == G && p.d == D) {                                                                             \
+    hipLaunchKernelGGL((w8a16_stream_kernel<BF16, ROW_SCALE, MP, TW, G, D, KS>), grid, block, 0, st, a); \
+    return true;                                                                                          \
   }
-  // LDS: 4 D TW 4 KB of weight rings + 2 MP 512 G bytes of activation chunks
-  if constexpr (64 / MP >= 8) { AYK_ST(8, 3) }
-  if constexpr (64 / MP >= 4) { AYK_ST(4, 3) }
+  // LDS: 4 D TW 4 KB of weight rings + 2 KS MP 512 G bytes of activation chunks
+  if constexpr (KS == 1 && 64 / MP >= 8) { AYK_ST(8, 3) }
+  if constexpr (KS == 1 && 64 / MP >= 4) { AYK_ST(4, 3) }
   AYK_ST(2, 3)
 #undef AYK_ST
   return false;
@@ -1255,15 +1310,22 @@ bool launch_stream_g(const StPlan& p, const RsArgs& a, hipStream_t st) {
 
 template <bool BF16, bool ROW_SCALE>
 bool launch_stream_kernel(const StPlan& p, const RsArgs& a, hipStream_t st) {
+  if (p.ks == 4) {
+    if (p.tw != 1) return false;
+    if (p.mp == 4) return launch_stream_g<BF16, ROW_SCALE, 4, 1, 4>(p, a, st);
+    if (p.mp == 8) return launch_stream_g<BF16, ROW_SCALE, 8, 1, 4>(p, a, st);
+    return false;
+  }
+  if (p.ks != 1) return false;
   switch (p.mp * 10 + p.tw) {
-    case 41: return launch_stream_g<BF16, ROW_SCALE, 4, 1>(p, a, st);
-    case 42: return launch_stream_g<BF16, ROW_SCALE, 4, 2>(p, a, st);
-    case 81: return launch_stream_g<BF16, ROW_SCALE, 8, 1>(p, a, st);
-    case 82: return launch_stream_g<BF16, ROW_SCALE, 8, 2>(p, a, st);
-    case 161: return launch_stream_g<BF16, ROW_SCALE, 16, 1>(p, a, st);
-    case 162: return launch_stream_g<BF16, ROW_SCALE, 16, 2>(p, a, st);
-    case 321: return launch_stream_g<BF16, ROW_SCALE, 32, 1>(p, a, st);
-    case 322: return launch_stream_g<BF16, ROW_SCALE, 32, 2>(p, a, st);
+    case 41: return launch_stream_g<BF16, ROW_SCALE, 4, 1, 1>(p, a, st);
+    case 42: return launch_stream_g<BF16, ROW_SCALE, 4, 2, 1>(p, a, st);
+    case 81: return launch_stream_g<BF16, ROW_SCALE, 8, 1, 1>(p, a, st);
+    case 82: return launch_stream_g<BF16, ROW_SCALE, 8, 2, 1>(p, a, st);
+    case 161: return launch_stream_g<BF16, ROW_SCALE, 16, 1, 1>(p, a, st);
+    case 162: return launch_stream_g<BF16, ROW_SCALE, 16, 2, 1>(p, a, st);
+    case 321: return launch_stream_g<BF16, ROW_SCALE, 32, 1, 1>(p, a, st);
+    case 322: return launch_stream_g<BF16, ROW_SCALE, 32, 2, 1>(p, a, st);
     default: return false;
   }
 }

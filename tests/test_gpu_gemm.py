@@ -517,7 +517,8 @@ def test_weight_only_gemm_decode_plans(gpu, m, n, k, case, xdt):
     assert_linear_close(y, ref, "weight_only_gemm decode plan")
 
 
-# Wide decode projections (N >= 24576) take the stream kernel: every staged activation
+# Wide decode projections (N >= 24576), and narrower ones at M <= 8 with a four-way K
+# split inside the workgroup, take the stream kernel: every staged activation
 # row count (4, 8, 16, 32), ragged N (not a multiple of 64, nor of 16), every scale
 # layout, fp16, K whose stage count leaves a remainder after the unrolled loop (3584:
 # 14 stages in rounds of 6) or runs the remainder only (512: 2 stages).
@@ -528,6 +529,10 @@ def test_weight_only_gemm_decode_plans(gpu, m, n, k, case, xdt):
     (32, 24576, 3584, "channel_e8m0", torch.bfloat16),
     (2, 28672, 512, "channel", torch.float16),
     (17, 24704, 2560, "block128", torch.bfloat16),
+    # narrower projections at M <= 8: four K quarters of 16 rows per workgroup
+    (3, 1000, 6144, "e8m0_32", torch.float16),
+    (7, 3000, 2048, "block128", torch.bfloat16),
+    (4, 8192, 14336, "channel", torch.bfloat16),
 ])
 def test_weight_only_gemm_stream(gpu, m, n, k, case, xdt):
     from ayaka.kernel.hip import fp8_weight_only_gemm
