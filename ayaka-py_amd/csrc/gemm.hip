@@ -24,6 +24,7 @@
 // 144 bytes so the 32 rows a wavefront reads at one K offset fall on distinct banks.
 #include "ayk_common.h"
 #include "gemm_block.h"
+#include "gemm_skinny.h"
 #include "gemm_tiles.h"
 #include "gemm_util.h"
 
@@ -1701,6 +1702,19 @@ Block256Args block256_args(const GemmArgs& g) {
   return b;
 }
 
+SkinnyFp8Args skinny_args(const GemmArgs& g, bool mx) {
+  SkinnyFp8Args k{};
+  k.mx = mx;
+  k.a = g.a; k.lda = g.lda; k.w = g.w; k.ldw = g.ldw;
+  k.M = g.M; k.N = g.N; k.K = g.K;
+  k.sa = g.sa; k.sa_vec = g.sa_vec; k.ld_sa = g.ld_sa;
+  k.sb = g.sb; k.sb_vec = g.sb_vec; k.ld_sb = g.ld_sb;
+  k.bias = g.bias; k.bias_dtype = g.bias_dtype;
+  k.out = g.out; k.out_dtype = g.out_dtype; k.ldo = g.ldo;
+  k.ws = g.ws; k.ws_bytes = g.ws_bytes;
+  return k;
+}
+
 template <int MODE>
 int launch_gemm(const GemmArgs& g, hipStream_t st, const char* op) {
   // The large-tile kernels need K % 64 == 0 (128 for MXFP8), fp32 scales, N % 4 == 0 and 16-byte
@@ -1730,6 +1744,14 @@ int launch_gemm(const GemmArgs& g, hipStream_t st, const char* op) {
                         (g.ldo * out_bytes) % 16 == 0 && aligned16(g.out) &&
                         (g.bias == nullptr || (reinterpret_cast<uintptr_t>(g.bias) & 15) == 0);
     if (big_ok) return launch_block_big(g, st, op);
+  }
+  // Decode batches (M <= 64) with fp32 or UE8M0 scales: the weight-streaming kernel
+  // (gemm_skinny.hip) where its shape and alignment rules hold.
+  if constexpr (MODE == MODE_SCALED || MODE == MODE_MX) {
+    if (g.M <= 64 && (MODE == MODE_MX || (g.sa_dtype == AYK_F32 && g.sb_dtype == AYK_F32))) {
+      const SkinnyFp8Args sk = skinny_args(g, MODE == MODE_MX);
+      if (skinny_fp8_supported(sk)) return skinny_fp8_launch(sk, st, op);
+    }
   }
   if (g.M <= 32) return launch_cfg<MODE, 128, 32, 4, 1>(g, st, op);
   if (g.M <= 64) return launch_cfg<MODE, 128, 64, 2, 2>(g, st, op);
@@ -1761,7 +1783,8 @@ size_t ayk_fp8_scaled_mm_workspace_bytes(int64_t M, int64_t N, int64_t K) {
   if (M < 1 || N < 1 || K < 1) return 0;
   const size_t split = scaled_split_workspace(M, N, K);
   const size_t tail = M >= kBigTile && N >= kBigTile ? tail_workspace(tail_plan(M, N, K, false)) : 0;
-  return split > tail ? split : tail;
+  const size_t skinny = skinny_fp8_workspace(M, N, K, false);
+  return split > tail ? (split > skinny ? split : skinny) : (tail > skinny ? tail : skinny);
 }
 
 int ayk_fp8_scaled_mm(const void* a, int64_t lda, const void* b, int64_t ldb, int64_t M, int64_t N,
@@ -1890,7 +1913,8 @@ size_t ayk_mxfp8_scaled_mm_workspace_bytes(int64_t M, int64_t N, int64_t K) {
   if (M < 1 || N < 1 || K < 1) return 0;
   const size_t split = scaled_split_workspace(M, N, K);
   const size_t tail = M >= kBigTile && N >= kBigTile ? tail_workspace(tail_plan(M, N, K, true)) : 0;
-  return split > tail ? split : tail;
+  const size_t skinny = skinny_fp8_workspace(M, N, K, true);
+  return split > tail ? (split > skinny ? split : skinny) : (tail > skinny ? tail : skinny);
 }
 
 int ayk_mxfp8_scaled_mm(const void* a, int64_t lda, const uint8_t* a_scale, int64_t ld_as,

@@ -1,0 +1,522 @@
+// FP8 x FP8 GEMM for decode batches, M <= 64 (fp8_scaled_mm rowwise / per-tensor and
+// mxfp8_scaled_mm), gfx950.
+//
+//   out[m, n] = sum_k a[m, k] w[n, k] * sa[m] * sb[n] (+ bias[n])          (fp32 scales)
+//   out[m, n] = sum_k a[m, k] 2^ea[m, k/32] w[n, k] 2^ew[n, k/32] (+ bias)   (UE8M0 codes)
+//
+// (python/ayaka/kernel/triton/gemm/fp8_gemm.py:246, fp8_mxfp8_gemm.py:163; oracle
+// reference/gemm.py:17-37, 73-92.) At these batch sizes the weight bytes bound the
+// work, so the kernel is a weight stream, the structure of the W8A16 decode stream
+// kernel: every wavefront streams its own 32 FN weight rows through a private LDS ring
+// of 3 stages, one 128-K "pair" per stage, filled by direct-to-LDS loads of 8 rows x
+// 128 contiguous bytes (nontemporal: read once), with no workgroup barrier per stage.
+// The activation rows are shared: the workgroup stages them into double-buffered LDS
+// chunks of G pairs, each wavefront loading its share with the chunk's first stage,
+// one barrier per chunk. With KS > 1 the KS wavefronts of a row group take the KS
+// parts of the K range and their sums meet in LDS at the end.
+//
+// MFMA v_mfma_scale_f32_32x32x64_f8f6f4 in the 256 x 256 pair kernel's arrangement:
+// the weight is operand A (a 32-row tile), the activations operand B (32 rows); for
+// step t of a pair, lane (r = lane % 32, h = lane / 32) holds K [64 t + 16 h, + 16) and
+// [64 t + 32 + 16 h, + 16) of its row, which puts the hardware's 32-K scale block b at
+// memory K [64 t + 32 b, + 32), i.e. MX group 2 t + b: lane half h passes byte 2 t + h
+// of its row's code dword for the pair. LDS row r holds logical 16-byte chunk c at
+// physical chunk c ^ ((r >> 1) & 7), so the 32 rows of a fragment read fall on distinct
+// banks. fp32 scales (and the bias) are applied in the epilogue; MX codes enter the
+// MFMA (the MX UE8M0 decode of the reference, code 0 as 2^-127, is the MFMA's).
+#include "gemm_skinny.h"
+
+#include <utility>
+
+#include "ayk_common.h"
+#include "gemm_util.h"
+
+namespace ayk {
+namespace {
+
+typedef int v8i __attribute__((ext_vector_type(8)));
+typedef int v4i __attribute__((ext_vector_type(4)));
+typedef float v16f __attribute__((ext_vector_type(16)));
+typedef uint32_t v4u __attribute__((ext_vector_type(4)));
+
+constexpr int kWaves = 4;
+constexpr int kPairK = 128;  // K bytes per stage
+constexpr int kDepth = 3;    // stages in a wavefront's ring
+constexpr int kCodeOne = 127;
+
+template <typename F, int... I>
+__device__ inline void static_for_impl(F&& f, std::integer_sequence<int, I...>) {
+  (f(std::integral_constant<int, I>{}), ...);
+}
+template <int N, typename F>
+__device__ inline void static_for(F&& f) {
+  static_for_impl(f, std::make_integer_sequence<int, N>{});
+}
+
+__device__ inline uint32_t lds_u32(const uint8_t* p) {
+  return (uint32_t)(uintptr_t)(const __attribute__((address_space(3))) uint8_t*)p;
+}
+__device__ inline void dma16_nt(const uint8_t* src, uint8_t* lds_dst) {
+  __builtin_amdgcn_global_load_lds(src, (__attribute__((address_space(3))) void*)lds_dst, 16, 0, 2);
+}
+__device__ inline void dma16(const uint8_t* src, uint8_t* lds_dst) {
+  __builtin_amdgcn_global_load_lds(src, (__attribute__((address_space(3))) void*)lds_dst, 16, 0, 0);
+}
+
+// All LDS reads of one step in one assembly statement ending with lgkmcnt(0): the
+// compiler cannot relate them to the direct loads in flight into other buffers (it would
+// otherwise wait for all of them first), and every result is final when it ends.
+template <int NB>
+__device__ inline void step_reads(v4u (&b)[NB], const uint32_t (&ab)[NB]);
+#define AYK_SR(o, i) "ds_read_b128 %" #o ", %" #i "\n\t"
+template <>
+__device__ inline void step_reads<4>(v4u (&b)[4], const uint32_t (&ab)[4]) {
+  asm volatile(AYK_SR(0, 4) AYK_SR(1, 5) AYK_SR(2, 6) AYK_SR(3, 7) "s_waitcnt lgkmcnt(0)"
+               : "=&v"(b[0]), "=&v"(b[1]), "=&v"(b[2]), "=&v"(b[3])
+               : "v"(ab[0]), "v"(ab[1]), "v"(ab[2]), "v"(ab[3])
+               : "memory");
+}
+template <>
+__device__ inline void step_reads<6>(v4u (&b)[6], const uint32_t (&ab)[6]) {
+  asm volatile(AYK_SR(0, 6) AYK_SR(1, 7) AYK_SR(2, 8) AYK_SR(3, 9) AYK_SR(4, 10) AYK_SR(5, 11) "s_waitcnt lgkmcnt(0)"
+               : "=&v"(b[0]), "=&v"(b[1]), "=&v"(b[2]), "=&v"(b[3]), "=&v"(b[4]), "=&v"(b[5])
+               : "v"(ab[0]), "v"(ab[1]), "v"(ab[2]), "v"(ab[3]), "v"(ab[4]), "v"(ab[5])
+               : "memory");
+}
+template <>
+__device__ inline void step_reads<8>(v4u (&b)[8], const uint32_t (&ab)[8]) {
+  asm volatile(AYK_SR(0, 8) AYK_SR(1, 9) AYK_SR(2, 10) AYK_SR(3, 11) AYK_SR(4, 12) AYK_SR(5, 13) AYK_SR(6, 14)
+               AYK_SR(7, 15) "s_waitcnt lgkmcnt(0)"
+               : "=&v"(b[0]), "=&v"(b[1]), "=&v"(b[2]), "=&v"(b[3]), "=&v"(b[4]), "=&v"(b[5]), "=&v"(b[6]), "=&v"(b[7])
+               : "v"(ab[0]), "v"(ab[1]), "v"(ab[2]), "v"(ab[3]), "v"(ab[4]), "v"(ab[5]), "v"(ab[6]), "v"(ab[7])
+               : "memory");
+}
+#undef AYK_SR
+
+// The code dwords of a stage (one per fragment row), likewise in one statement.
+template <int NC>
+__device__ inline void code_reads(uint32_t (&c)[NC], const uint32_t (&ac)[NC]);
+template <>
+__device__ inline void code_reads<2>(uint32_t (&c)[2], const uint32_t (&ac)[2]) {
+  asm volatile("ds_read_b32 %0, %2\n\tds_read_b32 %1, %3\n\ts_waitcnt lgkmcnt(0)"
+               : "=&v"(c[0]), "=&v"(c[1])
+               : "v"(ac[0]), "v"(ac[1])
+               : "memory");
+}
+template <>
+__device__ inline void code_reads<3>(uint32_t (&c)[3], const uint32_t (&ac)[3]) {
+  asm volatile("ds_read_b32 %0, %3\n\tds_read_b32 %1, %4\n\tds_read_b32 %2, %5\n\ts_waitcnt lgkmcnt(0)"
+               : "=&v"(c[0]), "=&v"(c[1]), "=&v"(c[2])
+               : "v"(ac[0]), "v"(ac[1]), "v"(ac[2])
+               : "memory");
+}
+template <>
+__device__ inline void code_reads<4>(uint32_t (&c)[4], const uint32_t (&ac)[4]) {
+  asm volatile(
+      "ds_read_b32 %0, %4\n\tds_read_b32 %1, %5\n\tds_read_b32 %2, %6\n\tds_read_b32 %3, %7\n\ts_waitcnt lgkmcnt(0)"
+      : "=&v"(c[0]), "=&v"(c[1]), "=&v"(c[2]), "=&v"(c[3])
+      : "v"(ac[0]), "v"(ac[1]), "v"(ac[2]), "v"(ac[3])
+      : "memory");
+}
+
+struct KArgs {
+  SkinnyFp8Args g;
+  int64_t kps;  // K per grid-y split
+};
+
+// FN 32-row weight tiles per wavefront, FM 32-row activation tiles (M <= 32 FM), KS K
+// parts per row group, G pairs per activation chunk.
+template <bool MX, int FN, int FM, int KS, int G>
+__global__ __launch_bounds__(kWaves * kWave) void fp8_skinny_kernel(KArgs ka) {
+  const SkinnyFp8Args& g = ka.g;
+  constexpr int D = kDepth;
+  constexpr int RW = 32 * FN;                // weight rows per wavefront
+  constexpr int RG = kWaves / KS;            // row groups per workgroup
+  constexpr int R = RG * RW;                 // weight rows per workgroup
+  constexpr int MP = 32 * FM;                // activation rows staged
+  constexpr int kWStage = RW * kPairK;       // bytes of a wavefront stage
+  constexpr int kWIns = kWStage / 1024;      // direct loads per wavefront stage
+  constexpr int kXRow = kPairK * G;          // bytes of one activation row of a chunk part
+  constexpr int kXPart = MP * kXRow;
+  constexpr int kXChunk = KS * kXPart;
+  constexpr int kXIns = kXChunk / (1024 * kWaves);  // activation loads per wavefront and chunk
+  constexpr int kCodeIns = MX ? (FN + FM + 1) / 2 : 0;  // code loads per stage (64 dwords each)
+  constexpr int kOpsW = kWIns + kCodeIns;
+  constexpr int U = G % D == 0 ? G : (D % G == 0 ? D : G * D);  // a multiple of G and D
+  static_assert(kXChunk % (1024 * kWaves) == 0, "whole activation loads per wavefront");
+  static_assert(D - 1 <= G, "an activation buffer is refilled only after a barrier past its last read");
+  constexpr auto wait_after = [](int u) {  // loads issued after stage s, before its wait
+    int n = 0;
+    for (int t = u + 1; t <= u + D - 2; ++t) n += kOpsW + (t % G == 0 ? kXIns : 0);
+    return n;
+  };
+  static_assert(wait_after(0) <= 63 && wait_after(G - 1) <= 63, "vmcnt range");
+
+  __shared__ __attribute__((aligned(1024))) uint8_t wring[kWaves * D * kWStage];
+  __shared__ __attribute__((aligned(1024))) uint8_t xbuf[2 * kXChunk];
+  __shared__ uint32_t cring[MX ? kWaves * D * kCodeIns * kWave : 1];
+  const int lane = threadIdx.x & (kWave - 1);
+  const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x / kWave);
+  const int frow = lane & 31, h = lane >> 5;
+  uint8_t* myring = wring + wave * D * kWStage;
+  const int part = wave / RG, rg = wave % RG;
+  const int64_t n_wave = (int64_t)blockIdx.x * R + rg * RW;
+  const int64_t kbeg = (int64_t)blockIdx.y * ka.kps;
+  const int64_t klen = g.K - kbeg < ka.kps ? g.K - kbeg : ka.kps;
+  const int64_t plen = klen / KS;  // whole chunks of G pairs (host plan)
+  const int64_t kpart = kbeg + part * plen;
+  const int ns = (int)(plen / kPairK);
+
+  // Weight loads: load j of a stage covers rows 8 j .. 8 j + 7 of the wavefront, lane L
+  // row 8 j + L / 8 at physical chunk L % 8; rows past N re-read row N - 1.
+  const uint8_t* wsrc[kWIns];
+#pragma unroll
+  for (int j = 0; j < kWIns; ++j) {
+    const int row = 8 * j + (lane >> 3);
+    const int64_t n = n_wave + row < g.N ? n_wave + row : g.N - 1;
+    wsrc[j] = g.w + n * g.ldw + kpart + 16 * ((lane & 7) ^ ((row >> 1) & 7));
+  }
+  // Activation loads: load j of wavefront w fills chunk bytes 1024 (w kXIns + j) ..:
+  // K part q, row m, pair segment sg and physical chunk p of that row; rows past M
+  // repeat row M - 1.
+  const uint8_t* xsrc[kXIns];
+  uint32_t xdst[kXIns];
+#pragma unroll
+  for (int j = 0; j < kXIns; ++j) {
+    const int byte = 1024 * (wave * kXIns + j) + 16 * lane;
+    const int q = byte / kXPart;
+    const int m = (byte % kXPart) / kXRow;
+    const int within = byte % kXRow;
+    const int sg = within / kPairK, p = (within % kPairK) / 16;
+    const int64_t mm = m < g.M ? m : g.M - 1;
+    xsrc[j] = g.a + mm * g.lda + kbeg + q * plen + sg * kPairK + 16 * (p ^ ((m >> 1) & 7));
+    xdst[j] = __builtin_amdgcn_readfirstlane(1024 * (wave * kXIns + j));
+  }
+  // MX code dwords of a stage, through LDS like the operands (a register load would be
+  // waited for with every direct load before it): entry e = 64 j + lane of code load j
+  // is weight row e of the wavefront for e < 32 FN, then activation row e - 32 FN;
+  // entries past the last repeat it. Rows past N or M repeat the last row.
+  const uint8_t* csrc[MX ? kCodeIns : 1];
+  uint32_t* mycodes = cring + wave * D * kCodeIns * kWave;
+  if constexpr (MX) {
+#pragma unroll
+    for (int j = 0; j < kCodeIns; ++j) {
+      int e = kWave * j + lane;
+      e = e < 32 * (FN + FM) ? e : 32 * (FN + FM) - 1;
+      if (e < 32 * FN) {
+        const int64_t n = n_wave + e < g.N ? n_wave + e : g.N - 1;
+        csrc[j] = static_cast<const uint8_t*>(g.sb) + n * g.ld_sb + kpart / 32;
+      } else {
+        const int64_t m = e - 32 * FN < g.M ? e - 32 * FN : g.M - 1;
+        csrc[j] = static_cast<const uint8_t*>(g.sa) + m * g.ld_sa + kpart / 32;
+      }
+    }
+  }
+
+  // Stage t (clamped to the last; a clamped stage only rewrites data no later stage
+  // reads, or the same data) into slot t % D; the chunk's activations with its first
+  // stage (xl: t % G == 0, known at compile time at every call site).
+  auto issue = [&](int slot, int t, bool xl) {
+    const int tc = t < ns ? t : ns - 1;
+    const int64_t k = (int64_t)tc * kPairK;
+#pragma unroll
+    for (int j = 0; j < kWIns; ++j) dma16_nt(wsrc[j] + k, myring + slot * kWStage + 1024 * j);
+    if constexpr (MX) {
+#pragma unroll
+      for (int j = 0; j < kCodeIns; ++j)
+        __builtin_amdgcn_global_load_lds(csrc[j] + k / 32,
+                                         (__attribute__((address_space(3))) void*)(mycodes + (slot * kCodeIns + j) * kWave),
+                                         4, 0, 0);
+    }
+    if (xl) {
+      const int c = tc / G;
+      uint8_t* xb = xbuf + (c & 1) * kXChunk;
+#pragma unroll
+      for (int j = 0; j < kXIns; ++j) dma16(xsrc[j] + (int64_t)c * kXRow, xb + xdst[j]);
+    }
+  };
+
+  v16f acc[FN][FM];
+#pragma unroll
+  for (int i = 0; i < FN; ++i)
+#pragma unroll
+    for (int j = 0; j < FM; ++j)
+#pragma unroll
+      for (int r = 0; r < 16; ++r) acc[i][j][r] = 0.0f;
+  const int fsw = (frow >> 1) & 7;
+  auto compute = [&](int slot, int s) {
+    const uint32_t wbase = lds_u32(myring + slot * kWStage);
+    const uint32_t xbase = lds_u32(xbuf + ((s / G) & 1) * kXChunk + part * kXPart) + (uint32_t)((s % G) * kPairK);
+    uint32_t wc[FN], xc[FM];
+    if constexpr (MX) {
+      const uint32_t cb = lds_u32(reinterpret_cast<const uint8_t*>(mycodes + slot * kCodeIns * kWave)) + 4 * frow;
+      uint32_t ca[FN + FM];
+#pragma unroll
+      for (int i = 0; i < FN + FM; ++i) ca[i] = cb + 128 * i;
+      uint32_t cv[FN + FM];
+      code_reads<FN + FM>(cv, ca);
+#pragma unroll
+      for (int i = 0; i < FN; ++i) wc[i] = cv[i];
+#pragma unroll
+      for (int j = 0; j < FM; ++j) xc[j] = cv[FN + j];
+    }
+#pragma unroll
+    for (int t = 0; t < 2; ++t) {
+      constexpr int NB = 2 * (FN + FM);
+      uint32_t ab[NB];
+      v4u v[NB];
+#pragma unroll
+      for (int i = 0; i < FN; ++i) {
+        const uint32_t row = wbase + (32 * i + frow) * kPairK;
+        ab[2 * i] = row + (((4 * t + h) ^ fsw) << 4);
+        ab[2 * i + 1] = row + (((4 * t + 2 + h) ^ fsw) << 4);
+      }
+#pragma unroll
+      for (int j = 0; j < FM; ++j) {
+        const uint32_t row = xbase + (32 * j + frow) * kXRow;
+        ab[2 * FN + 2 * j] = row + (((4 * t + h) ^ fsw) << 4);
+        ab[2 * FN + 2 * j + 1] = row + (((4 * t + 2 + h) ^ fsw) << 4);
+      }
+      step_reads<NB>(v, ab);
+      const int sh = 8 * (2 * t + h);
+#pragma unroll
+      for (int i = 0; i < FN; ++i) {
+        const v8i wf = __builtin_shufflevector(__builtin_bit_cast(v4i, v[2 * i]), __builtin_bit_cast(v4i, v[2 * i + 1]), 0, 1, 2, 3, 4, 5, 6, 7);
+        const int cw = MX ? (int)(wc[i] >> sh) : kCodeOne;
+#pragma unroll
+        for (int j = 0; j < FM; ++j) {
+          const v8i xf = __builtin_shufflevector(__builtin_bit_cast(v4i, v[2 * FN + 2 * j]),
+                                                 __builtin_bit_cast(v4i, v[2 * FN + 2 * j + 1]), 0, 1, 2, 3, 4, 5, 6, 7);
+          const int cx = MX ? (int)(xc[j] >> sh) : kCodeOne;
+          acc[i][j] = __builtin_amdgcn_mfma_scale_f32_32x32x64_f8f6f4(wf, xf, acc[i][j], 0, 0, 0, cw, 0, cx);
+        }
+      }
+    }
+  };
+
+#pragma unroll
+  for (int d = 0; d < D - 1; ++d) issue(d, d, d % G == 0);
+  // Step s: wait for stage s (its activation chunk too), at a chunk start a barrier,
+  // refill slot (s - 1) % D with stage s + D - 1, compute stage s. The main loop runs
+  // whole rounds of U steps with no exit inside; the remainder runs after it.
+  auto step = [&](auto uc, int s) {
+    constexpr int u = decltype(uc)::value;
+    wait_vmcnt<wait_after(u % G)>();
+    if (u % G == 0) __builtin_amdgcn_s_barrier();
+    issue((u + D - 1) % D, s + D - 1, (u + D - 1) % G == 0);
+    compute(u % D, s);
+  };
+  int s0 = 0;
+  for (; s0 + U <= ns; s0 += U) {
+    static_for<U>([&](auto uc) { step(uc, s0 + decltype(uc)::value); });
+  }
+  static_for<U - 1>([&](auto uc) {
+    if (s0 + decltype(uc)::value < ns) step(uc, s0 + decltype(uc)::value);  // workgroup-uniform
+  });
+  wait_vmcnt<0>();  // no direct load may still be writing LDS when the workgroup ends
+
+  if constexpr (KS > 1) {
+    // The K parts of a row group meet in LDS in part order (the rings are free once
+    // every wavefront is past its last stage).
+    constexpr int kSlots = FN * FM * 16;
+    static_assert(kWaves * kSlots * kWave * 4 <= kWaves * D * kWStage, "the sums fit the rings");
+    float* red = reinterpret_cast<float*>(wring);
+    __syncthreads();
+#pragma unroll
+    for (int i = 0; i < FN; ++i)
+#pragma unroll
+      for (int j = 0; j < FM; ++j)
+#pragma unroll
+        for (int r = 0; r < 16; ++r) red[(wave * kSlots + (i * FM + j) * 16 + r) * kWave + lane] = acc[i][j][r];
+    __syncthreads();
+    if (part != 0) return;
+#pragma unroll
+    for (int i = 0; i < FN; ++i)
+#pragma unroll
+      for (int j = 0; j < FM; ++j)
+#pragma unroll
+        for (int r = 0; r < 16; ++r) {
+          float v = 0.0f;
+#pragma unroll
+          for (int qq = 0; qq < KS; ++qq) v += red[((qq * RG + rg) * kSlots + (i * FM + j) * 16 + r) * kWave + lane];
+          acc[i][j][r] = v;
+        }
+  }
+
+  // Epilogue. acc[i][j][4 grp + qq] = D[n = n_wave + 32 i + 8 grp + 4 h + qq][m = 32 j + frow].
+  const bool split = gridDim.y > 1;
+  const float* sa = static_cast<const float*>(g.sa);
+  const float* sb = static_cast<const float*>(g.sb);
+  const int eb = g.out_dtype == AYK_F32 ? 4 : 2;
+#pragma unroll
+  for (int j = 0; j < FM; ++j) {
+    const int64_t m = 32 * j + frow;
+    if (m >= g.M) continue;
+    const float sam = MX ? 1.0f : sa[g.sa_vec ? m : 0];
+#pragma unroll
+    for (int i = 0; i < FN; ++i)
+#pragma unroll
+      for (int grp = 0; grp < 4; ++grp) {
+        const int64_t n0 = n_wave + 32 * i + 8 * grp + 4 * h;
+        float v[4];
+#pragma unroll
+        for (int qq = 0; qq < 4; ++qq) {
+          const int64_t n = n0 + qq < g.N ? n0 + qq : g.N - 1;
+          float y = acc[i][j][4 * grp + qq];
+          if constexpr (!MX) y = (y * sam) * sb[g.sb_vec ? n : 0];
+          if (!split && g.bias) y += load_f32(g.bias, g.bias_dtype, n);
+          v[qq] = y;
+        }
+        if (split) {
+          float* pr = ka.g.ws + ((int64_t)blockIdx.y * g.M + m) * g.N;
+#pragma unroll
+          for (int qq = 0; qq < 4; ++qq)
+            if (n0 + qq < g.N) pr[n0 + qq] = v[qq];
+        } else if (n0 + 3 < g.N && eb == 2 &&
+                   (reinterpret_cast<uintptr_t>(static_cast<uint16_t*>(g.out) + m * g.ldo + n0) & 7) == 0) {
+          uint32_t pk[2];
+#pragma unroll
+          for (int qq = 0; qq < 2; ++qq) {
+            if (g.out_dtype == AYK_BF16) pk[qq] = pack_bf16x2(v[2 * qq], v[2 * qq + 1]);
+            else pk[qq] = (uint32_t)f32_to_f16_bits(v[2 * qq]) | ((uint32_t)f32_to_f16_bits(v[2 * qq + 1]) << 16);
+          }
+          *reinterpret_cast<uint2*>(static_cast<uint16_t*>(g.out) + m * g.ldo + n0) = make_uint2(pk[0], pk[1]);
+        } else {
+#pragma unroll
+          for (int qq = 0; qq < 4; ++qq)
+            if (n0 + qq < g.N) store_f32(g.out, g.out_dtype, m * g.ldo + n0 + qq, v[qq]);
+        }
+      }
+  }
+}
+
+// Fixed-order sum of the grid-y partials, bias, one rounding.
+__global__ __launch_bounds__(256) void skinny_reduce(const float* __restrict__ part, int64_t M, int64_t N, int split,
+                                                    const void* __restrict__ bias, int bias_dtype, void* __restrict__ out,
+                                                    int out_dtype, int64_t ldo) {
+  const int64_t i = (int64_t)blockIdx.x * 256 + threadIdx.x;
+  if (i >= M * N) return;
+  const int64_t m = i / N, n = i - m * N;
+  float v = 0.0f;
+  for (int s = 0; s < split; ++s) v += part[(int64_t)s * M * N + i];
+  if (bias) v += load_f32(bias, bias_dtype, n);
+  store_f32(out, out_dtype, m * ldo + n, v);
+}
+
+// Launch plan from the shape alone (the workspace query reproduces it). Rows per
+// workgroup R = 32 FN (4 / KS) from the first of (FN, KS) = (2, 1), (1, 1), (2, 2),
+// (2, 4), (1, 4) that gives >= 192 workgroups while the activation bytes a workgroup
+// reads stay within its weight bytes (R >= 32 FM); short of that, the last admissible
+// one and a grid-y K split up to one round of 256 workgroups. LDS: 4 x 3 x 4 KB FN of
+// rings + 2 KS 32 FM 128 G of activation chunks <= 160 KB.
+struct SkPlan {
+  bool ok;
+  int fn, fm, ks, g, split;
+  int64_t kps;
+};
+constexpr int64_t skinny_lds(int fn, int fm, int ks, int g, bool mx) {
+  return (int64_t)kWaves * kDepth * 4096 * fn + 2LL * ks * 32 * fm * kPairK * g +
+         (mx ? (int64_t)kWaves * kDepth * ((fn + fm + 1) / 2) * kWave * 4 : 0);
+}
+SkPlan skinny_plan(int64_t M, int64_t N, int64_t K, bool mx) {
+  SkPlan p{};
+  if (M < 1 || M > 64 || N < 1 || K % 256 || K >= ((int64_t)1 << 31)) return p;
+  p.fm = M <= 32 ? 1 : 2;
+  const int cand[5][2] = {{2, 1}, {1, 1}, {2, 2}, {2, 4}, {1, 4}};
+  int pick = -1;
+  for (int c = 0; c < 5; ++c) {
+    const int fn = cand[c][0], ks = cand[c][1];
+    const int r = 32 * fn * (kWaves / ks);
+    if (r < 32 * p.fm || K % (ks * kPairK * 2) || skinny_lds(fn, p.fm, ks, 2, mx) > 160 * 1024) continue;
+    pick = c;
+    if (cdiv(N, r) >= 192) break;
+  }
+  if (pick < 0) return p;
+  p.fn = cand[pick][0];
+  p.ks = cand[pick][1];
+  const int64_t wgs = cdiv(N, 32 * p.fn * (kWaves / p.ks));
+  // Activation chunk: 4 pairs per part where both buffers fit 32 KB and K allows, else 2.
+  p.g = p.ks * p.fm == 1 && K % (4 * kPairK) == 0 && skinny_lds(p.fn, p.fm, p.ks, 4, mx) <= 160 * 1024 ? 4 : 2;
+  const int64_t gran = (int64_t)p.ks * kPairK * p.g;  // K of one chunk over all parts
+  int64_t split = 1;
+  while (wgs * split * 2 <= 256 && K % (gran * split * 2) == 0 && K / (split * 2) >= 2048) split *= 2;
+  p.split = (int)split;
+  p.kps = K / split;
+  p.ok = wgs <= 0x7FFFFFFF;
+  return p;
+}
+
+template <bool MX, int FN, int FM, int KS>
+bool launch_g(const SkPlan& p, const KArgs& ka, hipStream_t st) {
+  const dim3 grid((unsigned)cdiv(ka.g.N, 32 * FN * (kWaves / KS)), (unsigned)p.split), block(kWaves * kWave);
+  if constexpr (skinny_lds(FN, FM, KS, 2, MX) <= 160 * 1024) {
+    if (p.g == 2) {
+      hipLaunchKernelGGL((fp8_skinny_kernel<MX, FN, FM, KS, 2>), grid, block, 0, st, ka);
+      return true;
+    }
+  }
+  if constexpr (KS * FM == 1 && skinny_lds(FN, FM, KS, 4, MX) <= 160 * 1024) {
+    if (p.g == 4) {
+      hipLaunchKernelGGL((fp8_skinny_kernel<MX, FN, FM, KS, 4>), grid, block, 0, st, ka);
+      return true;
+    }
+  }
+  return false;
+}
+
+template <bool MX>
+bool launch_mx(const SkPlan& p, const KArgs& ka, hipStream_t st) {
+  const int key = p.fn * 100 + p.fm * 10 + p.ks;
+  switch (key) {
+    case 211: return launch_g<MX, 2, 1, 1>(p, ka, st);
+    case 221: return launch_g<MX, 2, 2, 1>(p, ka, st);
+    case 111: return launch_g<MX, 1, 1, 1>(p, ka, st);
+    case 121: return launch_g<MX, 1, 2, 1>(p, ka, st);
+    case 212: return launch_g<MX, 2, 1, 2>(p, ka, st);
+    case 222: return launch_g<MX, 2, 2, 2>(p, ka, st);
+    case 214: return launch_g<MX, 2, 1, 4>(p, ka, st);
+    case 114: return launch_g<MX, 1, 1, 4>(p, ka, st);
+    default: return false;
+  }
+}
+
+}  // namespace
+
+bool skinny_fp8_supported(const SkinnyFp8Args& g) {
+  const SkPlan p = skinny_plan(g.M, g.N, g.K, g.mx != 0);
+  if (!p.ok) return false;
+  if (g.lda % 16 || g.ldw % 16 || !aligned16(g.a) || !aligned16(g.w)) return false;
+  if (g.mx) {
+    // code dwords of one 128-K pair are 4-byte aligned loads
+    if ((reinterpret_cast<uintptr_t>(g.sa) & 3) || (reinterpret_cast<uintptr_t>(g.sb) & 3) || g.ld_sa % 4 || g.ld_sb % 4)
+      return false;
+  }
+  return g.out_dtype == AYK_F32 || g.out_dtype == AYK_BF16 || g.out_dtype == AYK_F16;
+}
+
+size_t skinny_fp8_workspace(int64_t M, int64_t N, int64_t K, bool mx) {
+  const SkPlan p = skinny_plan(M, N, K, mx);
+  return p.ok && p.split > 1 ? (size_t)p.split * (size_t)M * (size_t)N * sizeof(float) : 0;
+}
+
+int skinny_fp8_launch(const SkinnyFp8Args& g, hipStream_t st, const char* op) {
+  const SkPlan p = skinny_plan(g.M, g.N, g.K, g.mx != 0);
+  if (!p.ok) return fail(AYK_EINVAL, "%s: no decode-batch plan for this shape", op);
+  if (p.split > 1) {
+    const size_t need = (size_t)p.split * (size_t)g.M * (size_t)g.N * sizeof(float);
+    if (g.ws == nullptr || g.ws_bytes < need)
+      return fail(AYK_EWORKSPACE, "%s: workspace of %zu bytes required, %zu given", op, need, g.ws_bytes);
+  }
+  KArgs ka{g, p.kps};
+  const bool launched = g.mx ? launch_mx<true>(p, ka, st) : launch_mx<false>(p, ka, st);
+  if (!launched) return fail(AYK_EINVAL, "%s: no decode-batch kernel for this plan", op);
+  if (int rc = check_launch(op)) return rc;
+  if (p.split > 1) {
+    hipLaunchKernelGGL(skinny_reduce, dim3((unsigned)cdiv(g.M * g.N, 256)), dim3(256), 0, st, g.ws, g.M, g.N, p.split,
+                       g.bias, g.bias_dtype, g.out, g.out_dtype, g.ldo);
+    return check_launch(op);
+  }
+  return AYK_OK;
+}
+
+}  // namespace ayk

@@ -164,6 +164,59 @@ def test_mxfp8_scaled_mm_split_k(gpu, m, n, k):
     assert_linear_close(y, ref, "mxfp8_scaled_mm split-K")
 
 
+# Decode batches (M <= 64, K % 256 == 0): the weight-streaming kernel. Each shape picks
+# a different plan: rows per wavefront (32 or 64), activation tiles (M <= 32 or <= 64),
+# K parts per row group (1, 2, 4), activation chunk of 2 or 4 pairs, grid K split.
+SKINNY_MNK = [
+    (2, 3000, 2048),     # 32 rows, 4 K parts, ragged N
+    (8, 24576, 2048),    # 32 rows, chunks of 4 pairs, one round of workgroups
+    (17, 5000, 1280),    # K % 512 != 0: 2-pair chunks only
+    (33, 1000, 4096),    # two activation tiles, 2 K parts, grid split 2
+    (48, 57344, 1024),   # 64 rows per wavefront, two activation tiles
+    (64, 1302, 8192),    # N % 4 != 0 rows: element stores, grid split
+    (1, 4096, 4096),     # a single row
+]
+
+
+@pytest.mark.parametrize("m,n,k", SKINNY_MNK)
+@pytest.mark.parametrize("rowwise,out_dtype", [(True, torch.bfloat16), (False, torch.float16), (True, torch.float32)])
+def test_fp8_scaled_mm_decode_batch(gpu, m, n, k, rowwise, out_dtype):
+    from ayaka.kernel.hip import fp8_scaled_mm
+
+    _say(f"fp8_scaled_mm decode batch m={m} n={n} k={k} rowwise={rowwise} out={out_dtype}")
+    a = _fp8((m, k), seed=m + 61, scale=40)
+    w = _fp8((n, k), seed=n + 62, scale=40)
+    sa = (torch.rand(m, generator=_gen(63)) * 0.01 + 1e-3) if rowwise else torch.tensor(0.004)
+    sb = (torch.rand(n, generator=_gen(64)) * 0.01 + 1e-3) if rowwise else torch.tensor(0.002)
+    bias = (torch.randn(n, generator=_gen(65)) * 10).to(torch.bfloat16)
+    ref = ora.fp8_scaled_mm(a, w, sa, sb, bias)
+    buf = torch.full((m, n + 6), 7.0, dtype=out_dtype, device=gpu)  # row stride n + 6
+    out = buf[:, :n]
+    fp8_scaled_mm(a.to(gpu), w.to(gpu).t(), sa.to(gpu), sb.to(gpu), bias.to(gpu), out=out)
+    assert_linear_close(out, ref, "fp8_scaled_mm decode batch")
+    assert torch.all(buf[:, n:].float() == 7.0), "wrote past the output columns"
+
+
+@pytest.mark.parametrize("m,n,k", [(2, 520, 2048), (40, 1000, 3072), (9, 20000, 1024), (64, 4100, 8192),
+                                   (64, 2048, 28672), (30, 57344, 512)])
+def test_mxfp8_scaled_mm_decode_batch(gpu, m, n, k):
+    """MXFP8 decode batches: the UE8M0 code dwords of each 128-K pair staged with the
+    operands; K parts and grid splits start their codes at their own K offset."""
+    from ayaka.kernel.hip import mxfp8_scaled_mm
+
+    _say(f"mxfp8_scaled_mm decode batch m={m} n={n} k={k}")
+    torch.manual_seed(m + n + k + 3)
+    x = torch.distributions.StudentT(3.0).sample((m, k))
+    wf = torch.randn(n, k, generator=_gen(66))
+    qa, ca = ora.per_token_group_quant_mxfp8(x, 32)
+    qw, cw = ora.per_token_group_quant_mxfp8(wf, 32)
+    bias = (torch.randn(n, generator=_gen(67)) * 10).to(torch.bfloat16)
+    ref = ora.mxfp8_scaled_mm(qa, ca, qw, cw, bias)
+    y = mxfp8_scaled_mm(qa.to(gpu), ca.to(gpu), qw.to(gpu), cw.to(gpu), bias.to(gpu),
+                        out=torch.empty(m, n, dtype=torch.bfloat16, device=gpu))
+    assert_linear_close(y, ref, "mxfp8_scaled_mm decode batch")
+
+
 # 276 tiles of 256 x 256: one whole round, then a last round of 20 tiles that the pair
 # kernel splits over K (three 512-K pieces each) into the workspace, ragged M and N.
 TAIL_MNK = (1300, 11712, 1536)
