@@ -1702,9 +1702,9 @@ Block256Args block256_args(const GemmArgs& g) {
   return b;
 }
 
-SkinnyFp8Args skinny_args(const GemmArgs& g, bool mx) {
+SkinnyFp8Args skinny_args(const GemmArgs& g, int mode) {
   SkinnyFp8Args k{};
-  k.mx = mx;
+  k.mode = mode;
   k.a = g.a; k.lda = g.lda; k.w = g.w; k.ldw = g.ldw;
   k.M = g.M; k.N = g.N; k.K = g.K;
   k.sa = g.sa; k.sa_vec = g.sa_vec; k.ld_sa = g.ld_sa;
@@ -1712,6 +1712,10 @@ SkinnyFp8Args skinny_args(const GemmArgs& g, bool mx) {
   k.bias = g.bias; k.bias_dtype = g.bias_dtype;
   k.out = g.out; k.out_dtype = g.out_dtype; k.ldo = g.ldo;
   k.ws = g.ws; k.ws_bytes = g.ws_bytes;
+  if (mode == 2) {  // block-128 tables: default row strides as the block kernels
+    k.ld_sa = g.ld_sa > 0 ? g.ld_sa : g.K / 128;
+    k.ld_sb = g.ld_sb > 0 ? g.ld_sb : cdiv(g.K, 128);
+  }
   return k;
 }
 
@@ -1747,9 +1751,9 @@ int launch_gemm(const GemmArgs& g, hipStream_t st, const char* op) {
   }
   // Decode batches (M <= 64) with fp32 or UE8M0 scales: the weight-streaming kernel
   // (gemm_skinny.hip) where its shape and alignment rules hold.
-  if constexpr (MODE == MODE_SCALED || MODE == MODE_MX) {
+  if constexpr (MODE == MODE_SCALED || MODE == MODE_MX || MODE == MODE_BLOCK) {
     if (g.M <= 64 && (MODE == MODE_MX || (g.sa_dtype == AYK_F32 && g.sb_dtype == AYK_F32))) {
-      const SkinnyFp8Args sk = skinny_args(g, MODE == MODE_MX);
+      const SkinnyFp8Args sk = skinny_args(g, MODE == MODE_MX ? 1 : (MODE == MODE_BLOCK ? 2 : 0));
       if (skinny_fp8_supported(sk)) return skinny_fp8_launch(sk, st, op);
     }
   }
@@ -1783,7 +1787,7 @@ size_t ayk_fp8_scaled_mm_workspace_bytes(int64_t M, int64_t N, int64_t K) {
   if (M < 1 || N < 1 || K < 1) return 0;
   const size_t split = scaled_split_workspace(M, N, K);
   const size_t tail = M >= kBigTile && N >= kBigTile ? tail_workspace(tail_plan(M, N, K, false)) : 0;
-  const size_t skinny = skinny_fp8_workspace(M, N, K, false);
+  const size_t skinny = skinny_fp8_workspace(M, N, K, 0);
   return split > tail ? (split > skinny ? split : skinny) : (tail > skinny ? tail : skinny);
 }
 
@@ -1841,7 +1845,9 @@ int ayk_int8_scaled_mm(const void* a, int64_t lda, const void* b, int64_t ldb, i
 
 size_t ayk_fp8_blockwise_mm_workspace_bytes(int64_t M, int64_t N, int64_t K) {
   if (M < 1 || N < 1 || K < 1 || K % 128) return 0;
-  return block_split_workspace(M, N, K);
+  const size_t split = block_split_workspace(M, N, K);
+  const size_t skinny = skinny_fp8_workspace(M, N, K, 2);
+  return split > skinny ? split : skinny;
 }
 
 int ayk_fp8_blockwise_mm(const void* a, int64_t lda, const void* b, int64_t ldb, int64_t M,
@@ -1913,7 +1919,7 @@ size_t ayk_mxfp8_scaled_mm_workspace_bytes(int64_t M, int64_t N, int64_t K) {
   if (M < 1 || N < 1 || K < 1) return 0;
   const size_t split = scaled_split_workspace(M, N, K);
   const size_t tail = M >= kBigTile && N >= kBigTile ? tail_workspace(tail_plan(M, N, K, true)) : 0;
-  const size_t skinny = skinny_fp8_workspace(M, N, K, true);
+  const size_t skinny = skinny_fp8_workspace(M, N, K, 1);
   return split > tail ? (split > skinny ? split : skinny) : (tail > skinny ? tail : skinny);
 }
 

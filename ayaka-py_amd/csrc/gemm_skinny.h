@@ -10,7 +10,9 @@
 namespace ayk {
 
 struct SkinnyFp8Args {
-  int mx;            // 0: fp32 per-row / per-tensor scales; 1: UE8M0 codes per 32 K
+  int mode;          // 0: fp32 per-row / per-tensor scales; 1: UE8M0 codes per 32 K;
+                     // 2: fp32 block-128 scales (sa [M, ld_sa] or, with sa_vec, [KB, M];
+                     //    sb [ceil(N / 128), ld_sb])
   const uint8_t* a;  // [M, K] e4m3, row stride lda
   int64_t lda;
   const uint8_t* w;  // [N, K] e4m3, row stride ldw
@@ -34,7 +36,7 @@ struct SkinnyFp8Args {
 // Whether the kernel takes this problem (shape, alignment and scale-layout rules).
 bool skinny_fp8_supported(const SkinnyFp8Args& g);
 // Bytes of K-split partials a launch of this shape needs (0: none); shape only.
-size_t skinny_fp8_workspace(int64_t M, int64_t N, int64_t K, bool mx);
+size_t skinny_fp8_workspace(int64_t M, int64_t N, int64_t K, int mode);
 // Launch (the kernel and, with a K split, the fixed-order reduce). Returns an ayk_status.
 int skinny_fp8_launch(const SkinnyFp8Args& g, hipStream_t st, const char* op);
 

@@ -1,11 +1,12 @@
-// FP8 x FP8 GEMM for decode batches, M <= 64 (fp8_scaled_mm rowwise / per-tensor and
-// mxfp8_scaled_mm), gfx950.
+// FP8 x FP8 GEMM for decode batches, M <= 64 (fp8_scaled_mm rowwise / per-tensor,
+// mxfp8_scaled_mm and fp8_blockwise_mm), gfx950.
 //
 //   out[m, n] = sum_k a[m, k] w[n, k] * sa[m] * sb[n] (+ bias[n])          (fp32 scales)
 //   out[m, n] = sum_k a[m, k] 2^ea[m, k/32] w[n, k] 2^ew[n, k/32] (+ bias)   (UE8M0 codes)
+//   out[m, n] = sum_kb sa[m, kb] sb[n/128, kb] sum_{k in kb} a[m, k] w[n, k] (+ bias)  (block-128)
 //
-// (python/ayaka/kernel/triton/gemm/fp8_gemm.py:246, fp8_mxfp8_gemm.py:163; oracle
-// reference/gemm.py:17-37, 73-92.) At these batch sizes the weight bytes bound the
+// (python/ayaka/kernel/triton/gemm/fp8_gemm.py:127-204, 246, fp8_mxfp8_gemm.py:163;
+// oracle reference/gemm.py:17-92.) At these batch sizes the weight bytes bound the
 // work, so the kernel is a weight stream, the structure of the W8A16 decode stream
 // kernel: every wavefront streams its own 32 FN weight rows through a private LDS ring
 // of 3 stages, one 128-K "pair" per stage, filled by direct-to-LDS loads of 8 rows x
@@ -43,6 +44,16 @@ constexpr int kWaves = 4;
 constexpr int kPairK = 128;  // K bytes per stage
 constexpr int kDepth = 3;    // stages in a wavefront's ring
 constexpr int kCodeOne = 127;
+
+// Scale modes: fp32 per-row / per-tensor scales in the epilogue, UE8M0 codes inside the
+// MFMA, or block-128 fp32 scales folded after every 128-K stage.
+constexpr int kSmScaled = 0, kSmMx = 1, kSmBlock = 2;
+// Scale loads per stage (64 dwords each, through LDS): MX, one code dword per weight and
+// activation row; block-128, one activation scale per row plus the wavefront's weight
+// scale (its rows lie in one 128-row block).
+constexpr int scale_ins(int sm, int fn, int fm) {
+  return sm == kSmMx ? (fn + fm + 1) / 2 : (sm == kSmBlock ? (32 * fm + 64) / 64 : 0);
+}
 
 template <typename F, int... I>
 __device__ inline void static_for_impl(F&& f, std::integer_sequence<int, I...>) {
@@ -124,11 +135,63 @@ struct KArgs {
   int64_t kps;  // K per grid-y split
 };
 
+// Epilogue of both forms: scales (fp32 mode), bias, output type, or the grid-y partials.
+// acc[i][j][4 grp + qq] = D[n = n_wave + 32 i + 8 grp + 4 h + qq][m = 32 j + frow].
+template <int SM, int FN, int FM>
+__device__ inline void store_tiles(const KArgs& ka, const v16f (&acc)[FN][FM], int64_t n_wave, int frow, int h) {
+  const SkinnyFp8Args& g = ka.g;
+  const bool split = gridDim.y > 1;
+  const float* sa = static_cast<const float*>(g.sa);
+  const float* sb = static_cast<const float*>(g.sb);
+  const int eb = g.out_dtype == AYK_F32 ? 4 : 2;
+#pragma unroll
+  for (int j = 0; j < FM; ++j) {
+    const int64_t m = 32 * j + frow;
+    if (m >= g.M) continue;
+    const float sam = SM == kSmScaled ? sa[g.sa_vec ? m : 0] : 1.0f;
+#pragma unroll
+    for (int i = 0; i < FN; ++i)
+#pragma unroll
+      for (int grp = 0; grp < 4; ++grp) {
+        const int64_t n0 = n_wave + 32 * i + 8 * grp + 4 * h;
+        float v[4];
+#pragma unroll
+        for (int qq = 0; qq < 4; ++qq) {
+          const int64_t n = n0 + qq < g.N ? n0 + qq : g.N - 1;
+          float y = acc[i][j][4 * grp + qq];
+          if constexpr (SM == kSmScaled) y = (y * sam) * sb[g.sb_vec ? n : 0];
+          if (!split && g.bias) y += load_f32(g.bias, g.bias_dtype, n);
+          v[qq] = y;
+        }
+        if (split) {
+          float* pr = ka.g.ws + ((int64_t)blockIdx.y * g.M + m) * g.N;
+#pragma unroll
+          for (int qq = 0; qq < 4; ++qq)
+            if (n0 + qq < g.N) pr[n0 + qq] = v[qq];
+        } else if (n0 + 3 < g.N && eb == 2 &&
+                   (reinterpret_cast<uintptr_t>(static_cast<uint16_t*>(g.out) + m * g.ldo + n0) & 7) == 0) {
+          uint32_t pk[2];
+#pragma unroll
+          for (int qq = 0; qq < 2; ++qq) {
+            if (g.out_dtype == AYK_BF16) pk[qq] = pack_bf16x2(v[2 * qq], v[2 * qq + 1]);
+            else pk[qq] = (uint32_t)f32_to_f16_bits(v[2 * qq]) | ((uint32_t)f32_to_f16_bits(v[2 * qq + 1]) << 16);
+          }
+          *reinterpret_cast<uint2*>(static_cast<uint16_t*>(g.out) + m * g.ldo + n0) = make_uint2(pk[0], pk[1]);
+        } else {
+#pragma unroll
+          for (int qq = 0; qq < 4; ++qq)
+            if (n0 + qq < g.N) store_f32(g.out, g.out_dtype, m * g.ldo + n0 + qq, v[qq]);
+        }
+      }
+  }
+}
+
 // FN 32-row weight tiles per wavefront, FM 32-row activation tiles (M <= 32 FM), KS K
 // parts per row group, G pairs per activation chunk.
-template <bool MX, int FN, int FM, int KS, int G>
-__global__ __launch_bounds__(kWaves * kWave) void fp8_skinny_kernel(KArgs ka) {
+template <int SM, int FN, int FM, int KS, int G>
+__global__ __launch_bounds__(kWaves * kWave, FN == 1 && KS == 1 ? 2 : 1) void fp8_skinny_kernel(KArgs ka) {
   const SkinnyFp8Args& g = ka.g;
+  constexpr bool MX = SM == kSmMx, BLK = SM == kSmBlock;
   constexpr int D = kDepth;
   constexpr int RW = 32 * FN;                // weight rows per wavefront
   constexpr int RG = kWaves / KS;            // row groups per workgroup
@@ -140,7 +203,7 @@ __global__ __launch_bounds__(kWaves * kWave) void fp8_skinny_kernel(KArgs ka) {
   constexpr int kXPart = MP * kXRow;
   constexpr int kXChunk = KS * kXPart;
   constexpr int kXIns = kXChunk / (1024 * kWaves);  // activation loads per wavefront and chunk
-  constexpr int kCodeIns = MX ? (FN + FM + 1) / 2 : 0;  // code loads per stage (64 dwords each)
+  constexpr int kCodeIns = scale_ins(SM, FN, FM);  // scale loads per stage
   constexpr int kOpsW = kWIns + kCodeIns;
   constexpr int U = G % D == 0 ? G : (D % G == 0 ? D : G * D);  // a multiple of G and D
   static_assert(kXChunk % (1024 * kWaves) == 0, "whole activation loads per wavefront");
@@ -154,7 +217,7 @@ __global__ __launch_bounds__(kWaves * kWave) void fp8_skinny_kernel(KArgs ka) {
 
   __shared__ __attribute__((aligned(1024))) uint8_t wring[kWaves * D * kWStage];
   __shared__ __attribute__((aligned(1024))) uint8_t xbuf[2 * kXChunk];
-  __shared__ uint32_t cring[MX ? kWaves * D * kCodeIns * kWave : 1];
+  __shared__ uint32_t cring[kCodeIns ? kWaves * D * kCodeIns * kWave : 1];
   const int lane = threadIdx.x & (kWave - 1);
   const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x / kWave);
   const int frow = lane & 31, h = lane >> 5;
@@ -192,11 +255,14 @@ __global__ __launch_bounds__(kWaves * kWave) void fp8_skinny_kernel(KArgs ka) {
     xsrc[j] = g.a + mm * g.lda + kbeg + q * plen + sg * kPairK + 16 * (p ^ ((m >> 1) & 7));
     xdst[j] = __builtin_amdgcn_readfirstlane(1024 * (wave * kXIns + j));
   }
-  // MX code dwords of a stage, through LDS like the operands (a register load would be
-  // waited for with every direct load before it): entry e = 64 j + lane of code load j
-  // is weight row e of the wavefront for e < 32 FN, then activation row e - 32 FN;
-  // entries past the last repeat it. Rows past N or M repeat the last row.
-  const uint8_t* csrc[MX ? kCodeIns : 1];
+  // Scale dwords of a stage, through LDS like the operands (a register load would be
+  // waited for with every direct load before it). Entry e = 64 j + lane of load j, at
+  // csrc[j] + stage cstep[j]:
+  //   MX: weight row e of the wavefront for e < 32 FN, then activation row e - 32 FN;
+  //   block-128: activation row e for e < 32 FM, then the wavefront's weight scale.
+  // Entries past the last repeat it; rows past N or M repeat the last row.
+  const uint8_t* csrc[kCodeIns ? kCodeIns : 1];
+  uint32_t cstep[kCodeIns ? kCodeIns : 1];
   uint32_t* mycodes = cring + wave * D * kCodeIns * kWave;
   if constexpr (MX) {
 #pragma unroll
@@ -210,6 +276,25 @@ __global__ __launch_bounds__(kWaves * kWave) void fp8_skinny_kernel(KArgs ka) {
         const int64_t m = e - 32 * FN < g.M ? e - 32 * FN : g.M - 1;
         csrc[j] = static_cast<const uint8_t*>(g.sa) + m * g.ld_sa + kpart / 32;
       }
+      cstep[j] = kPairK / 32;
+    }
+  }
+  if constexpr (BLK) {
+    const int64_t kb0 = kpart / kPairK;
+    const int64_t nb = (n_wave < g.N ? n_wave : g.N - 1) / 128;
+#pragma unroll
+    for (int j = 0; j < kCodeIns; ++j) {
+      int e = kWave * j + lane;
+      e = e < 32 * FM + 1 ? e : 32 * FM;
+      if (e < 32 * FM) {
+        const int64_t m = e < g.M ? e : g.M - 1;
+        csrc[j] = reinterpret_cast<const uint8_t*>(static_cast<const float*>(g.sa) +
+                                                   (g.sa_vec ? kb0 * g.M + m : m * g.ld_sa + kb0));
+        cstep[j] = g.sa_vec ? 4 * (uint32_t)g.M : 4;
+      } else {
+        csrc[j] = reinterpret_cast<const uint8_t*>(static_cast<const float*>(g.sb) + nb * g.ld_sb + kb0);
+        cstep[j] = 4;
+      }
     }
   }
 
@@ -221,10 +306,10 @@ __global__ __launch_bounds__(kWaves * kWave) void fp8_skinny_kernel(KArgs ka) {
     const int64_t k = (int64_t)tc * kPairK;
 #pragma unroll
     for (int j = 0; j < kWIns; ++j) dma16_nt(wsrc[j] + k, myring + slot * kWStage + 1024 * j);
-    if constexpr (MX) {
+    if constexpr (kCodeIns > 0) {
 #pragma unroll
       for (int j = 0; j < kCodeIns; ++j)
-        __builtin_amdgcn_global_load_lds(csrc[j] + k / 32,
+        __builtin_amdgcn_global_load_lds(csrc[j] + (int64_t)tc * cstep[j],
                                          (__attribute__((address_space(3))) void*)(mycodes + (slot * kCodeIns + j) * kWave),
                                          4, 0, 0);
     }
@@ -248,6 +333,18 @@ __global__ __launch_bounds__(kWaves * kWave) void fp8_skinny_kernel(KArgs ka) {
     const uint32_t wbase = lds_u32(myring + slot * kWStage);
     const uint32_t xbase = lds_u32(xbuf + ((s / G) & 1) * kXChunk + part * kXPart) + (uint32_t)((s % G) * kPairK);
     uint32_t wc[FN], xc[FM];
+    float bsc[FM];  // block-128: sa[m, kb] sb[n / 128, kb] of this lane's row of tile j
+    if constexpr (BLK) {
+      const uint32_t cb = lds_u32(reinterpret_cast<const uint8_t*>(mycodes + slot * kCodeIns * kWave));
+      uint32_t ca[FM + 1], cv[FM + 1];
+#pragma unroll
+      for (int j = 0; j < FM; ++j) ca[j] = cb + 4 * (32 * j + frow);
+      ca[FM] = cb + 4 * 32 * FM;
+      code_reads<FM + 1>(cv, ca);
+#pragma unroll
+      for (int j = 0; j < FM; ++j) bsc[j] = __builtin_bit_cast(float, cv[j]) * __builtin_bit_cast(float, cv[FM]);
+    }
+    v16f part[BLK ? FN : 1][BLK ? FM : 1];
     if constexpr (MX) {
       const uint32_t cb = lds_u32(reinterpret_cast<const uint8_t*>(mycodes + slot * kCodeIns * kWave)) + 4 * frow;
       uint32_t ca[FN + FM];
@@ -288,9 +385,22 @@ __global__ __launch_bounds__(kWaves * kWave) void fp8_skinny_kernel(KArgs ka) {
           const v8i xf = __builtin_shufflevector(__builtin_bit_cast(v4i, v[2 * FN + 2 * j]),
                                                  __builtin_bit_cast(v4i, v[2 * FN + 2 * j + 1]), 0, 1, 2, 3, 4, 5, 6, 7);
           const int cx = MX ? (int)(xc[j] >> sh) : kCodeOne;
-          acc[i][j] = __builtin_amdgcn_mfma_scale_f32_32x32x64_f8f6f4(wf, xf, acc[i][j], 0, 0, 0, cw, 0, cx);
+          if constexpr (BLK) {
+            const v16f c = t == 0 ? v16f{} : part[i][j];
+            part[i][j] = __builtin_amdgcn_mfma_scale_f32_32x32x64_f8f6f4(wf, xf, c, 0, 0, 0, cw, 0, cx);
+          } else {
+            acc[i][j] = __builtin_amdgcn_mfma_scale_f32_32x32x64_f8f6f4(wf, xf, acc[i][j], 0, 0, 0, cw, 0, cx);
+          }
         }
       }
+    }
+    if constexpr (BLK) {  // fold the 128-K block: one fma per accumulator
+#pragma unroll
+      for (int i = 0; i < FN; ++i)
+#pragma unroll
+        for (int j = 0; j < FM; ++j)
+#pragma unroll
+          for (int r = 0; r < 16; ++r) acc[i][j][r] = __builtin_fmaf(part[i][j][r], bsc[j], acc[i][j][r]);
     }
   };
 
@@ -343,51 +453,7 @@ __global__ __launch_bounds__(kWaves * kWave) void fp8_skinny_kernel(KArgs ka) {
         }
   }
 
-  // Epilogue. acc[i][j][4 grp + qq] = D[n = n_wave + 32 i + 8 grp + 4 h + qq][m = 32 j + frow].
-  const bool split = gridDim.y > 1;
-  const float* sa = static_cast<const float*>(g.sa);
-  const float* sb = static_cast<const float*>(g.sb);
-  const int eb = g.out_dtype == AYK_F32 ? 4 : 2;
-#pragma unroll
-  for (int j = 0; j < FM; ++j) {
-    const int64_t m = 32 * j + frow;
-    if (m >= g.M) continue;
-    const float sam = MX ? 1.0f : sa[g.sa_vec ? m : 0];
-#pragma unroll
-    for (int i = 0; i < FN; ++i)
-#pragma unroll
-      for (int grp = 0; grp < 4; ++grp) {
-        const int64_t n0 = n_wave + 32 * i + 8 * grp + 4 * h;
-        float v[4];
-#pragma unroll
-        for (int qq = 0; qq < 4; ++qq) {
-          const int64_t n = n0 + qq < g.N ? n0 + qq : g.N - 1;
-          float y = acc[i][j][4 * grp + qq];
-          if constexpr (!MX) y = (y * sam) * sb[g.sb_vec ? n : 0];
-          if (!split && g.bias) y += load_f32(g.bias, g.bias_dtype, n);
-          v[qq] = y;
-        }
-        if (split) {
-          float* pr = ka.g.ws + ((int64_t)blockIdx.y * g.M + m) * g.N;
-#pragma unroll
-          for (int qq = 0; qq < 4; ++qq)
-            if (n0 + qq < g.N) pr[n0 + qq] = v[qq];
-        } else if (n0 + 3 < g.N && eb == 2 &&
-                   (reinterpret_cast<uintptr_t>(static_cast<uint16_t*>(g.out) + m * g.ldo + n0) & 7) == 0) {
-          uint32_t pk[2];
-#pragma unroll
-          for (int qq = 0; qq < 2; ++qq) {
-            if (g.out_dtype == AYK_BF16) pk[qq] = pack_bf16x2(v[2 * qq], v[2 * qq + 1]);
-            else pk[qq] = (uint32_t)f32_to_f16_bits(v[2 * qq]) | ((uint32_t)f32_to_f16_bits(v[2 * qq + 1]) << 16);
-          }
-          *reinterpret_cast<uint2*>(static_cast<uint16_t*>(g.out) + m * g.ldo + n0) = make_uint2(pk[0], pk[1]);
-        } else {
-#pragma unroll
-          for (int qq = 0; qq < 4; ++qq)
-            if (n0 + qq < g.N) store_f32(g.out, g.out_dtype, m * g.ldo + n0 + qq, v[qq]);
-        }
-      }
-  }
+  store_tiles<SM, FN, FM>(ka, acc, n_wave, frow, h);
 }
 
 // Fixed-order sum of the grid-y partials, bias, one rounding.
@@ -403,40 +469,68 @@ __global__ __launch_bounds__(256) void skinny_reduce(const float* __restrict__ p
   store_f32(out, out_dtype, m * ldo + n, v);
 }
 
-// Launch plan from the shape alone (the workspace query reproduces it). Rows per
-// workgroup R = 32 FN (4 / KS) from the first of (FN, KS) = (2, 1), (1, 1), (2, 2),
-// (2, 4), (1, 4) that gives >= 192 workgroups while the activation bytes a workgroup
-// reads stay within its weight bytes (R >= 32 FM); short of that, the last admissible
-// one and a grid-y K split up to one round of 256 workgroups. LDS: 4 x 3 x 4 KB FN of
-// rings + 2 KS 32 FM 128 G of activation chunks <= 160 KB.
+// Launch plan from the shape alone (the workspace query reproduces it), in three tiers
+// (below). Measured on the decode shapes: two resident workgroups of 32-row wavefronts
+// beat one of 64-row wavefronts or of K parts wherever the grid reaches half the chip
+// (DeepSeek-V3 block-128 at M = 32: 42.7 -> 32.7 us and 37.7 -> 30.5 us).
 struct SkPlan {
   bool ok;
   int fn, fm, ks, g, split;
   int64_t kps;
 };
-constexpr int64_t skinny_lds(int fn, int fm, int ks, int g, bool mx) {
+constexpr int64_t skinny_lds(int fn, int fm, int ks, int g, int sm) {
   return (int64_t)kWaves * kDepth * 4096 * fn + 2LL * ks * 32 * fm * kPairK * g +
-         (mx ? (int64_t)kWaves * kDepth * ((fn + fm + 1) / 2) * kWave * 4 : 0);
+         (int64_t)kWaves * kDepth * scale_ins(sm, fn, fm) * kWave * 4;
 }
-SkPlan skinny_plan(int64_t M, int64_t N, int64_t K, bool mx) {
+SkPlan skinny_plan(int64_t M, int64_t N, int64_t K, int sm) {
   SkPlan p{};
   if (M < 1 || M > 64 || N < 1 || K % 256 || K >= ((int64_t)1 << 31)) return p;
   p.fm = M <= 32 ? 1 : 2;
-  const int cand[5][2] = {{2, 1}, {1, 1}, {2, 2}, {2, 4}, {1, 4}};
+  // 1. 64 rows per wavefront (256 a workgroup) where that alone gives >= 192 workgroups.
+  if (cdiv(N, 256) >= 192 && skinny_lds(2, p.fm, 1, 2, sm) <= 160 * 1024) {
+    p.fn = 2;
+    p.ks = 1;
+    p.g = p.fm == 1 && K % (4 * kPairK) == 0 ? 4 : 2;
+    p.split = 1;
+    p.kps = K;
+    p.ok = true;
+    return p;
+  }
+  // 2. 32 rows per wavefront, whole K per wavefront, 2-pair chunks: <= 80 KB of LDS, two
+  // workgroups per CU; a grid K split up to 256 workgroups (>= 2048 K each), taken when
+  // it reaches >= 128 workgroups.
+  {
+    const int64_t w1 = cdiv(N, 128);
+    int64_t split = 1;
+    while (w1 * split * 2 <= 256 && K % (2 * kPairK * split * 2) == 0 && K / (split * 2) >= 2048) split *= 2;
+    if (w1 * split >= 128) {
+      p.fn = 1;
+      p.ks = 1;
+      p.g = 2;
+      p.split = (int)split;
+      p.kps = K / split;
+      p.ok = w1 <= 0x7FFFFFFF;
+      return p;
+    }
+  }
+  // 3. Narrow projections: K parts inside the workgroup. The first of (FN, KS) = (1, 1),
+  // (2, 4), (1, 2), (1, 4) giving >= 192 workgroups (R >= 32 FM, K a multiple of KS
+  // 2-pair chunks, LDS within 160 KB), else the last admissible, then a grid K split up
+  // to 256 workgroups.
+  const int cand[4][2] = {{1, 1}, {2, 4}, {1, 2}, {1, 4}};
   int pick = -1;
-  for (int c = 0; c < 5; ++c) {
+  for (int c = 0; c < 4; ++c) {
     const int fn = cand[c][0], ks = cand[c][1];
     const int r = 32 * fn * (kWaves / ks);
-    if (r < 32 * p.fm || K % (ks * kPairK * 2) || skinny_lds(fn, p.fm, ks, 2, mx) > 160 * 1024) continue;
+    if (r < 32 * p.fm || K % (ks * kPairK * 2) || skinny_lds(fn, p.fm, ks, 2, sm) > 160 * 1024) continue;
     pick = c;
     if (cdiv(N, r) >= 192) break;
   }
   if (pick < 0) return p;
   p.fn = cand[pick][0];
   p.ks = cand[pick][1];
+  p.g = 2;
   const int64_t wgs = cdiv(N, 32 * p.fn * (kWaves / p.ks));
-  // Activation chunk: 4 pairs per part where both buffers fit 32 KB and K allows, else 2.
-  p.g = p.ks * p.fm == 1 && K % (4 * kPairK) == 0 && skinny_lds(p.fn, p.fm, p.ks, 4, mx) <= 160 * 1024 ? 4 : 2;
   const int64_t gran = (int64_t)p.ks * kPairK * p.g;  // K of one chunk over all parts
   int64_t split = 1;
   while (wgs * split * 2 <= 256 && K % (gran * split * 2) == 0 && K / (split * 2) >= 2048) split *= 2;
@@ -446,36 +540,36 @@ SkPlan skinny_plan(int64_t M, int64_t N, int64_t K, bool mx) {
   return p;
 }
 
-template <bool MX, int FN, int FM, int KS>
+template <int SM, int FN, int FM, int KS>
 bool launch_g(const SkPlan& p, const KArgs& ka, hipStream_t st) {
   const dim3 grid((unsigned)cdiv(ka.g.N, 32 * FN * (kWaves / KS)), (unsigned)p.split), block(kWaves * kWave);
-  if constexpr (skinny_lds(FN, FM, KS, 2, MX) <= 160 * 1024) {
+  if constexpr (skinny_lds(FN, FM, KS, 2, SM) <= 160 * 1024) {
     if (p.g == 2) {
-      hipLaunchKernelGGL((fp8_skinny_kernel<MX, FN, FM, KS, 2>), grid, block, 0, st, ka);
+      hipLaunchKernelGGL((fp8_skinny_kernel<SM, FN, FM, KS, 2>), grid, block, 0, st, ka);
       return true;
     }
   }
-  if constexpr (KS * FM == 1 && skinny_lds(FN, FM, KS, 4, MX) <= 160 * 1024) {
+  if constexpr (KS * FM == 1 && skinny_lds(FN, FM, KS, 4, SM) <= 160 * 1024) {
     if (p.g == 4) {
-      hipLaunchKernelGGL((fp8_skinny_kernel<MX, FN, FM, KS, 4>), grid, block, 0, st, ka);
+      hipLaunchKernelGGL((fp8_skinny_kernel<SM, FN, FM, KS, 4>), grid, block, 0, st, ka);
       return true;
     }
   }
   return false;
 }
 
-template <bool MX>
-bool launch_mx(const SkPlan& p, const KArgs& ka, hipStream_t st) {
+template <int SM>
+bool launch_sm(const SkPlan& p, const KArgs& ka, hipStream_t st) {
   const int key = p.fn * 100 + p.fm * 10 + p.ks;
   switch (key) {
-    case 211: return launch_g<MX, 2, 1, 1>(p, ka, st);
-    case 221: return launch_g<MX, 2, 2, 1>(p, ka, st);
-    case 111: return launch_g<MX, 1, 1, 1>(p, ka, st);
-    case 121: return launch_g<MX, 1, 2, 1>(p, ka, st);
-    case 212: return launch_g<MX, 2, 1, 2>(p, ka, st);
-    case 222: return launch_g<MX, 2, 2, 2>(p, ka, st);
-    case 214: return launch_g<MX, 2, 1, 4>(p, ka, st);
-    case 114: return launch_g<MX, 1, 1, 4>(p, ka, st);
+    case 211: return launch_g<SM, 2, 1, 1>(p, ka, st);
+    case 221: return launch_g<SM, 2, 2, 1>(p, ka, st);
+    case 111: return launch_g<SM, 1, 1, 1>(p, ka, st);
+    case 121: return launch_g<SM, 1, 2, 1>(p, ka, st);
+    case 214: return launch_g<SM, 2, 1, 4>(p, ka, st);
+    case 112: return launch_g<SM, 1, 1, 2>(p, ka, st);
+    case 122: return launch_g<SM, 1, 2, 2>(p, ka, st);
+    case 114: return launch_g<SM, 1, 1, 4>(p, ka, st);
     default: return false;
   }
 }
@@ -483,24 +577,29 @@ bool launch_mx(const SkPlan& p, const KArgs& ka, hipStream_t st) {
 }  // namespace
 
 bool skinny_fp8_supported(const SkinnyFp8Args& g) {
-  const SkPlan p = skinny_plan(g.M, g.N, g.K, g.mx != 0);
+  const SkPlan p = skinny_plan(g.M, g.N, g.K, g.mode);
   if (!p.ok) return false;
   if (g.lda % 16 || g.ldw % 16 || !aligned16(g.a) || !aligned16(g.w)) return false;
-  if (g.mx) {
+  if (g.mode == kSmMx) {
     // code dwords of one 128-K pair are 4-byte aligned loads
     if ((reinterpret_cast<uintptr_t>(g.sa) & 3) || (reinterpret_cast<uintptr_t>(g.sb) & 3) || g.ld_sa % 4 || g.ld_sb % 4)
+      return false;
+  }
+  if (g.mode == kSmBlock) {
+    if ((reinterpret_cast<uintptr_t>(g.sa) & 3) || (reinterpret_cast<uintptr_t>(g.sb) & 3) || g.ld_sb < g.K / 128 ||
+        (!g.sa_vec && g.ld_sa < g.K / 128))
       return false;
   }
   return g.out_dtype == AYK_F32 || g.out_dtype == AYK_BF16 || g.out_dtype == AYK_F16;
 }
 
-size_t skinny_fp8_workspace(int64_t M, int64_t N, int64_t K, bool mx) {
-  const SkPlan p = skinny_plan(M, N, K, mx);
+size_t skinny_fp8_workspace(int64_t M, int64_t N, int64_t K, int mode) {
+  const SkPlan p = skinny_plan(M, N, K, mode);
   return p.ok && p.split > 1 ? (size_t)p.split * (size_t)M * (size_t)N * sizeof(float) : 0;
 }
 
 int skinny_fp8_launch(const SkinnyFp8Args& g, hipStream_t st, const char* op) {
-  const SkPlan p = skinny_plan(g.M, g.N, g.K, g.mx != 0);
+  const SkPlan p = skinny_plan(g.M, g.N, g.K, g.mode);
   if (!p.ok) return fail(AYK_EINVAL, "%s: no decode-batch plan for this shape", op);
   if (p.split > 1) {
     const size_t need = (size_t)p.split * (size_t)g.M * (size_t)g.N * sizeof(float);
@@ -508,7 +607,9 @@ int skinny_fp8_launch(const SkinnyFp8Args& g, hipStream_t st, const char* op) {
       return fail(AYK_EWORKSPACE, "%s: workspace of %zu bytes required, %zu given", op, need, g.ws_bytes);
   }
   KArgs ka{g, p.kps};
-  const bool launched = g.mx ? launch_mx<true>(p, ka, st) : launch_mx<false>(p, ka, st);
+  const bool launched = g.mode == kSmMx      ? launch_sm<kSmMx>(p, ka, st)
+                        : g.mode == kSmBlock ? launch_sm<kSmBlock>(p, ka, st)
+                                             : launch_sm<kSmScaled>(p, ka, st);
   if (!launched) return fail(AYK_EINVAL, "%s: no decode-batch kernel for this plan", op);
   if (int rc = check_launch(op)) return rc;
   if (p.split > 1) {

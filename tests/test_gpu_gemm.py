@@ -169,8 +169,11 @@ def test_mxfp8_scaled_mm_split_k(gpu, m, n, k):
 # K parts per row group (1, 2, 4), activation chunk of 2 or 4 pairs, grid K split.
 SKINNY_MNK = [
     (2, 3000, 2048),     # 32 rows, 4 K parts, ragged N
-    (8, 24576, 2048),    # 32 rows, chunks of 4 pairs, one round of workgroups
-    (17, 5000, 1280),    # K % 512 != 0: 2-pair chunks only
+    (8, 24576, 2048),    # 32 rows, whole K, two workgroups per CU
+    (16, 57344, 1024),   # 64 rows per wavefront, chunks of 4 pairs
+    (8, 14336, 2048),    # 64 rows per wavefront, 4 K parts
+    (17, 5000, 1280),    # K % 512 != 0: whole K per wavefront, under 128 workgroups
+    (40, 20000, 2048),   # two activation tiles, 32 rows, whole K
     (33, 1000, 4096),    # two activation tiles, 2 K parts, grid split 2
     (48, 57344, 1024),   # 64 rows per wavefront, two activation tiles
     (64, 1302, 8192),    # N % 4 != 0 rows: element stores, grid split
@@ -393,17 +396,19 @@ def test_fp8_blockwise_mm_256_scale_edges(gpu):
 
 
 @pytest.mark.parametrize("m,n,k,col_major,sdt,with_bias", [
-    (32, 1024, 4096, False, torch.float32, True),     # K split 4
+    (32, 1024, 4096, False, torch.float16, True),     # K split 4
     (200, 768, 8192, True, torch.bfloat16, True),     # split 8, column-major activation scales
     (7, 256, 2048, False, torch.float16, False),      # split 2, 7 rows
     (256, 2048, 7168, False, torch.float32, False),   # DeepSeek-V3 K, split 4
-    (32, 7168, 18432, False, torch.float32, True),    # DeepSeek-V3 (7168, 18432) at M = 32, split 16
-    (16, 64, 4096, False, torch.float32, False),      # N < 128: general kernel split 4
+    (32, 7168, 18432, False, torch.bfloat16, True),   # DeepSeek-V3 (7168, 18432) at M = 32, split 16
+    (16, 64, 4096, False, torch.float16, False),      # N < 128: general kernel split 4
     (40, 96, 8192, True, torch.bfloat16, True),       # N < 128, 64-row tiles: split 8
 ])
 def test_fp8_blockwise_mm_split_k(gpu, m, n, k, col_major, sdt, with_bias):
     """Launches with too few 128 x 128 tiles split K over fp32 partials (the workspace the
-    wrapper allocates from the size query) and reduce them in a fixed order."""
+    wrapper allocates from the size query) and reduce them in a fixed order. (Up to 64
+    rows with fp32 weight scales take the decode-batch kernel instead: 16-bit weight scales
+    here keep these on the general kernel.)"""
     from ayaka.kernel.hip import _lib, fp8_blockwise_mm
 
     _say(f"fp8_blockwise_mm split-K m={m} n={n} k={k} col_major={col_major} sdt={sdt} bias={with_bias}")
@@ -419,6 +424,33 @@ def test_fp8_blockwise_mm_split_k(gpu, m, n, k, col_major, sdt, with_bias):
     out = fp8_blockwise_mm(a.to(gpu), w.to(gpu), sa_arg.to(gpu), sb.to(gpu),
                            bias.to(gpu) if bias is not None else None, a_scale_col_major=col_major)
     assert_linear_close(out, ref, "blockwise_mm split-K")
+
+
+@pytest.mark.parametrize("m,n,k,col_major,with_bias", [
+    (32, 18432, 7168, False, True),    # DeepSeek-V3 up at M = 32
+    (32, 7168, 18432, True, False),    # DeepSeek-V3 down at M = 32, column-major activation scales
+    (5, 1000, 2048, False, True),      # N not a multiple of 128: the last block's rows clamp
+    (64, 300, 8192, True, True),       # two activation tiles, grid K split
+    (16, 64, 4096, False, False),      # N < 128
+    (40, 4096, 1280, False, True),     # K % 512 != 0
+])
+def test_fp8_blockwise_mm_decode_batch(gpu, m, n, k, col_major, with_bias):
+    """Block-128 decode batches with fp32 scales: the weight-streaming kernel folds every
+    128-K stage's partial with sa[m, kb] sb[n / 128, kb] (block amax spread 1e-3 .. 1)."""
+    from ayaka.kernel.hip import fp8_blockwise_mm
+
+    _say(f"fp8_blockwise_mm decode batch m={m} n={n} k={k} col_major={col_major} bias={with_bias}")
+    kb, nb = k // 128, -(-n // 128)
+    a = _fp8((m, k), seed=m + 71, scale=30)
+    w = _fp8((n, k), seed=n + 72, scale=30)
+    sa = torch.exp(torch.rand(m, kb, generator=_gen(74)) * -6.9).float()
+    sb = torch.exp(torch.rand(nb, kb, generator=_gen(75)) * -6.9).float()
+    sa_arg = sa.t().contiguous() if col_major else sa
+    bias = (torch.randn(n, generator=_gen(76)) * 5).to(torch.bfloat16) if with_bias else None
+    ref = ora.fp8_blockwise_mm(a, w, sa_arg, sb, bias, col_major)
+    out = fp8_blockwise_mm(a.to(gpu), w.to(gpu), sa_arg.to(gpu), sb.to(gpu),
+                           bias.to(gpu) if bias is not None else None, a_scale_col_major=col_major)
+    assert_linear_close(out, ref, "blockwise_mm decode batch")
 
 
 @pytest.mark.parametrize("m,n,k", [(1, 512, 1024), (1, 1000, 8192), (64, 256, 512), (100, 300, 1024), (512, 512, 2048), (33, 96, 96),
