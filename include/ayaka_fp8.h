@@ -103,9 +103,10 @@ int ayk_fp8_scaled_mm(const void* a, int64_t lda, const void* b, int64_t ldb,
                       void* workspace, size_t workspace_bytes, ayk_stream_t stream);
 /* Bytes of split-K partials ayk_fp8_scaled_mm may need for this shape (0: none). A
  * launch short of one full round of tiles splits K; a launch whose last round of
- * 256 x 256 tiles is at most a third full splits that round's tiles over K. Each
- * piece writes its scaled fp32 partial and a fixed-order sum adds the bias and rounds
- * once. */
+ * 256 x 256 tiles is at most a third full splits that round's tiles over K; a decode
+ * batch (M <= 64) on a narrow projection splits K across workgroups. Each piece writes
+ * its fp32 partial and a fixed-order sum adds the bias and rounds once. The size is
+ * the largest any of these needs for the shape. */
 size_t ayk_fp8_scaled_mm_workspace_bytes(int64_t M, int64_t N, int64_t K);
 
 /* Replaces ayaka::int8_scaled_mm (gemm/int8_gemm.py:134; oracle reference/gemm.py:192-211).
@@ -134,8 +135,8 @@ int ayk_fp8_blockwise_mm(const void* a, int64_t lda, const void* b, int64_t ldb,
                          void* out, int out_dtype, int64_t ldo,
                          void* workspace, size_t workspace_bytes, ayk_stream_t stream);
 /* Bytes of split-K partials ayk_fp8_blockwise_mm may need for this shape (0: none). A
- * launch with fewer tiles than fill the machine splits K and sums fp32 partials in a
- * fixed order before the single rounding. */
+ * launch with fewer tiles than fill the machine (or, for M <= 64, fewer row groups)
+ * splits K and sums fp32 partials in a fixed order before the single rounding. */
 size_t ayk_fp8_blockwise_mm_workspace_bytes(int64_t M, int64_t N, int64_t K);
 
 /* Replaces fp8_blockwise_scaled_grouped_mm (kernel/triton/moe/moe_grouped_gemm.py:599,

@@ -317,6 +317,9 @@ def test_c_abi_rejects_bad_arguments_without_a_gpu():
     assert b"multiple of 16" in lib.ayk_last_error()
     assert lib.ayk_mxfp8_scaled_mm(None, 48, None, 1, None, 48, None, 1, 2, 2, 48, None, 0, None, 2, 2, None, 0, None) == _lib.AYK_EINVAL
     assert lib.ayk_mxfp8_scaled_mm_workspace_bytes(64, 8192, 28672) > 0
+    # the decode-batch kernel's grid split (Llama-3-70B down at M = 64: 64 workgroups x 4)
+    assert lib.ayk_mxfp8_scaled_mm_workspace_bytes(64, 8192, 28672) >= 4 * 64 * 8192 * 4
+    assert lib.ayk_fp8_blockwise_mm_workspace_bytes(32, 7168, 18432) >= 4 * 32 * 7168 * 4
     assert lib.ayk_fp8_weight_only_gemv(None, _lib.AYK_F32, None, 16, 4, 16, None, 0, 1, 1, 16, None, None, 0, None) == _lib.AYK_EINVAL
     # zero-sized problems are no-ops that succeed without touching a device
     assert lib.ayk_per_token_quant_fp8(None, _lib.AYK_BF16, 0, 16, 16, None, 16, None, None) == _lib.AYK_OK
