@@ -19,7 +19,9 @@
 //
 // Tiling. 512 threads = 8 wavefronts, two per SIMD, so one wavefront's rescale (VALU)
 // runs beside the other's MFMAs. Wavefront (wn, wm) owns weight rows [128 wn, +128) --
-// inside one 128-row scale block -- and activation rows [64 wm, +64): 4 x 2 MFMA tiles of
+// inside one 128-row scale block -- and activation rows [64 wm, +64) (wave_role: the two
+// wavefronts of a SIMD own activation rows in different halves of the tile, so that a
+// wavefront whose rows all lie past M skips its MFMAs without idling a SIMD): 4 x 2 MFMA tiles of
 // 32 x 32, 128 fp32 accumulators in VGPRs (this file is compiled with the VGPR form of
 // the MFMAs). One 128-K block is one "pair" of 64-K MFMA steps; operands move HBM/L2 ->
 // LDS with direct-to-LDS 16-byte loads covering 8 rows x 128 bytes each, into two 64 KB
@@ -48,6 +50,12 @@ constexpr int kDma = kPairBytes / 1024 / 8;      // direct loads per wavefront p
 constexpr int FN = 4, FM = 2;                    // MFMA tiles per wavefront (n, m)
 constexpr int kCodeOne = 127;                    // UE8M0 code of 1.0
 constexpr int kRegion = 16 * 1024;               // a wavefront's epilogue staging region
+
+// Wavefront w -> (wn, wm). Wavefronts w and w + 4 share a SIMD; they get wm and wm + 2.
+__device__ inline void wave_role(int w, int& wn, int& wm) {
+  wn = (w >> 1) & 1;
+  wm = (w & 1) | ((w >> 2) << 1);
+}
 
 __device__ inline v16f mfma_scaled(const v8i& w, const v8i& a, const v16f& c, int code_a) {
   return __builtin_amdgcn_mfma_scale_f32_32x32x64_f8f6f4(w, a, c, 0, 0, 0, kCodeOne, 0, code_a);
@@ -81,7 +89,9 @@ __device__ __attribute__((always_inline)) inline void block256_epilogue(const Bl
   constexpr int kRowsPerStore = 64 / kChunks;       // rows one store instruction covers
   static_assert(32 * kRowBytes <= kRegion, "staging slab must fit the region");
   const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
-  const int wn = wave >> 2, wm = wave & 3, h = lane >> 5, frow = lane & 31;
+  int wn, wm;
+  wave_role(wave, wn, wm);
+  const int h = lane >> 5, frow = lane & 31;
   const int64_t n_w = n_tile + wn * 128;
 #pragma unroll
   for (int j = 0; j < FM; ++j) {
@@ -169,9 +179,13 @@ __device__ __attribute__((always_inline)) inline void block256_tile(const Block2
                                                                     int64_t klen, uint8_t* P0, uint8_t* P1) {
   const int tid = threadIdx.x, lane = tid & 63;
   const int wave_u = __builtin_amdgcn_readfirstlane(tid >> 6);
-  const int wn = wave_u >> 2, wm = wave_u & 3;
+  int wn, wm;
+  wave_role(wave_u, wn, wm);
   const int h = lane >> 5, frow = lane & 31;
   const int64_t n_base = (int64_t)tn * kTile, m_base = (int64_t)tm * kTile;
+  // Activation rows past M (an expert's or the tile tail's): a wavefront with none of
+  // its 64 rows below M skips its MFMAs and its epilogue (wave-uniform).
+  const bool rows_live = m_base + 64 * wm < g.M;
   const int np = (int)(klen / kPairK);   // K blocks of this range (>= 1)
   const int npairs = (np + 1) & ~1;      // the loop runs pairs two at a time
   const int kb0 = (int)(k0 / kPairK);
@@ -312,7 +326,7 @@ __device__ __attribute__((always_inline)) inline void block256_tile(const Block2
   // U is zero before the first block, so its rescale is moot.
   constexpr int kSchedMfma = 0x008, kSchedValu = 0x002, kSchedDsRead = 0x100;
   auto pair = [&](int p, uint8_t* cur, uint8_t* nxt) {
-    const bool live = p < np;  // wave-uniform
+    const bool live = p < np && rows_live;  // wave-uniform
     if (live) {
 #pragma unroll
       for (int i = 0; i < FN; ++i) {
@@ -382,6 +396,7 @@ __device__ __attribute__((always_inline)) inline void block256_tile(const Block2
   lds_barrier();  // no wavefront still reads a pair buffer: they become staging regions
 
   uint8_t* region = (wave_u < 4 ? P0 : P1) + (wave_u & 3) * kRegion;
+  if (!rows_live) return;
   if (g.out_dtype == AYK_BF16) block256_epilogue_out<AYK_BF16>(g, U, mu, m_base, n_base, region);
   else if (g.out_dtype == AYK_F16) block256_epilogue_out<AYK_F16>(g, U, mu, m_base, n_base, region);
   else block256_epilogue_out<AYK_F32>(g, U, mu, m_base, n_base, region);
