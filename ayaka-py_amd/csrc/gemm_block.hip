@@ -546,13 +546,17 @@ bool block256_supported(const Block256Args& g) {
          (g.bias == nullptr || aligned16(g.bias)) && (g.sb_dtype == AYK_F32 || g.sb_dtype == AYK_BF16 || g.sb_dtype == AYK_F16);
 }
 
-// Under one round of tiles (256 workgroups, one per CU): the largest power-of-two K
-// split that still fits in that round, at least 1024 K per split.
+// Under half a round of tiles (256 workgroups, one per CU): as many K pieces as fit in
+// that round, each at least 1024 K and a whole number of 128-K blocks (the last one may
+// be shorter). Returns the number of pieces; block256_kps gives their K.
+int64_t block256_kps(int64_t K, int64_t split) { return cdiv(K / kPairK, split) * kPairK; }
 int64_t block256_split(int64_t M, int64_t N, int64_t K) {
   const int64_t tiles = cdiv(M, kTile) * cdiv(N, kTile);
-  int64_t split = 1;
-  while (tiles * split * 2 <= 256 && K / (split * 2) >= 1024 && (K / kPairK) % (split * 2) == 0) split *= 2;
-  return split;
+  if (tiles * 2 > 256) return 1;
+  const int64_t want = 256 / tiles, most = K / 1024;
+  const int64_t split = want < most ? want : most;
+  if (split <= 1) return 1;
+  return cdiv(K, block256_kps(K, split));
 }
 
 int block256_launch(const Block256Args& g, hipStream_t st, const char* op) {
@@ -568,7 +572,7 @@ int block256_launch(const Block256Args& g, hipStream_t st, const char* op) {
   if (g.ws == nullptr || g.ws_bytes < need)
     return fail(AYK_EWORKSPACE, "%s: workspace of %zu bytes required, %zu given", op, need, g.ws_bytes);
   hipLaunchKernelGGL(fp8_block256_kernel, dim3((unsigned)tiles, (unsigned)split), dim3(kThreads), 0, st, g, tiles_m,
-                     g.K / split);
+                     block256_kps(g.K, split));
   if (int rc = check_launch(op)) return rc;
   hipLaunchKernelGGL(block256_reduce, dim3((unsigned)cdiv(g.M * g.N, 256)), dim3(256), 0, st, g.ws, g.M, g.N, (int)split,
                      g.bias, g.bias_dtype, g.out, g.out_dtype, g.ldo);

@@ -344,6 +344,7 @@ BLOCK256 = [
     (4096, 2304, 1152, True, torch.bfloat16, torch.float32, False),
     (2304, 4352, 384, False, torch.float16, torch.float16, True),
     (2048, 4096, 8192, False, torch.float32, torch.bfloat16, True),   # 128 tiles: K split 2
+    (512, 2304, 7040, True, torch.float32, torch.bfloat16, True),     # 18 tiles: 6 K pieces, the last 5 blocks of 10
     (4096, 2048, 256, True, torch.float32, torch.bfloat16, False),    # two blocks, one pair
 ]
 
