@@ -1282,6 +1282,19 @@ StPlan stream_plan(int64_t M, int64_t N, int64_t K, int64_t bx) {
     p.tw = 1;
     p.g = 2;
     if (K % (4 * kStK * p.g)) return StPlan{};
+  } else if (p.mp == 16 && K >= 8192) {
+    // 9-16 rows over a long K (Llama-3-8B down): 16-row wavefronts over whole K, 80 KB of
+    // LDS (two workgroups per CU), a grid K split up to 256 workgroups (18.1 -> 16.3 us
+    // at M = 16). qkv, o and every 32-row case measured faster on the row-stream kernel.
+    p.ks = 1;
+    p.tw = 1;
+    p.g = 2;
+    const int64_t wgs = cdiv(N, 16 * kStWaves);
+    int64_t split = 1;
+    while (wgs * split * 2 <= 256 && K % (kStK * p.g * split * 2) == 0 && K / (split * 2) >= 2048) split *= 2;
+    if (K % (kStK * p.g * split)) return StPlan{};
+    p.split = (int)split;
+    p.kps = K / split;
   } else {
     return StPlan{};
   }

@@ -619,6 +619,10 @@ def test_weight_only_gemm_decode_plans(gpu, m, n, k, case, xdt):
     (3, 1000, 6144, "e8m0_32", torch.float16),
     (7, 3000, 2048, "block128", torch.bfloat16),
     (4, 8192, 14336, "channel", torch.bfloat16),
+    # 9-16 rows over a long K: whole-K 16-row wavefronts with a grid K split (fixed-order reduce)
+    (16, 4096, 14336, "channel", torch.bfloat16),
+    (9, 1000, 8192, "block128", torch.float16),
+    (12, 700, 12288, "e8m0_32", torch.bfloat16),
 ])
 def test_weight_only_gemm_stream(gpu, m, n, k, case, xdt):
     from ayaka.kernel.hip import fp8_weight_only_gemm
