@@ -24,7 +24,8 @@
 // of its row's code dword for the pair. LDS row r holds logical 16-byte chunk c at
 // physical chunk c ^ ((r >> 1) & 7), so the 32 rows of a fragment read fall on distinct
 // banks. fp32 scales (and the bias) are applied in the epilogue; MX codes enter the
-// MFMA (the MX UE8M0 decode of the reference, code 0 as 2^-127, is the MFMA's).
+// MFMA (the MX UE8M0 decode of the reference, code 0 as 2^-127, is the MFMA's); block-128
+// scales fold each 128-K stage's partial sums.
 #include "gemm_skinny.h"
 
 #include <utility>
@@ -135,7 +136,7 @@ struct KArgs {
   int64_t kps;  // K per grid-y split
 };
 
-// Epilogue of both forms: scales (fp32 mode), bias, output type, or the grid-y partials.
+// Epilogue: scales (fp32 mode), bias, output type, or the grid-y partials.
 // acc[i][j][4 grp + qq] = D[n = n_wave + 32 i + 8 grp + 4 h + qq][m = 32 j + frow].
 template <int SM, int FN, int FM>
 __device__ inline void store_tiles(const KArgs& ka, const v16f (&acc)[FN][FM], int64_t n_wave, int frow, int h) {
@@ -470,9 +471,10 @@ __global__ __launch_bounds__(256) void skinny_reduce(const float* __restrict__ p
 }
 
 // Launch plan from the shape alone (the workspace query reproduces it), in three tiers
-// (below). Measured on the decode shapes: two resident workgroups of 32-row wavefronts
-// beat one of 64-row wavefronts or of K parts wherever the grid reaches half the chip
-// (DeepSeek-V3 block-128 at M = 32: 42.7 -> 32.7 us and 37.7 -> 30.5 us).
+// (below), from a sweep over (FN, KS, G, split) on the decode shapes: two resident
+// workgroups of 32-row wavefronts beat one of 64-row wavefronts or of K parts wherever
+// the grid reaches half the chip (DeepSeek-V3 block-128 at M = 32, up and down: 42.7 ->
+// 37.9 us and 37.7 -> 31.6 us against the previous plan).
 struct SkPlan {
   bool ok;
   int fn, fm, ks, g, split;
