@@ -188,8 +188,10 @@ __device__ inline void store_tiles(const KArgs& ka, const v16f (&acc)[FN][FM], i
 }
 
 // FN 32-row weight tiles per wavefront, FM 32-row activation tiles (M <= 32 FM), KS K
-// parts per row group, G pairs per activation chunk.
-template <int SM, int FN, int FM, int KS, int G>
+// parts per row group, G pairs per activation chunk, CH stages per scale load (1: one
+// 4-byte scale per row and stage; 4: one 16-byte load per row covers four stages,
+// double-buffered per wavefront, for 16-byte aligned scale rows).
+template <int SM, int FN, int FM, int KS, int G, int CH>
 __global__ __launch_bounds__(kWaves * kWave, FN == 1 && KS == 1 ? 2 : 1) void fp8_skinny_kernel(KArgs ka) {
   const SkinnyFp8Args& g = ka.g;
   constexpr bool MX = SM == kSmMx, BLK = SM == kSmBlock;
@@ -204,21 +206,23 @@ __global__ __launch_bounds__(kWaves * kWave, FN == 1 && KS == 1 ? 2 : 1) void fp
   constexpr int kXPart = MP * kXRow;
   constexpr int kXChunk = KS * kXPart;
   constexpr int kXIns = kXChunk / (1024 * kWaves);  // activation loads per wavefront and chunk
-  constexpr int kCodeIns = scale_ins(SM, FN, FM);  // scale loads per stage
-  constexpr int kOpsW = kWIns + kCodeIns;
-  constexpr int U = G % D == 0 ? G : (D % G == 0 ? D : G * D);  // a multiple of G and D
+  constexpr int kCodeIns = scale_ins(SM, FN, FM);  // scale loads per stage (CH = 1) or per CH stages
+  static_assert(CH == 1 || (CH == 4 && D - 1 <= CH), "a scale buffer is refilled after its last stage");
+  constexpr int lcm2 = G % D == 0 ? G : (D % G == 0 ? D : G * D);
+  constexpr int U = lcm2 % CH == 0 ? lcm2 : (CH % lcm2 == 0 ? CH : lcm2 * CH);  // a multiple of G, D and CH
   static_assert(kXChunk % (1024 * kWaves) == 0, "whole activation loads per wavefront");
   static_assert(D - 1 <= G, "an activation buffer is refilled only after a barrier past its last read");
   constexpr auto wait_after = [](int u) {  // loads issued after stage s, before its wait
     int n = 0;
-    for (int t = u + 1; t <= u + D - 2; ++t) n += kOpsW + (t % G == 0 ? kXIns : 0);
+    for (int t = u + 1; t <= u + D - 2; ++t) n += kWIns + (t % CH == 0 ? kCodeIns : 0) + (t % G == 0 ? kXIns : 0);
     return n;
   };
   static_assert(wait_after(0) <= 63 && wait_after(G - 1) <= 63, "vmcnt range");
 
   __shared__ __attribute__((aligned(1024))) uint8_t wring[kWaves * D * kWStage];
   __shared__ __attribute__((aligned(1024))) uint8_t xbuf[2 * kXChunk];
-  __shared__ uint32_t cring[kCodeIns ? kWaves * D * kCodeIns * kWave : 1];
+  constexpr int kCodeSlots = CH == 1 ? D : 2;  // scale buffers per wavefront
+  __shared__ __attribute__((aligned(16))) uint32_t cring[kCodeIns ? kWaves * kCodeSlots * kCodeIns * kWave * CH : 1];
   const int lane = threadIdx.x & (kWave - 1);
   const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x / kWave);
   const int frow = lane & 31, h = lane >> 5;
@@ -264,7 +268,7 @@ __global__ __launch_bounds__(kWaves * kWave, FN == 1 && KS == 1 ? 2 : 1) void fp
   // Entries past the last repeat it; rows past N or M repeat the last row.
   const uint8_t* csrc[kCodeIns ? kCodeIns : 1];
   uint32_t cstep[kCodeIns ? kCodeIns : 1];
-  uint32_t* mycodes = cring + wave * D * kCodeIns * kWave;
+  uint32_t* mycodes = cring + wave * kCodeSlots * kCodeIns * kWave * CH;
   if constexpr (MX) {
 #pragma unroll
     for (int j = 0; j < kCodeIns; ++j) {
@@ -301,18 +305,28 @@ __global__ __launch_bounds__(kWaves * kWave, FN == 1 && KS == 1 ? 2 : 1) void fp
 
   // Stage t (clamped to the last; a clamped stage only rewrites data no later stage
   // reads, or the same data) into slot t % D; the chunk's activations with its first
-  // stage (xl: t % G == 0, known at compile time at every call site).
-  auto issue = [&](int slot, int t, bool xl) {
+  // stage (xl: t % G == 0) and, with CH = 4, the scales of stages t .. t + 3 with stage t
+  // (sl: t % 4 == 0), both known at compile time at every call site.
+  auto issue = [&](int slot, int t, bool xl, bool sl) {
     const int tc = t < ns ? t : ns - 1;
     const int64_t k = (int64_t)tc * kPairK;
 #pragma unroll
     for (int j = 0; j < kWIns; ++j) dma16_nt(wsrc[j] + k, myring + slot * kWStage + 1024 * j);
-    if constexpr (kCodeIns > 0) {
+    if constexpr (kCodeIns > 0 && CH == 1) {
 #pragma unroll
       for (int j = 0; j < kCodeIns; ++j)
         __builtin_amdgcn_global_load_lds(csrc[j] + (int64_t)tc * cstep[j],
                                          (__attribute__((address_space(3))) void*)(mycodes + (slot * kCodeIns + j) * kWave),
                                          4, 0, 0);
+    }
+    if constexpr (kCodeIns > 0 && CH == 4) {
+      if (sl) {
+        const int c = tc / CH;
+#pragma unroll
+        for (int j = 0; j < kCodeIns; ++j)
+          dma16(csrc[j] + (int64_t)c * CH * cstep[j],
+                reinterpret_cast<uint8_t*>(mycodes + ((c & 1) * kCodeIns + j) * kWave * CH));
+      }
     }
     if (xl) {
       const int c = tc / G;
@@ -335,22 +349,24 @@ __global__ __launch_bounds__(kWaves * kWave, FN == 1 && KS == 1 ? 2 : 1) void fp
     const uint32_t xbase = lds_u32(xbuf + ((s / G) & 1) * kXChunk + part * kXPart) + (uint32_t)((s % G) * kPairK);
     uint32_t wc[FN], xc[FM];
     float bsc[FM];  // block-128: sa[m, kb] sb[n / 128, kb] of this lane's row of tile j
+    // Scale entry e of this stage: buffer base + e (4 CH) + 4 (s mod CH).
+    const uint32_t cb = CH == 1 ? lds_u32(reinterpret_cast<const uint8_t*>(mycodes + slot * kCodeIns * kWave))
+                                : lds_u32(reinterpret_cast<const uint8_t*>(mycodes + ((s / CH) & 1) * kCodeIns * kWave * CH)) +
+                                      4 * (s % CH);
     if constexpr (BLK) {
-      const uint32_t cb = lds_u32(reinterpret_cast<const uint8_t*>(mycodes + slot * kCodeIns * kWave));
       uint32_t ca[FM + 1], cv[FM + 1];
 #pragma unroll
-      for (int j = 0; j < FM; ++j) ca[j] = cb + 4 * (32 * j + frow);
-      ca[FM] = cb + 4 * 32 * FM;
+      for (int j = 0; j < FM; ++j) ca[j] = cb + 4 * CH * (32 * j + frow);
+      ca[FM] = cb + 4 * CH * 32 * FM;
       code_reads<FM + 1>(cv, ca);
 #pragma unroll
       for (int j = 0; j < FM; ++j) bsc[j] = __builtin_bit_cast(float, cv[j]) * __builtin_bit_cast(float, cv[FM]);
     }
     v16f part[BLK ? FN : 1][BLK ? FM : 1];
     if constexpr (MX) {
-      const uint32_t cb = lds_u32(reinterpret_cast<const uint8_t*>(mycodes + slot * kCodeIns * kWave)) + 4 * frow;
       uint32_t ca[FN + FM];
 #pragma unroll
-      for (int i = 0; i < FN + FM; ++i) ca[i] = cb + 128 * i;
+      for (int i = 0; i < FN + FM; ++i) ca[i] = cb + 4 * CH * (32 * i + frow);
       uint32_t cv[FN + FM];
       code_reads<FN + FM>(cv, ca);
 #pragma unroll
@@ -406,7 +422,7 @@ __global__ __launch_bounds__(kWaves * kWave, FN == 1 && KS == 1 ? 2 : 1) void fp
   };
 
 #pragma unroll
-  for (int d = 0; d < D - 1; ++d) issue(d, d, d % G == 0);
+  for (int d = 0; d < D - 1; ++d) issue(d, d, d % G == 0, d % CH == 0);
   // Step s: wait for stage s (its activation chunk too), at a chunk start a barrier,
   // refill slot (s - 1) % D with stage s + D - 1, compute stage s. The main loop runs
   // whole rounds of U steps with no exit inside; the remainder runs after it.
@@ -414,7 +430,7 @@ __global__ __launch_bounds__(kWaves * kWave, FN == 1 && KS == 1 ? 2 : 1) void fp
     constexpr int u = decltype(uc)::value;
     wait_vmcnt<wait_after(u % G)>();
     if (u % G == 0) __builtin_amdgcn_s_barrier();
-    issue((u + D - 1) % D, s + D - 1, (u + D - 1) % G == 0);
+    issue((u + D - 1) % D, s + D - 1, (u + D - 1) % G == 0, (u + D - 1) % CH == 0);
     compute(u % D, s);
   };
   int s0 = 0;
@@ -480,9 +496,9 @@ struct SkPlan {
   int fn, fm, ks, g, split;
   int64_t kps;
 };
-constexpr int64_t skinny_lds(int fn, int fm, int ks, int g, int sm) {
+constexpr int64_t skinny_lds(int fn, int fm, int ks, int g, int sm, int ch = 1) {
   return (int64_t)kWaves * kDepth * 4096 * fn + 2LL * ks * 32 * fm * kPairK * g +
-         (int64_t)kWaves * kDepth * scale_ins(sm, fn, fm) * kWave * 4;
+         (int64_t)kWaves * (ch == 1 ? kDepth : 2) * scale_ins(sm, fn, fm) * kWave * 4 * ch;
 }
 SkPlan skinny_plan(int64_t M, int64_t N, int64_t K, int sm) {
   SkPlan p{};
@@ -542,38 +558,58 @@ SkPlan skinny_plan(int64_t M, int64_t N, int64_t K, int sm) {
   return p;
 }
 
-template <int SM, int FN, int FM, int KS>
-bool launch_g(const SkPlan& p, const KArgs& ka, hipStream_t st) {
+template <int SM, int FN, int FM, int KS, int CH>
+bool launch_gc(const SkPlan& p, const KArgs& ka, hipStream_t st) {
   const dim3 grid((unsigned)cdiv(ka.g.N, 32 * FN * (kWaves / KS)), (unsigned)p.split), block(kWaves * kWave);
-  if constexpr (skinny_lds(FN, FM, KS, 2, SM) <= 160 * 1024) {
+  if constexpr (skinny_lds(FN, FM, KS, 2, SM, CH) <= 160 * 1024) {
     if (p.g == 2) {
-      hipLaunchKernelGGL((fp8_skinny_kernel<SM, FN, FM, KS, 2>), grid, block, 0, st, ka);
+      hipLaunchKernelGGL((fp8_skinny_kernel<SM, FN, FM, KS, 2, CH>), grid, block, 0, st, ka);
       return true;
     }
   }
-  if constexpr (KS * FM == 1 && skinny_lds(FN, FM, KS, 4, SM) <= 160 * 1024) {
+  if constexpr (KS * FM == 1 && skinny_lds(FN, FM, KS, 4, SM, CH) <= 160 * 1024) {
     if (p.g == 4) {
-      hipLaunchKernelGGL((fp8_skinny_kernel<SM, FN, FM, KS, 4>), grid, block, 0, st, ka);
+      hipLaunchKernelGGL((fp8_skinny_kernel<SM, FN, FM, KS, 4, CH>), grid, block, 0, st, ka);
       return true;
     }
   }
   return false;
 }
+template <int SM, int FN, int FM, int KS>
+bool launch_g(const SkPlan& p, const KArgs& ka, hipStream_t st, int ch) {
+  if (ch == 4) return launch_gc<SM, FN, FM, KS, 4>(p, ka, st);
+  return launch_gc<SM, FN, FM, KS, 1>(p, ka, st);
+}
 
 template <int SM>
-bool launch_sm(const SkPlan& p, const KArgs& ka, hipStream_t st) {
+bool launch_sm(const SkPlan& p, const KArgs& ka, hipStream_t st, int ch) {
   const int key = p.fn * 100 + p.fm * 10 + p.ks;
   switch (key) {
-    case 211: return launch_g<SM, 2, 1, 1>(p, ka, st);
-    case 221: return launch_g<SM, 2, 2, 1>(p, ka, st);
-    case 111: return launch_g<SM, 1, 1, 1>(p, ka, st);
-    case 121: return launch_g<SM, 1, 2, 1>(p, ka, st);
-    case 214: return launch_g<SM, 2, 1, 4>(p, ka, st);
-    case 112: return launch_g<SM, 1, 1, 2>(p, ka, st);
-    case 122: return launch_g<SM, 1, 2, 2>(p, ka, st);
-    case 114: return launch_g<SM, 1, 1, 4>(p, ka, st);
+    case 211: return launch_g<SM, 2, 1, 1>(p, ka, st, ch);
+    case 221: return launch_g<SM, 2, 2, 1>(p, ka, st, ch);
+    case 111: return launch_g<SM, 1, 1, 1>(p, ka, st, ch);
+    case 121: return launch_g<SM, 1, 2, 1>(p, ka, st, ch);
+    case 214: return launch_g<SM, 2, 1, 4>(p, ka, st, ch);
+    case 112: return launch_g<SM, 1, 1, 2>(p, ka, st, ch);
+    case 122: return launch_g<SM, 1, 2, 2>(p, ka, st, ch);
+    case 114: return launch_g<SM, 1, 1, 4>(p, ka, st, ch);
     default: return false;
   }
+}
+
+// Stages per scale load: 4 (one 16-byte load per scale row) when every row of scales is
+// 16-byte aligned at each part's first stage and a part's stages come in whole fours, and
+// the extra LDS keeps the plan's workgroups per CU; else 1. Block-128 needs row-major
+// activation scales (a row's blocks contiguous).
+int scale_chunk(const SkinnyFp8Args& g, const SkPlan& p) {
+  if (g.mode == kSmScaled) return 1;
+  const int64_t plen = p.kps / p.ks;
+  if (plen % (4 * kPairK) || (reinterpret_cast<uintptr_t>(g.sa) & 15) || (reinterpret_cast<uintptr_t>(g.sb) & 15)) return 1;
+  if (g.mode == kSmMx && (g.ld_sa % 16 || g.ld_sb % 16)) return 1;
+  if (g.mode == kSmBlock && (g.sa_vec || g.ld_sa % 4 || g.ld_sb % 4)) return 1;
+  const int64_t l1 = skinny_lds(p.fn, p.fm, p.ks, p.g, g.mode, 1), l4 = skinny_lds(p.fn, p.fm, p.ks, p.g, g.mode, 4);
+  if (l4 > 160 * 1024 || (l1 <= 80 * 1024 && l4 > 80 * 1024)) return 1;
+  return 4;
 }
 
 }  // namespace
@@ -609,9 +645,10 @@ int skinny_fp8_launch(const SkinnyFp8Args& g, hipStream_t st, const char* op) {
       return fail(AYK_EWORKSPACE, "%s: workspace of %zu bytes required, %zu given", op, need, g.ws_bytes);
   }
   KArgs ka{g, p.kps};
-  const bool launched = g.mode == kSmMx      ? launch_sm<kSmMx>(p, ka, st)
-                        : g.mode == kSmBlock ? launch_sm<kSmBlock>(p, ka, st)
-                                             : launch_sm<kSmScaled>(p, ka, st);
+  const int ch = scale_chunk(g, p);
+  const bool launched = g.mode == kSmMx      ? launch_sm<kSmMx>(p, ka, st, ch)
+                        : g.mode == kSmBlock ? launch_sm<kSmBlock>(p, ka, st, ch)
+                                             : launch_sm<kSmScaled>(p, ka, st, ch);
   if (!launched) return fail(AYK_EINVAL, "%s: no decode-batch kernel for this plan", op);
   if (int rc = check_launch(op)) return rc;
   if (p.split > 1) {

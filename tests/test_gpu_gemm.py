@@ -201,10 +201,12 @@ def test_fp8_scaled_mm_decode_batch(gpu, m, n, k, rowwise, out_dtype):
 
 
 @pytest.mark.parametrize("m,n,k", [(2, 520, 2048), (40, 1000, 3072), (9, 20000, 1024), (64, 4100, 8192),
-                                   (64, 2048, 28672), (30, 57344, 512)])
+                                   (64, 2048, 28672), (30, 57344, 512),
+                                   (8, 3000, 1280)])  # K not in whole 512-K chunks: one code load per stage
 def test_mxfp8_scaled_mm_decode_batch(gpu, m, n, k):
-    """MXFP8 decode batches: the UE8M0 code dwords of each 128-K pair staged with the
-    operands; K parts and grid splits start their codes at their own K offset."""
+    """MXFP8 decode batches: the UE8M0 code dwords staged with the operands, four 128-K
+    pairs per 16-byte load where the code rows allow it; K parts and grid splits start
+    their codes at their own K offset."""
     from ayaka.kernel.hip import mxfp8_scaled_mm
 
     _say(f"mxfp8_scaled_mm decode batch m={m} n={n} k={k}")
