@@ -222,6 +222,45 @@ def test_mxfp8_scaled_mm_decode_batch(gpu, m, n, k):
     assert_linear_close(y, ref, "mxfp8_scaled_mm decode batch")
 
 
+def _offset_view(t: torch.Tensor, offset_elems: int) -> torch.Tensor:
+    """A contiguous copy of `t` that starts `offset_elems` elements into its buffer (a
+    pointer aligned to the element size but not to 16 bytes)."""
+    buf = torch.empty(t.numel() + offset_elems, dtype=t.dtype, device=t.device)
+    view = buf[offset_elems:].view(t.shape)
+    view.copy_(t)
+    assert view.is_contiguous() and view.data_ptr() % 16 != 0
+    return view
+
+
+def test_decode_batch_scales_not_16_byte_aligned(gpu):
+    """Scale rows that are not 16-byte aligned take the one-load-per-stage path of the
+    decode-batch kernel (the four-stage 16-byte loads need aligned rows): MXFP8 codes
+    4 bytes into their buffer, block-128 activation scales one float in."""
+    from ayaka.kernel.hip import fp8_blockwise_mm, mxfp8_scaled_mm
+
+    _say("decode batch, scale rows off 16-byte alignment")
+    m, n, k = 9, 20000, 1024
+    torch.manual_seed(81)
+    x = torch.distributions.StudentT(3.0).sample((m, k))
+    wf = torch.randn(n, k, generator=_gen(82))
+    qa, ca = ora.per_token_group_quant_mxfp8(x, 32)
+    qw, cw = ora.per_token_group_quant_mxfp8(wf, 32)
+    ref = ora.mxfp8_scaled_mm(qa, ca, qw, cw)
+    y = mxfp8_scaled_mm(qa.to(gpu), _offset_view(ca.to(gpu), 4), qw.to(gpu), _offset_view(cw.to(gpu), 4),
+                        out=torch.empty(m, n, dtype=torch.bfloat16, device=gpu))
+    assert_linear_close(y, ref, "mxfp8 decode batch, offset codes")
+
+    m, n, k = 32, 4096, 2048
+    kb, nb = k // 128, n // 128
+    a = _fp8((m, k), seed=83, scale=30)
+    w = _fp8((n, k), seed=84, scale=30)
+    sa = torch.exp(torch.rand(m, kb, generator=_gen(85)) * -6.9).float()
+    sb = torch.exp(torch.rand(nb, kb, generator=_gen(86)) * -6.9).float()
+    ref = ora.fp8_blockwise_mm(a, w, sa, sb, None, False)
+    out = fp8_blockwise_mm(a.to(gpu), w.to(gpu), _offset_view(sa.to(gpu), 1), _offset_view(sb.to(gpu), 1))
+    assert_linear_close(out, ref, "blockwise decode batch, offset scales")
+
+
 # 276 tiles of 256 x 256: one whole round, then a last round of 20 tiles that the pair
 # kernel splits over K (three 512-K pieces each) into the workspace, ragged M and N.
 TAIL_MNK = (1300, 11712, 1536)
