@@ -66,6 +66,18 @@ def _compile(hipcc: str, src: pathlib.Path) -> pathlib.Path:
     return obj
 
 
+def _check_resolves(lib: pathlib.Path) -> None:
+    """Load the linked library with every symbol bound now. A kernel template whose host
+    side fails to instantiate leaves its launch stub undefined without a compile error;
+    the library then links but cannot be loaded."""
+    import ctypes
+
+    try:
+        ctypes.CDLL(str(lib), mode=os.RTLD_NOW | os.RTLD_LOCAL)
+    except OSError as err:
+        raise RuntimeError(f"{lib.name} does not load: {err}") from err
+
+
 def build(verbose: bool = False) -> pathlib.Path:
     """Compile every ``csrc/*.hip`` for gfx950 and link ``libayaka_fp8.so``."""
     hipcc = _hipcc()
@@ -82,6 +94,7 @@ def build(verbose: bool = False) -> pathlib.Path:
     proc = subprocess.run(cmd, capture_output=True, text=True)
     if proc.returncode != 0:
         raise RuntimeError(f"link failed:\n{proc.stderr}")
+    _check_resolves(tmp)
     os.replace(tmp, target)
     if verbose:
         print(f"built {target}")
