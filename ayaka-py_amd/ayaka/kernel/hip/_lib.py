@@ -52,6 +52,7 @@ _f = ctypes.c_float
 #: name -> argtypes (restype int unless listed in _RESTYPES)
 SIGNATURES: dict[str, list[Any]] = {
     "ayk_last_error": [],
+    "ayk_last_plan": [],
     "ayk_abi_version": [],
     "ayk_device_supported": [_i],
     "ayk_per_token_quant_fp8": [_p, _i, _l, _l, _l, _p, _l, _p, _p],
@@ -80,6 +81,7 @@ SIGNATURES: dict[str, list[Any]] = {
 }
 _RESTYPES: dict[str, Any] = {
     "ayk_last_error": ctypes.c_char_p,
+    "ayk_last_plan": ctypes.c_char_p,
     "ayk_fp8_weight_only_gemv_workspace_bytes": _z,
     "ayk_fp8_blockwise_gemv_workspace_bytes": _z,
     "ayk_fp8_blockwise_mm_workspace_bytes": _z,
@@ -155,6 +157,11 @@ def call(name: str, *args: Any) -> None:
     if status == AYK_EINVAL:
         raise ValueError(message)
     raise RuntimeError(f"{name} failed ({status}): {message}")
+
+
+def last_plan() -> str:
+    """The kernels (and K split) of the last GEMM launch on this thread."""
+    return (load_library().ayk_last_plan() or b"").decode("utf-8", "replace")
 
 
 def query(name: str, *args: Any) -> int:

@@ -50,6 +50,9 @@ _LAYER_ONLY_ATTRS = frozenset(
     {"output_partition_sizes", "input_size_per_partition", "input_size", "output_size", "params_dtype", "device"}
 )
 
+#: non-persistent buffer holding an fp32 copy of a bf16 block-128 weight-scale table
+_BLOCK_SCALE_F32 = "_fp8_block_scale_f32"
+
 _SCALE_DTYPE_NAMES = {torch.uint8: "e8m0", torch.float32: "float32", torch.bfloat16: "bfloat16"}
 
 
@@ -178,6 +181,8 @@ def _scale_loader(layer: nn.Module, parameter: torch.Tensor, loaded_weight: torc
         raise TypeError("parameter must be a torch.Tensor")
     if loaded_weight.is_meta:
         raise WeightLoadError("scale loading requires a materialized checkpoint tensor")
+    if getattr(layer, _BLOCK_SCALE_F32, None) is not None:
+        setattr(layer, _BLOCK_SCALE_F32, None)  # stale once the scale parameter is written
     destination = _scale_destination(layer, parameter.data, loaded_weight, shard_id)
     if destination is None:
         parameter.data.copy_(loaded_weight)
@@ -325,8 +330,22 @@ class FP8BlockLinearMethod(_FP8LinearMethodBase):
     def _rows_per_scale(self, input_size):
         return BLOCK128
 
+    def process_weights_after_loading(self, layer: nn.Module) -> None:
+        super().process_weights_after_loading(layer)
+        # The W8A8 GEMM's decode-batch kernel (M <= 64) reads fp32 block scales. A bf16
+        # table widens to fp32 exactly, so a widened copy, made once here, gives the same
+        # products; the parameter itself keeps the checkpoint's dtype. The scale loader
+        # drops the copy whenever it writes the parameter again.
+        scale = layer.weight_scale_inv
+        layer.register_buffer(_BLOCK_SCALE_F32, scale.detach().float() if scale.dtype != torch.float32 else None,
+                              persistent=False)
+
     def _run(self, layer, x, bias):
-        return fp8_block_linear(x, layer.weight, layer.weight_scale_inv, bias)
+        scale = layer.weight_scale_inv
+        widened = getattr(layer, _BLOCK_SCALE_F32, None)
+        if widened is not None and x.numel() > x.shape[-1]:  # M > 1: the W8A8 GEMM
+            scale = widened
+        return fp8_block_linear(x, layer.weight, scale, bias)
 
 
 class FP8W8A16LinearMethod(_FP8LinearMethodBase):

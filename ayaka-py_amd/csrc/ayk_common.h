@@ -306,5 +306,8 @@ inline bool aligned16(const void* p) { return (reinterpret_cast<uintptr_t>(p) & 
 int fail(int status, const char* fmt, ...);
 int check_launch(const char* what);
 int check_device();
+// Records which kernels and split the last GEMM launch on this thread used (read back
+// through ayk_last_plan; tests assert that a case reaches the kernel it targets).
+void note_plan(const char* fmt, ...);
 
 }  // namespace ayk

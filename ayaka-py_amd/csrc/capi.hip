@@ -8,6 +8,7 @@
 namespace ayk {
 
 static thread_local char g_last_error[512] = "";
+static thread_local char g_last_plan[160] = "";
 
 int fail(int status, const char* fmt, ...) {
   va_list args;
@@ -15,6 +16,13 @@ int fail(int status, const char* fmt, ...) {
   vsnprintf(g_last_error, sizeof(g_last_error), fmt, args);
   va_end(args);
   return status;
+}
+
+void note_plan(const char* fmt, ...) {
+  va_list args;
+  va_start(args, fmt);
+  vsnprintf(g_last_plan, sizeof(g_last_plan), fmt, args);
+  va_end(args);
 }
 
 int check_launch(const char* what) {
@@ -58,6 +66,8 @@ int check_device() {
 extern "C" {
 
 const char* ayk_last_error(void) { return ayk::g_last_error; }
+
+const char* ayk_last_plan(void) { return ayk::g_last_plan; }
 
 int ayk_abi_version(void) { return 100; }
 

@@ -1571,6 +1571,7 @@ int launch_pair_tail(GemmArgs g, int64_t tiles, hipStream_t st, const char* op) 
   g.kps = 0;
   g.dp_tiles = tp.dp_tiles;
   g.tail_split = tp.split;
+  note_plan("pair tail=%d", tp.split);
   if (tp.split == 1) {
     hipLaunchKernelGGL((fp8_gemm_pair_kernel<MODE>), dim3((unsigned)tiles), dim3(kThreads), 0, st, g);
     return check_launch(op);
@@ -1607,11 +1608,13 @@ int launch_big(GemmArgs g, hipStream_t st, const char* op) {
           return fail(AYK_EWORKSPACE, "%s: workspace of %zu bytes required, %zu given", op, need, g.ws_bytes);
       }
       if (split == 1) return launch_pair_tail<MODE>(g, tiles, st, op);
+      note_plan("pair split=%d", (int)split);
       hipLaunchKernelGGL((fp8_gemm_pair_kernel<MODE>), dim3((unsigned)tiles, (unsigned)split), dim3(kThreads), 0, st, g);
       if (int rc = check_launch(op)) return rc;
       hipLaunchKernelGGL(block_split_reduce, dim3((unsigned)cdiv(g.M * g.N, 256)), dim3(256), 0, st, g.ws, g.M, g.N,
                          (int)split, g.bias, g.bias_dtype, g.out, g.out_dtype, g.ldo);
     } else {
+      note_plan("mx128");
       hipLaunchKernelGGL((fp8_gemm_mx128_kernel<MODE>), dim3((unsigned)tiles), dim3(kThreads), 0, st, g);
     }
   } else if (g.K % (2 * kBigK) == 0) {
@@ -1625,6 +1628,7 @@ int launch_big(GemmArgs g, hipStream_t st, const char* op) {
       g.kps = scaled_kps(g.K, split);
     }
     if (split == 1 && MODE == MODE_SCALED) return launch_pair_tail<MODE>(g, tiles, st, op);
+    note_plan("pair split=%d", (int)split);
     hipLaunchKernelGGL((fp8_gemm_pair_kernel<MODE>), dim3((unsigned)tiles, (unsigned)split), dim3(kThreads), 0, st, g);
     if (split > 1) {
       if (int rc = check_launch(op)) return rc;
@@ -1632,6 +1636,7 @@ int launch_big(GemmArgs g, hipStream_t st, const char* op) {
                          (int)split, g.bias, g.bias_dtype, g.out, g.out_dtype, g.ldo);
     }
   } else {
+    note_plan("big");
     hipLaunchKernelGGL((fp8_gemm_big_kernel<MODE>), dim3((unsigned)tiles), dim3(kThreads), 0, st, g);
   }
   return check_launch(op);
@@ -1642,6 +1647,7 @@ int launch_block_big(GemmArgs g, hipStream_t st, const char* op) {
   const int64_t tiles = (int64_t)g.tiles_m * cdiv(g.N, kBlkTile);
   if (tiles > 0x7FFFFFFF) return fail(AYK_EINVAL, "%s: problem too large", op);
   const int64_t split = block_split(g.M, g.N, g.K);
+  note_plan("block128 split=%d", (int)split);
   if (split == 1) {
     hipLaunchKernelGGL(fp8_gemm_block_kernel, dim3((unsigned)tiles), dim3(kBlkThreads), 0, st, g);
     return check_launch(op);
@@ -1671,6 +1677,7 @@ int launch_cfg(GemmArgs g, hipStream_t st, const char* op) {
       return fail(AYK_EWORKSPACE, "%s: workspace of %zu bytes required, %zu given", op, need, g.ws_bytes);
     g.kps = MODE == MODE_BLOCK ? g.K / split : scaled_kps(g.K, split);
   }
+  note_plan("general %dx%d split=%d", BM, BN, (int)split);
   hipLaunchKernelGGL((fp8_gemm_kernel<MODE, BN, BM, WN, WM>), dim3((unsigned)tiles, (unsigned)split), dim3(kThreads), 0, st, g);
   if (int rc = check_launch(op)) return rc;
   if (split > 1) {

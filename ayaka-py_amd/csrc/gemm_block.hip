@@ -564,6 +564,7 @@ int block256_launch(const Block256Args& g, hipStream_t st, const char* op) {
   const int64_t tiles = (int64_t)tiles_m * cdiv(g.N, kTile);
   if (tiles > 0x7FFFFFFF) return fail(AYK_EINVAL, "%s: problem too large", op);
   const int64_t split = block256_split(g.M, g.N, g.K);
+  note_plan("block256 split=%d", (int)split);
   if (split == 1) {
     hipLaunchKernelGGL(fp8_block256_kernel, dim3((unsigned)tiles), dim3(kThreads), 0, st, g, tiles_m, (int64_t)0);
     return check_launch(op);
@@ -583,6 +584,7 @@ int grouped_block256_launch(const Grouped256Args& ga, hipStream_t st, const char
   // Upper bound on the tiles: every expert adds at most one partial 256-row tile.
   const int64_t bound = cdiv((cdiv(ga.m_total, kTile) + ga.num_experts) * cdiv(ga.n, kTile), 128) * 128;
   if (bound > 0x7FFFFFFF) return fail(AYK_EINVAL, "%s: problem too large", op);
+  note_plan("grouped_block256");
   hipLaunchKernelGGL(fp8_grouped_block256_kernel, dim3((unsigned)bound), dim3(kThreads), 0, st, ga);
   return check_launch(op);
 }

@@ -646,6 +646,7 @@ int skinny_fp8_launch(const SkinnyFp8Args& g, hipStream_t st, const char* op) {
   }
   KArgs ka{g, p.kps};
   const int ch = scale_chunk(g, p);
+  note_plan("skinny fn=%d fm=%d ks=%d g=%d ch=%d split=%d", p.fn, p.fm, p.ks, p.g, ch, (int)p.split);
   const bool launched = g.mode == kSmMx      ? launch_sm<kSmMx>(p, ka, st, ch)
                         : g.mode == kSmBlock ? launch_sm<kSmBlock>(p, ka, st, ch)
                                              : launch_sm<kSmScaled>(p, ka, st, ch);

@@ -49,6 +49,13 @@ typedef enum ayk_status {
 /* Message of the last failing call on this thread ("" if none). */
 const char* ayk_last_error(void);
 
+/* Which kernels (and K split) the last GEMM launch on this thread ran, e.g.
+ * "skinny fn=2 fm=2 ks=1 g=2 ch=4 split=1" or "pair tail=4": a diagnostic string,
+ * not a stable format. No counterpart in the reference (its Triton launches pick
+ * configurations inside Triton's autotuner); tests and profilers read it to assert
+ * that a shape reaches the kernel it targets. */
+const char* ayk_last_plan(void);
+
 /* Library ABI version (major * 100 + minor). */
 int ayk_abi_version(void);
 

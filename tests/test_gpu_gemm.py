@@ -6,6 +6,7 @@ floor 1e-3 of the output scale). Shapes cover tile tails in M, N and K, the
 padded-K path, every scale dtype, and decode M in {1, 4, 16, 32}.
 """
 
+import re
 import sys
 
 import pytest
@@ -25,6 +26,13 @@ def _say(msg: str) -> None:
 
 def _gen(seed: int) -> torch.Generator:
     return torch.Generator().manual_seed(seed)
+
+
+def _plan() -> str:
+    """Kernels and split of the last GEMM launch (the library's own record)."""
+    from ayaka.kernel.hip import _lib
+
+    return _lib.last_plan()
 
 
 def _fp8(shape, seed, scale=1.0):
@@ -196,6 +204,7 @@ def test_fp8_scaled_mm_decode_batch(gpu, m, n, k, rowwise, out_dtype):
     buf = torch.full((m, n + 6), 7.0, dtype=out_dtype, device=gpu)  # row stride n + 6
     out = buf[:, :n]
     fp8_scaled_mm(a.to(gpu), w.to(gpu).t(), sa.to(gpu), sb.to(gpu), bias.to(gpu), out=out)
+    assert _plan().startswith("skinny"), f"decode batch ran {_plan()!r}"
     assert_linear_close(out, ref, "fp8_scaled_mm decode batch")
     assert torch.all(buf[:, n:].float() == 7.0), "wrote past the output columns"
 
@@ -219,6 +228,7 @@ def test_mxfp8_scaled_mm_decode_batch(gpu, m, n, k):
     ref = ora.mxfp8_scaled_mm(qa, ca, qw, cw, bias)
     y = mxfp8_scaled_mm(qa.to(gpu), ca.to(gpu), qw.to(gpu), cw.to(gpu), bias.to(gpu),
                         out=torch.empty(m, n, dtype=torch.bfloat16, device=gpu))
+    assert _plan().startswith("skinny"), f"decode batch ran {_plan()!r}"
     assert_linear_close(y, ref, "mxfp8_scaled_mm decode batch")
 
 
@@ -248,6 +258,7 @@ def test_decode_batch_scales_not_16_byte_aligned(gpu):
     ref = ora.mxfp8_scaled_mm(qa, ca, qw, cw)
     y = mxfp8_scaled_mm(qa.to(gpu), _offset_view(ca.to(gpu), 4), qw.to(gpu), _offset_view(cw.to(gpu), 4),
                         out=torch.empty(m, n, dtype=torch.bfloat16, device=gpu))
+    assert _plan().startswith("skinny") and "ch=1" in _plan(), _plan()
     assert_linear_close(y, ref, "mxfp8 decode batch, offset codes")
 
     m, n, k = 32, 4096, 2048
@@ -258,6 +269,7 @@ def test_decode_batch_scales_not_16_byte_aligned(gpu):
     sb = torch.exp(torch.rand(nb, kb, generator=_gen(86)) * -6.9).float()
     ref = ora.fp8_blockwise_mm(a, w, sa, sb, None, False)
     out = fp8_blockwise_mm(a.to(gpu), w.to(gpu), _offset_view(sa.to(gpu), 1), _offset_view(sb.to(gpu), 1))
+    assert _plan().startswith("skinny") and "ch=1" in _plan(), _plan()
     assert_linear_close(out, ref, "blockwise decode batch, offset scales")
 
 
@@ -465,6 +477,7 @@ def test_fp8_blockwise_mm_split_k(gpu, m, n, k, col_major, sdt, with_bias):
     ref = ora.fp8_blockwise_mm(a, w, sa_arg, sb, bias, col_major)
     out = fp8_blockwise_mm(a.to(gpu), w.to(gpu), sa_arg.to(gpu), sb.to(gpu),
                            bias.to(gpu) if bias is not None else None, a_scale_col_major=col_major)
+    assert not re.search(r"split=1\b", _plan()) and not _plan().startswith("skinny"), _plan()
     assert_linear_close(out, ref, "blockwise_mm split-K")
 
 
@@ -492,7 +505,95 @@ def test_fp8_blockwise_mm_decode_batch(gpu, m, n, k, col_major, with_bias):
     ref = ora.fp8_blockwise_mm(a, w, sa_arg, sb, bias, col_major)
     out = fp8_blockwise_mm(a.to(gpu), w.to(gpu), sa_arg.to(gpu), sb.to(gpu),
                            bias.to(gpu) if bias is not None else None, a_scale_col_major=col_major)
+    assert _plan().startswith("skinny"), f"decode batch ran {_plan()!r}"
     assert_linear_close(out, ref, "blockwise_mm decode batch")
+
+
+# Decode-batch plans that a case must reach, named by the library's launch record:
+# (mode, M, N, K, expected plan). Rows per wavefront 32 FN, activation tiles FM, K parts
+# KS, G pairs per activation chunk, CH stages per scale load, grid split. The FN = 2 /
+# KS = 4 plan needs more than 160 KB of LDS with a scale ring, so only fp32 per-row /
+# per-tensor scales (mode "scaled") reach it.
+DECODE_PLANS = [
+    ("block", 64, 18432, 7168, "skinny fn=1 fm=2 ks=1 g=2 ch=4 split=1"),  # DeepSeek-V3 up at M = 64
+    ("block", 64, 7168, 18432, "skinny fn=1 fm=2 ks=1 g=2 ch=4 split=4"),  # DeepSeek-V3 down at M = 64
+    ("block", 48, 4096, 2048, "skinny fn=1 fm=2 ks=2 g=2 ch=4 split=1"),
+    ("block", 16, 14000, 1024, "skinny fn=1 fm=1 ks=2 g=2 ch=4 split=1"),
+    ("mx", 64, 14000, 1024, "skinny fn=1 fm=2 ks=2 g=2 ch=4 split=1"),
+    ("mx", 20, 13000, 1024, "skinny fn=1 fm=1 ks=2 g=2 ch=4 split=1"),
+    ("scaled", 8, 14000, 1024, "skinny fn=2 fm=1 ks=4 g=2 ch=1 split=1"),
+    ("scaled", 24, 12800, 1024, "skinny fn=2 fm=1 ks=4 g=2 ch=1 split=1"),
+]
+
+
+@pytest.mark.parametrize("mode,m,n,k,plan", DECODE_PLANS, ids=[f"{c[0]}-{c[1]}x{c[2]}x{c[3]}" for c in DECODE_PLANS])
+def test_decode_batch_plans(gpu, mode, m, n, k, plan):
+    """Each case reaches its decode-batch plan (asserted on the launch record) and
+    matches the oracle: two activation tiles on the four-stage 16-byte scale path, and
+    the four-K-part 64-row plan."""
+    from ayaka.kernel.hip import fp8_blockwise_mm, fp8_scaled_mm, mxfp8_scaled_mm
+
+    _say(f"decode-batch plan {mode} m={m} n={n} k={k}: {plan}")
+    if mode == "block":
+        kb, nb = k // 128, -(-n // 128)
+        a = _fp8((m, k), seed=m + 91, scale=30)
+        w = _fp8((n, k), seed=n + 92, scale=30)
+        sa = torch.exp(torch.rand(m, kb, generator=_gen(93)) * -6.9).float()
+        sb = torch.exp(torch.rand(nb, kb, generator=_gen(94)) * -6.9).float()
+        bias = (torch.randn(n, generator=_gen(95)) * 5).to(torch.bfloat16)
+        ref = ora.fp8_blockwise_mm(a, w, sa, sb, bias, False)
+        out = fp8_blockwise_mm(a.to(gpu), w.to(gpu), sa.to(gpu), sb.to(gpu), bias.to(gpu))
+    elif mode == "mx":
+        torch.manual_seed(m + n)
+        qa, ca = ora.per_token_group_quant_mxfp8(torch.distributions.StudentT(3.0).sample((m, k)), 32)
+        qw, cw = ora.per_token_group_quant_mxfp8(torch.randn(n, k, generator=_gen(96)), 32)
+        ref = ora.mxfp8_scaled_mm(qa, ca, qw, cw)
+        out = mxfp8_scaled_mm(qa.to(gpu), ca.to(gpu), qw.to(gpu), cw.to(gpu),
+                              out=torch.empty(m, n, dtype=torch.bfloat16, device=gpu))
+    else:
+        a = _fp8((m, k), seed=m + 97, scale=40)
+        w = _fp8((n, k), seed=n + 98, scale=40)
+        sa = torch.rand(m, generator=_gen(99)) * 0.01 + 1e-3
+        sb = torch.rand(n, generator=_gen(100)) * 0.01 + 1e-3
+        ref = ora.fp8_scaled_mm(a, w, sa, sb)
+        out = fp8_scaled_mm(a.to(gpu), w.to(gpu).t(), sa.to(gpu), sb.to(gpu),
+                            out=torch.empty(m, n, dtype=torch.bfloat16, device=gpu))
+    assert _plan() == plan, f"expected {plan!r}, ran {_plan()!r}"
+    assert_linear_close(out, ref, f"decode-batch plan {mode} {m}x{n}x{k}")
+
+
+@pytest.mark.parametrize("m", [32, 64])
+def test_block128_default_bf16_scales_reach_decode_batch_kernel(gpu, m):
+    """A block-128 layer with the default bf16 weight-scale table (the reference's
+    ``scale_format`` default) runs the decode-batch kernel at M <= 64: the method widens
+    the table to fp32 once after loading. Same products as the bf16 table."""
+    from torch import nn
+
+    from ayaka.layers.linear.fp8 import FP8Config
+
+    n, k = 4096, 7168
+    _say(f"block-128 layer, default bf16 scales, m={m}")
+    wf = torch.randn(n, k, generator=_gen(101)) * 0.02
+    s = (wf.reshape(n // 128, 128, k // 128, 128).abs().amax(dim=(1, 3)) / 448).to(torch.bfloat16)
+    w = (wf / s.float().repeat_interleave(128, 0).repeat_interleave(128, 1)).to(FP8)
+    method = FP8Config.from_config({"weight_block_size": [128, 128]}).get_quant_method(None, "model.layers.0.mlp.up_proj")
+    layer = nn.Module()
+    method.create_weights(layer, output_partition_sizes=[n], input_size_per_partition=k, device=gpu)
+    assert layer.weight_scale_inv.dtype == torch.bfloat16
+    layer.weight.data.copy_(w.to(gpu))
+    layer.weight_scale_inv.weight_loader(layer, layer.weight_scale_inv, s.to(gpu))
+    method.process_weights_after_loading(layer)
+    x = torch.randn(m, k, generator=_gen(102)).to(torch.bfloat16)
+    y = method.apply(layer, x.to(gpu))
+    assert _plan().startswith("skinny"), f"default block-128 layer ran {_plan()!r}"
+    assert layer.weight_scale_inv.dtype == torch.bfloat16, "the parameter keeps the checkpoint dtype"
+    ref = ora.fp8_linear("w8a8_block128", x, w, s, None)
+    assert_linear_close(y, ref, f"default block-128 layer m={m}")
+    # Writing the scale again drops the widened copy; the next apply uses the new values.
+    layer.weight_scale_inv.weight_loader(layer, layer.weight_scale_inv, (s.float() * 2).to(torch.bfloat16).to(gpu))
+    method.process_weights_after_loading(layer)
+    y2 = method.apply(layer, x.to(gpu))
+    assert_linear_close(y2, ref * 2, f"default block-128 layer m={m}, rescaled")
 
 
 @pytest.mark.parametrize("m,n,k", [(1, 512, 1024), (1, 1000, 8192), (64, 256, 512), (100, 300, 1024), (512, 512, 2048), (33, 96, 96),

@@ -227,6 +227,9 @@ def test_fp8_config_method_selection():
         assert cfg.get_quant_method(None, "model.lm_head") is None
         assert cfg.get_quant_method(None, "model.lm_head.sub") is None
         assert cfg.get_capabilities().weight_bits == 8
+        # The reference reports {"cpu", "cuda"} (layers/linear/fp8.py:193); this package
+        # has no CPU path, so its methods report "cuda" only (a documented divergence).
+        assert cfg._make_method().get_capabilities().supported_devices == frozenset({"cuda"})
     assert L.FP8Config.from_config({"weight_block_size": [128, 128]}).scale_dtype is torch.bfloat16
     assert isinstance(L.FP8Config("w8a8_block128", scale_dtype=torch.float32)._make_method(), L.FP8BlockLinearMethod)
     with pytest.raises(L.CapabilityError):
