@@ -28,6 +28,8 @@
 #include "gemm_tiles.h"
 #include "gemm_util.h"
 
+#include <type_traits>
+
 namespace ayk {
 
 int mx_gemv(const void* a, const uint8_t* a_scale, const void* w, int64_t ldw,
@@ -76,6 +78,9 @@ struct GemmArgs {
   // K piece (b - dp_tiles) % tail_split of tile dp_tiles + (b - dp_tiles) / tail_split.
   int dp_tiles;
   int tail_split;
+  // 256 x 256 pair kernel: work items (tiles, plus tail pieces); a workgroup runs items
+  // blockIdx.x, blockIdx.x + gridDim.x, ...
+  int items;
 };
 
 __device__ inline v16f mfma(const v8i& wa, const v8i& ab, const v16f& c, int sw, int sa) {
@@ -432,7 +437,9 @@ struct BigScales {
 };
 template <int MODE>
 __device__ __attribute__((always_inline)) inline BigScales load_big_scales(const GemmArgs& g, int64_t m_tile, int64_t n_tile) {
-  const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+  int tid = threadIdx.x;
+  asm volatile("" : "+v"(tid));  // not hoisted out of the persistent kernel's item loop
+  const int lane = tid & 63, wave = tid >> 6;
   const int wn = wave >> 1, wm = wave & 1, h = lane >> 5, frow = lane & 31;
   BigScales sc;
 #pragma unroll
@@ -474,15 +481,23 @@ __device__ __attribute__((always_inline)) inline BigScales load_big_scales(const
 }
 
 
+// `nt`: final outputs are stored nontemporally, so that they do not take the L2 that
+// holds the next tiles' operand panels (Qwen2 gate_up at M = 4096: 625 -> 585 us); fp32
+// partials that a reduce reads back keep plain stores.
 template <int MODE, int OUT, bool BIAS>
 __device__ __attribute__((always_inline)) inline void big_epilogue_impl(const GemmArgs& g, const v16f (&acc)[4][4], const BigScales& sc,
-                                         int64_t m_tile, int64_t n_tile, uint8_t* stage_lds) {
+                                         int64_t m_tile, int64_t n_tile, uint8_t* stage_lds, bool nt) {
   constexpr int EB = OutBytes<OUT>::v;
   constexpr int kRowBytes = 256 * EB + 16;        // padded staging row
   constexpr int kStageRows = EB == 4 ? 32 : 64;   // rows staged at once (fits 64 KB)
   constexpr int kPasses = 64 / kStageRows;        // fp32: one pass per row half (wm)
   static_assert(kStageRows * kRowBytes <= kEpilogueLds, "staging tile must fit the first stage object");
-  const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+  // Lane addresses come from an opaque copy of the thread index: in the persistent pair
+  // kernel this code runs inside the item loop, and addresses hoisted out of it would
+  // stay live (and spill) through every K loop.
+  int tid = threadIdx.x;
+  asm volatile("" : "+v"(tid));
+  const int lane = tid & 63, wave = tid >> 6;
   const int wn = wave >> 1, wm = wave & 1, h = lane >> 5, frow = lane & 31;
 #pragma unroll
   for (int j = 0; j < 4; ++j) {
@@ -538,7 +553,8 @@ __device__ __attribute__((always_inline)) inline void big_epilogue_impl(const Ge
           const uint4 val = *reinterpret_cast<const uint4*>(stage_lds + r * kRowBytes + c * 16);
           uint8_t* dst = reinterpret_cast<uint8_t*>(g.out) + (gm * g.ldo + gn) * EB;
           if (gn + 16 / EB <= g.N) {
-            *reinterpret_cast<uint4*>(dst) = val;
+            if (nt) __builtin_nontemporal_store(v4i{(int)val.x, (int)val.y, (int)val.z, (int)val.w}, reinterpret_cast<v4i*>(dst));
+            else *reinterpret_cast<uint4*>(dst) = val;
           } else {  // N % 4 == 0: the first 8 bytes of the chunk are in range
             *reinterpret_cast<uint2*>(dst) = make_uint2(val.x, val.y);
           }
@@ -552,15 +568,15 @@ __device__ __attribute__((always_inline)) inline void big_epilogue_impl(const Ge
 
 template <int MODE>
 __device__ __attribute__((always_inline)) inline void big_epilogue(const GemmArgs& g, const v16f (&acc)[4][4], const BigScales& sc, int64_t m_tile,
-                                    int64_t n_tile, uint8_t* stage_lds) {
+                                    int64_t n_tile, uint8_t* stage_lds, bool nt = false) {
   if (g.bias) {
-    if (g.out_dtype == AYK_BF16) big_epilogue_impl<MODE, AYK_BF16, true>(g, acc, sc, m_tile, n_tile, stage_lds);
-    else if (g.out_dtype == AYK_F16) big_epilogue_impl<MODE, AYK_F16, true>(g, acc, sc, m_tile, n_tile, stage_lds);
-    else big_epilogue_impl<MODE, AYK_F32, true>(g, acc, sc, m_tile, n_tile, stage_lds);
+    if (g.out_dtype == AYK_BF16) big_epilogue_impl<MODE, AYK_BF16, true>(g, acc, sc, m_tile, n_tile, stage_lds, nt);
+    else if (g.out_dtype == AYK_F16) big_epilogue_impl<MODE, AYK_F16, true>(g, acc, sc, m_tile, n_tile, stage_lds, nt);
+    else big_epilogue_impl<MODE, AYK_F32, true>(g, acc, sc, m_tile, n_tile, stage_lds, nt);
   } else {
-    if (g.out_dtype == AYK_BF16) big_epilogue_impl<MODE, AYK_BF16, false>(g, acc, sc, m_tile, n_tile, stage_lds);
-    else if (g.out_dtype == AYK_F16) big_epilogue_impl<MODE, AYK_F16, false>(g, acc, sc, m_tile, n_tile, stage_lds);
-    else big_epilogue_impl<MODE, AYK_F32, false>(g, acc, sc, m_tile, n_tile, stage_lds);
+    if (g.out_dtype == AYK_BF16) big_epilogue_impl<MODE, AYK_BF16, false>(g, acc, sc, m_tile, n_tile, stage_lds, nt);
+    else if (g.out_dtype == AYK_F16) big_epilogue_impl<MODE, AYK_F16, false>(g, acc, sc, m_tile, n_tile, stage_lds, nt);
+    else big_epilogue_impl<MODE, AYK_F32, false>(g, acc, sc, m_tile, n_tile, stage_lds, nt);
   }
 }
 
@@ -710,67 +726,98 @@ __global__ __launch_bounds__(kThreads, 1) void fp8_gemm_big_kernel(GemmArgs g) {
 // hold a pair of steps: two 64 KB pair buffers, the second pair's loads in flight while
 // the first is multiplied. The fragment layout, the MFMA order and the epilogue are the
 // narrow kernel's; the step schedule (one barrier per pair) is its own.
+//
+// Persistent: a workgroup runs work items blockIdx.x, blockIdx.x + gridDim.x, ... (the
+// launch has at most one workgroup per CU, so item i runs on XCD i mod 8 as the tile
+// order assumes). One item is a whole tile, or one K piece of a tile (the K split of a
+// launch short of one round, blockIdx.y; the tail split of the last round). Across
+// items the pair stream does not drain: the next item's first pair is loaded during
+// the current item's last pair, and lands while the current item's epilogue runs
+// (staged through the pair buffer its last pair left free); the next item's second
+// pair is issued when the epilogue is done. Every item's MFMAs, loads and waits are
+// those of the single-tile kernel, so a tile's result is the same bit for bit.
+
+// One work item of the pair kernel: the tile, its K range and where its result goes.
+struct PairItem {
+  GemmArgs g;      // operand bases and K of the item's range; out / ldo / bias of its result
+  int tm, tn;
+  bool partial;    // an fp32 partial (K split or tail piece): plain stores, kept in L2
+};
+
 template <int MODE>
-__global__ __launch_bounds__(kThreads, 1) void fp8_gemm_pair_kernel(GemmArgs gin) {
-  // The tile (XCD-aware order) and K range of this workgroup:
-  //  * a K split of every tile (gin.kps > 0, launches short of one round): blockIdx.y's
-  //    K range, scaled fp32 partials to ws[y] ([M, N]);
+__device__ __attribute__((always_inline)) inline PairItem pair_item(const GemmArgs& gin, int item, int piece) {
+  //  * a K split of every tile (gin.kps > 0, launches short of one round): piece =
+  //    blockIdx.y's K range, scaled fp32 partials to ws[piece] ([M, N]);
   //  * a tail split (gin.tail_split > 1): the last, mostly empty round of tiles is
-  //    split over K across the CUs that round would leave idle; workgroup
-  //    b >= dp_tiles takes piece (b - dp_tiles) % tail_split of tile
-  //    dp_tiles + (b - dp_tiles) / tail_split, a 256 x 256 scaled fp32 partial in the
-  //    compact workspace [tail_split][tail tiles][256][256];
-  //  * otherwise tile blockIdx.x over all of K.
-  GemmArgs g = gin;
-  int tile_id = blockIdx.x, piece = blockIdx.y;
+  //    split over K across the CUs that round would leave idle; item b >= dp_tiles
+  //    takes piece (b - dp_tiles) % tail_split of tile dp_tiles + (b - dp_tiles) /
+  //    tail_split, a 256 x 256 scaled fp32 partial in the compact workspace
+  //    [tail_split][tail tiles][256][256];
+  //  * otherwise tile `item` over all of K.
+  PairItem it;
+  it.g = gin;
+  it.partial = false;
+  int tile_id = item;
   int64_t kps = gin.kps;
   bool tail = false;
-  if (gin.tail_split > 1 && (int)blockIdx.x >= gin.dp_tiles) {
-    const int u = (int)blockIdx.x - gin.dp_tiles;
+  if (gin.tail_split > 1 && item >= gin.dp_tiles) {
+    const int u = item - gin.dp_tiles;
     tile_id = gin.dp_tiles + u / gin.tail_split;
     piece = u % gin.tail_split;
     kps = gin.K / gin.tail_split;  // whole pairs (MX: whole 512-K chunks), by the plan
     tail = true;
   }
-  int tm, tn;
-  big_tile_coords(tile_id, g.tiles_m, (int)cdiv(g.N, kBigTile), tm, tn);
-  if constexpr (MODE == MODE_SCALED || MODE == MODE_MX || MODE == MODE_INT8) {
-    if (kps > 0) {
-      const int64_t k0 = (int64_t)piece * kps;  // MX: kps % 512 == 0 keeps the code rows 16-byte aligned
-      g.K = gin.K - k0 < kps ? gin.K - k0 : kps;
-      g.a = gin.a + k0;
-      g.w = gin.w + k0;
-      if constexpr (MODE == MODE_MX) {
-        g.sa = static_cast<const uint8_t*>(gin.sa) + k0 / 32;
-        g.sb = static_cast<const uint8_t*>(gin.sb) + k0 / 32;
-      }
-      g.bias = nullptr;
-      g.out_dtype = AYK_F32;
-      if (tail) {
-        // The epilogue addresses out + (m * ldo + n) with the tile's global (m, n): the
-        // base is moved back by the tile origin so that the tile lands at its slot.
-        const int tail_tiles = (int)(cdiv(gin.M, kBigTile) * cdiv(gin.N, kBigTile)) - gin.dp_tiles;
-        const int64_t slot = (int64_t)piece * tail_tiles + (tile_id - gin.dp_tiles);
-        g.out = gin.ws + slot * kBigTile * kBigTile - ((int64_t)tm * kBigTile * kBigTile + (int64_t)tn * kBigTile);
-        g.ldo = kBigTile;
-      } else {
-        g.out = gin.ws + (int64_t)piece * gin.M * gin.N;
-        g.ldo = gin.N;
-      }
+  big_tile_coords(tile_id, gin.tiles_m, (int)cdiv(gin.N, kBigTile), it.tm, it.tn);
+  if (kps > 0) {
+    GemmArgs& g = it.g;
+    const int64_t k0 = (int64_t)piece * kps;  // MX: kps % 512 == 0 keeps the code rows 16-byte aligned
+    g.K = gin.K - k0 < kps ? gin.K - k0 : kps;
+    g.a = gin.a + k0;
+    g.w = gin.w + k0;
+    if constexpr (MODE == MODE_MX) {
+      g.sa = static_cast<const uint8_t*>(gin.sa) + k0 / 32;
+      g.sb = static_cast<const uint8_t*>(gin.sb) + k0 / 32;
+    }
+    g.bias = nullptr;
+    g.out_dtype = AYK_F32;
+    it.partial = true;
+    if (tail) {
+      // The epilogue addresses out + (m * ldo + n) with the tile's global (m, n): the
+      // base is moved back by the tile origin so that the tile lands at its slot.
+      const int tail_tiles = (int)(cdiv(gin.M, kBigTile) * cdiv(gin.N, kBigTile)) - gin.dp_tiles;
+      const int64_t slot = (int64_t)piece * tail_tiles + (tile_id - gin.dp_tiles);
+      g.out = gin.ws + slot * kBigTile * kBigTile - ((int64_t)it.tm * kBigTile * kBigTile + (int64_t)it.tn * kBigTile);
+      g.ldo = kBigTile;
+    } else {
+      g.out = gin.ws + (int64_t)piece * gin.M * gin.N;
+      g.ldo = gin.N;
     }
   }
+  return it;
+}
+
+// What the loads of one work item need: its operand and code windows (this wavefront's
+// rows), its pair count and its K stagger.
+struct PairSrc {
+  __amdgpu_buffer_rsrc_t op, code;
+  int np, npairs, stag;
+};
+
+template <int MODE>
+__global__ __launch_bounds__(kThreads, 1) void fp8_gemm_pair_kernel(GemmArgs gin) {
   static_assert(row_scaled(MODE) || MODE == MODE_MX, "per-row / per-tensor scales or MX codes");
   constexpr int FN = 4, FM = 4;        // 32x32 MFMA tiles per wavefront (n, m)
   constexpr int kPairK = 2 * kBigK;    // 128 K bytes per pair
   constexpr int kPairBytes = 2 * kBigTile * kPairK;  // 64 KB
   constexpr int kDma = kPairBytes / 1024 / 4;        // direct loads per wavefront per pair (16)
-  static_assert(kPairBytes == kEpilogueLds, "the first pair buffer holds the epilogue's staging tile");
   // Two pair buffers in two distinct LDS objects (the compiler tells that reads of one
   // never alias the in-flight direct loads into the other).
   __shared__ __attribute__((aligned(1024))) uint8_t P0[kPairBytes];
   __shared__ __attribute__((aligned(1024))) uint8_t P1[kPairBytes];
+  static_assert(kPairBytes == kEpilogueLds, "a pair buffer holds the epilogue's staging tile");
   // MXFP8: the UE8M0 codes of the tile's 512 rows for a chunk of four pairs (16 bytes a
-  // row), in two 8 KB halves (chunk c in half c mod 2).
+  // row), in two 8 KB halves. Chunks alternate halves along the workgroup's whole pair
+  // stream (across items too), so a chunk is never loaded into the half being read.
   constexpr int kChunkBytes = 2 * kBigTile * 16;
   __shared__ __attribute__((aligned(1024))) uint8_t C[MODE == MODE_MX ? 2 * kChunkBytes : 16];
 
@@ -778,16 +825,6 @@ __global__ __launch_bounds__(kThreads, 1) void fp8_gemm_pair_kernel(GemmArgs gin
   const int wave_u = __builtin_amdgcn_readfirstlane(tid >> 6);  // keep descriptors in SGPRs
   const int wn = wave_u >> 1, wm = wave_u & 1;
   const int h = lane >> 5, frow = lane & 31;
-  const int64_t n_base = (int64_t)tn * kBigTile, m_base = (int64_t)tm * kBigTile;
-  const int np = (int)(g.K / kPairK);    // real pairs
-  const int npairs = (np + 1) & ~1;      // padded to the unroll (a padded pair computes zeros)
-  // K stagger in pairs: (tm mod 8) + (tn mod 2) (mod np), the narrow kernel's stagger
-  // of 2 (tm mod 8) + (tn mod 2) steps rounded to whole pairs.
-  // MXFP8 (np % 4 == 0) staggers in whole chunks of four pairs, which is coarse: only
-  // 4 ((tm mod 2) + (tn mod 2)) (mod np), the best of none, this and 4 (tm mod 8 ...).
-  const int stag = __builtin_amdgcn_readfirstlane(
-      MODE == MODE_MX ? 4 * (int)((unsigned)((tm & 1) + (tn & 1)) % (unsigned)(np / 4))
-                      : (int)((unsigned)((tm & 7) + (tn & 1)) % (unsigned)np));
 
   // Direct loads: wavefronts 0-1 fetch the 256 weight rows, 2-3 the 256 activation rows
   // (128 each). Load jj (0-15) of wavefront w reads operand rows 128 (w & 1) + 8 jj +
@@ -798,31 +835,69 @@ __global__ __launch_bounds__(kThreads, 1) void fp8_gemm_pair_kernel(GemmArgs gin
   // side s (0: weight, 1: activation) is LDS row 64 (2 s + R / 128) + R % 64 of half
   // (R % 128) / 64.
   const bool w_wave = wave_u < 2;
-  const int64_t ld = w_wave ? g.ldw : g.lda;
-  const int ld_u = __builtin_amdgcn_readfirstlane((int)ld);
-  const OperandWindow win = operand_window((w_wave ? n_base : m_base) + (wave_u & 1) * 128, w_wave ? g.N : g.M, ld);
-  const __amdgpu_buffer_rsrc_t op_rsrc = uniform_rsrc((w_wave ? g.w : g.a) + win.base_offset, win.records);
+  const int ld_u = __builtin_amdgcn_readfirstlane((int)(w_wave ? gin.ldw : gin.lda));
   const int voff_e = (lane >> 3) * ld_u + (((lane & 7) ^ ((lane >> 4) & 7)) << 4);
   const int voff_o = (lane >> 3) * ld_u + (((lane & 7) ^ ((4 + (lane >> 4)) & 7)) << 4);
-  // Issue pair p (< npairs) into pair buffer `dst`. A padded pair (p >= np) reads past
-  // every buffer window, which returns zeros.
-  auto issue = [&](int p, uint8_t* dst) {
-    int kp = (p < np ? p : np - 1) + stag;
-    kp = __builtin_amdgcn_readfirstlane(kp >= np ? kp - np : kp);
-    const int pad_off = __builtin_amdgcn_readfirstlane(p < np ? 0 : 0x40000000);
+  const int64_t ld_c = w_wave ? gin.ld_sb : gin.ld_sa;
+  const int ldc_u = __builtin_amdgcn_readfirstlane((int)ld_c);
+
+  using Src = PairSrc;
+  auto make_src = [&](const PairItem& it) -> Src {
+    const GemmArgs& g = it.g;
+    const int64_t n_base = (int64_t)it.tn * kBigTile, m_base = (int64_t)it.tm * kBigTile;
+    const int64_t row0 = (w_wave ? n_base : m_base) + (wave_u & 1) * 128;
+    const OperandWindow win = operand_window(row0, w_wave ? g.N : g.M, w_wave ? g.ldw : g.lda);
+    Src s;
+    s.op = uniform_rsrc((w_wave ? g.w : g.a) + win.base_offset, win.records);
+    // Code chunk loads mirror the operand loads: chunk row r (0-255 weight, 256-511
+    // activation) at byte 16 r of its half. Rows past M / N read zero codes.
+    const OperandWindow cwin = MODE == MODE_MX ? operand_window(row0, w_wave ? g.N : g.M, ld_c) : OperandWindow{0, 0};
+    s.code = uniform_rsrc(reinterpret_cast<const uint8_t*>(w_wave ? g.sb : g.sa) + cwin.base_offset, cwin.records);
+    s.np = __builtin_amdgcn_readfirstlane((int)(g.K / kPairK));  // real pairs
+    s.npairs = (s.np + 1) & ~1;  // padded to the unroll (a padded pair computes zeros)
+    // K stagger in pairs: (tm mod 8) + (tn mod 2) (mod np), the narrow kernel's stagger
+    // of 2 (tm mod 8) + (tn mod 2) steps rounded to whole pairs.
+    // MXFP8 (np % 4 == 0) staggers in whole chunks of four pairs, which is coarse: only
+    // 4 ((tm mod 2) + (tn mod 2)) (mod np), the best of none, this and 4 (tm mod 8 ...).
+    s.stag = __builtin_amdgcn_readfirstlane(
+        MODE == MODE_MX ? 4 * (int)((unsigned)((it.tm & 1) + (it.tn & 1)) % (unsigned)(s.np / 4))
+                        : (int)((unsigned)((it.tm & 7) + (it.tn & 1)) % (unsigned)s.np));
+    return s;
+  };
+  // Issue pair p (< npairs) of `src` into pair buffer `dst`. A padded pair (p >= np)
+  // reads past every buffer window, which returns zeros.
+  auto issue = [&](const Src& src, int p, uint8_t* dst) {
+    int kp = (p < src.np ? p : src.np - 1) + src.stag;
+    kp = __builtin_amdgcn_readfirstlane(kp >= src.np ? kp - src.np : kp);
+    const int pad_off = __builtin_amdgcn_readfirstlane(p < src.np ? 0 : 0x40000000);
 #pragma unroll
     for (int jj = 0; jj < kDma; ++jj) {
       const int soff = __builtin_amdgcn_readfirstlane(jj * 8 * ld_u + kp * kPairK + pad_off);
       __builtin_amdgcn_raw_ptr_buffer_load_lds(
-          op_rsrc, (__attribute__((address_space(3))) void*)(dst + ((jj >> 3) * (kPairBytes / 2) + (wave_u * 8 + (jj & 7)) * 1024)),
+          src.op, (__attribute__((address_space(3))) void*)(dst + ((jj >> 3) * (kPairBytes / 2) + (wave_u * 8 + (jj & 7)) * 1024)),
           16, (jj & 1) ? voff_o : voff_e, soff, 0, 0);
+    }
+  };
+  // Code chunk c of `src` (pairs 4c .. 4c + 3) into half `half` of C: two 16-byte
+  // direct loads of 64 rows per wavefront.
+  auto issue_codes = [&](const Src& src, int c, int half) {
+    if constexpr (MODE == MODE_MX) {
+      int kc = c + src.stag / 4;
+      kc = __builtin_amdgcn_readfirstlane(kc >= src.np / 4 ? kc - src.np / 4 : kc);
+#pragma unroll
+      for (int q = 0; q < 2; ++q)
+        __builtin_amdgcn_raw_ptr_buffer_load_lds(
+            src.code, (__attribute__((address_space(3))) void*)(C + (half * kChunkBytes + (wave_u * 128 + q * 64) * 16)), 16,
+            lane * ldc_u, __builtin_amdgcn_readfirstlane(q * 64 * ldc_u + kc * 16), 0, 0);
     }
   };
 
   // Fragment reads: a fragment's LDS row is frow plus a multiple of 32, so its swizzle
   // (row >> 1) & 7 is (frow >> 1) & 7 for all of them; step half t of the pair reads
   // logical chunks 4 t + h and 4 t + 2 + h. One 16-byte load at a single integer offset
-  // from the pair buffer each (see the narrow kernel).
+  // from the pair buffer each (the compiler attributes an LDS access to its buffer only
+  // through a short chain of address arithmetic; past it, it assumes the access may
+  // alias every in-flight direct load and waits for all of them).
   const int fsw = (frow >> 1) & 7;
   const int off_t[2][2] = {{frow * kPairK + ((h ^ fsw) << 4), frow * kPairK + (((2 + h) ^ fsw) << 4)},
                            {frow * kPairK + (((4 + h) ^ fsw) << 4), frow * kPairK + (((6 + h) ^ fsw) << 4)}};
@@ -844,42 +919,15 @@ __global__ __launch_bounds__(kThreads, 1) void fp8_gemm_pair_kernel(GemmArgs gin
   // Declaring an AGPR clobber makes the compiler select the AGPR form of the MFMAs.
   asm volatile("" ::: "a255");
   v16f acc[FN][FM];
-#pragma unroll
-  for (int i = 0; i < FN; ++i)
-#pragma unroll
-    for (int j = 0; j < FM; ++j)
-#pragma unroll
-      for (int r = 0; r < 16; ++r) acc[i][j][r] = 0.0f;
   // MXFP8: the codes of a fragment row for one pair are one dword (four 32-K blocks)
   // of its chunk row in C. Those of pair p + 1 are read during pair p into the second
   // set and moved to the first at the pair's end. Step half t of the pair uses block
   // 2 t + h in lane half h: the dword shifted right by 8 (2 t + h) (the MFMA reads the
   // low byte of its scale operands).
   uint32_t wc[2][FN], ac[2][FM];
-  // Code chunk loads mirror the operand loads: wavefronts 0-1 the weight rows, 2-3 the
-  // activation rows, 128 each, as two 16-byte direct loads of 64 rows; chunk row r
-  // (0-255 weight, 256-511 activation) at byte 16 r of its half. Rows past M / N read
-  // zero codes (never stored).
-  const int64_t ld_c = w_wave ? g.ld_sb : g.ld_sa;
-  const OperandWindow cwin = MODE == MODE_MX ? operand_window((w_wave ? n_base : m_base) + (wave_u & 1) * 128, w_wave ? g.N : g.M, ld_c)
-                                             : OperandWindow{0, 0};
-  const __amdgpu_buffer_rsrc_t code_rsrc =
-      uniform_rsrc(reinterpret_cast<const uint8_t*>(w_wave ? g.sb : g.sa) + cwin.base_offset, cwin.records);
-  const int ldc_u = __builtin_amdgcn_readfirstlane((int)ld_c);
-  auto issue_codes = [&](int c) {
+  auto read_codes = [&](int p, int set, int half) {
     if constexpr (MODE == MODE_MX) {
-      int kc = c + stag / 4;
-      kc = __builtin_amdgcn_readfirstlane(kc >= np / 4 ? kc - np / 4 : kc);
-#pragma unroll
-      for (int q = 0; q < 2; ++q)
-        __builtin_amdgcn_raw_ptr_buffer_load_lds(
-            code_rsrc, (__attribute__((address_space(3))) void*)(C + ((c & 1) * kChunkBytes + (wave_u * 128 + q * 64) * 16)), 16,
-            lane * ldc_u, __builtin_amdgcn_readfirstlane(q * 64 * ldc_u + kc * 16), 0, 0);
-    }
-  };
-  auto read_codes = [&](int p, int set) {
-    if constexpr (MODE == MODE_MX) {
-      const int base = ((p >> 2) & 1) * kChunkBytes + (p & 3) * 4;
+      const int base = half * kChunkBytes + (p & 3) * 4;
 #pragma unroll
       for (int i = 0; i < FN; ++i) wc[set][i] = *reinterpret_cast<const uint32_t*>(C + (base + (wn * 128 + i * 32 + frow) * 16));
 #pragma unroll
@@ -908,26 +956,22 @@ __global__ __launch_bounds__(kThreads, 1) void fp8_gemm_pair_kernel(GemmArgs gin
       }
   };
 
-  const BigScales scales = load_big_scales<MODE>(g, m_base, n_base);
-  // Prologue: pairs 0 and 1 in flight (pair 0's codes between them), pair 0 visible,
-  // step (0, 0)'s fragments in set 0.
-  issue(0, P0);
-  issue_codes(0);
-  issue(1, P1);
-  wait_vmcnt<kDma>();
-  lds_barrier();
-  read_frags(0, P0, 0);
-  read_codes(0, 0);
-
-  // Pair p in `cur`, pair p + 1 in flight into `nxt`, one barrier per pair. Step 0: the
-  // 16 MFMAs of fragment set 0 interleaved one for one with the reads of step 1's
-  // fragments (set 1) from `cur`. Step 1: wait for pair p + 1 and for this wavefront's
-  // reads, barrier (pair p + 1 is visible and nobody reads `cur` any more), read the
-  // next pair's codes, issue pair p + 2 into `cur`, then the 16 MFMAs of set 1
-  // interleaved with the direct loads and with the reads of pair p + 1's step 0
-  // fragments from `nxt`. Left to itself the scheduler puts all reads after the MFMAs,
-  // and their latency then stalls the next step's first MFMA.
-  auto pair = [&](int p, uint8_t* cur, uint8_t* nxt) {
+  // Pair p in `cur`, pair p + 1 in flight into `nxt`, one barrier per pair, in two
+  // halves. half0 (step 0): the 16 MFMAs of fragment set 0 interleaved one for one with
+  // the reads of step 1's fragments (set 1) from `cur`. half1 (step 1): wait for pair
+  // p + 1 and for this wavefront's reads, barrier (pair p + 1 is visible and nobody
+  // reads `cur` any more), read the next pair's codes, issue the loads `refill` names
+  // into `cur`, then the 16 MFMAs of set 1 interleaved with the direct loads and with
+  // the reads of pair p + 1's step 0 fragments from `nxt`. Left to itself the scheduler
+  // puts all reads after the MFMAs, and their latency then stalls the next step's first
+  // MFMA. The K loop's body starts with a half1, i.e. with the wait: at its head every
+  // LDS read comes after that wait, so the compiler never has to decide whether a read
+  // may alias a direct load in flight from before the loop. The buffers are
+  // compile-time choices (B: pair p in P0 or P1), so that every LDS access keeps its
+  // object (an access the compiler cannot attribute to a buffer is assumed to alias
+  // the in-flight direct loads, and it waits for all of them first).
+  auto half0 = [&](auto B) __attribute__((always_inline)) {
+    uint8_t* cur = decltype(B)::value == 0 ? P0 : P1;
     read_frags(1, cur, 1);
     mfmas(0, 0, FM);
 #pragma unroll
@@ -936,15 +980,18 @@ __global__ __launch_bounds__(kThreads, 1) void fp8_gemm_pair_kernel(GemmArgs gin
       __builtin_amdgcn_sched_group_barrier(0x100, 1, 0);  // one LDS read
     }
     __builtin_amdgcn_sched_barrier(0);
+  };
+  auto half1 = [&](auto B, auto&& codes_next, auto&& refill, auto&& frags_next) __attribute__((always_inline)) {
+    uint8_t* cur = decltype(B)::value == 0 ? P0 : P1;
+    uint8_t* nxt = decltype(B)::value == 0 ? P1 : P0;
     wait_vmcnt<0>();
     lds_barrier();
     __builtin_amdgcn_sched_barrier(0);
     // The next pair's codes are read before any new code load is in flight (the
     // compiler cannot tell the two halves of C apart and would wait for it).
-    read_codes(p + 1 < npairs ? p + 1 : npairs - 1, 1);
-    issue(p + 2 < npairs ? p + 2 : npairs - 1, cur);
-    if (MODE == MODE_MX && ((p + 2) & 3) == 0 && p + 2 < npairs) issue_codes((p + 2) >> 2);
-    read_frags(0, nxt, 0);
+    codes_next();
+    refill(cur);
+    frags_next(nxt);
     mfmas(1, 0, FM);
 #pragma unroll
     for (int i = 0; i < FN * FM; ++i) {
@@ -955,14 +1002,86 @@ __global__ __launch_bounds__(kThreads, 1) void fp8_gemm_pair_kernel(GemmArgs gin
     __builtin_amdgcn_sched_barrier(0);
     next_codes();
   };
-  for (int p = 0; p < npairs; p += 2) {
-    pair(p, P0, P1);
-    pair(p + 1, P1, P0);
-  }
-  // Every issued load has landed and no wavefront still reads a pair buffer.
-  wait_vmcnt<0>();
+
+  auto frags_step0 = [&](const uint8_t* buf) __attribute__((always_inline)) { read_frags(0, buf, 0); };
+  constexpr std::integral_constant<int, 0> kBuf0{};
+  constexpr std::integral_constant<int, 1> kBuf1{};
+  int item = blockIdx.x;
+  Src src = make_src(pair_item<MODE>(gin, item, blockIdx.y));
+  int cbase = 0;  // C half of the item's code chunk 0
+  // Prologue: pairs 0 and 1 in flight (pair 0's codes between them), pair 0 visible,
+  // step (0, 0)'s fragments in set 0.
+  issue(src, 0, P0);
+  issue_codes(src, 0, 0);
+  issue(src, 1, P1);
+  wait_vmcnt<kDma>();
   lds_barrier();
-  big_epilogue<MODE>(g, acc, scales, m_base, n_base, P0);
+  read_frags(0, P0, 0);
+  read_codes(0, 0, 0);
+  auto start_item = [&] __attribute__((always_inline)) {
+#pragma unroll
+    for (int i = 0; i < FN; ++i)
+#pragma unroll
+      for (int j = 0; j < FM; ++j)
+#pragma unroll
+        for (int r = 0; r < 16; ++r) acc[i][j][r] = 0.0f;
+    half0(kBuf0);  // pair 0, step 0
+  };
+  start_item();
+
+  // The item loop's body starts with a half1 too (the wait), for the same reason as the
+  // K loop's; an item's first half0 ends the previous iteration.
+  for (;;) {
+    const int npairs = src.npairs;
+    // Step 1 of pairs 0 .. npairs - 3 and step 0 of pairs 1 .. npairs - 2: each half1
+    // refills its buffer with pair p + 2 of this item.
+    for (int p = 0; p + 2 < npairs; p += 2) {
+      half1(kBuf0, [&] { read_codes(p + 1, 1, (cbase + ((p + 1) >> 2)) & 1); },
+            [&](uint8_t* cur) {
+              issue(src, p + 2, cur);
+              if (MODE == MODE_MX && ((p + 2) & 3) == 0) issue_codes(src, (p + 2) >> 2, (cbase + ((p + 2) >> 2)) & 1);
+            }, frags_step0);
+      half0(kBuf1);
+      half1(kBuf1, [&] { read_codes(p + 2, 1, (cbase + ((p + 2) >> 2)) & 1); },
+            [&](uint8_t* cur) {
+              issue(src, p + 3, cur);
+              if (MODE == MODE_MX && ((p + 3) & 3) == 0) issue_codes(src, (p + 3) >> 2, (cbase + ((p + 3) >> 2)) & 1);
+            }, frags_step0);
+      half0(kBuf0);
+    }
+    // The next item (this one again when there is none: its loads then land unused).
+    const int next = item + (int)gridDim.x;
+    const bool more = next < gin.items;
+    const Src nsrc = make_src(pair_item<MODE>(gin, more ? next : item, blockIdx.y));
+    const int ncbase = (cbase + npairs / 4) & 1;  // MX: npairs == np, a multiple of 4
+    const PairItem it = pair_item<MODE>(gin, item, blockIdx.y);
+    // Pair npairs - 2, step 1: its refill is this item's output scales (loaded one and a
+    // half pairs ahead of the epilogue) and the next item's pair 0 (and code chunk 0).
+    BigScales scales;
+    half1(kBuf0, [&] { read_codes(npairs - 1, 1, (cbase + ((npairs - 1) >> 2)) & 1); },
+          [&](uint8_t* cur) {
+            scales = load_big_scales<MODE>(it.g, (int64_t)it.tm * kBigTile, (int64_t)it.tn * kBigTile);
+            issue(nsrc, 0, cur);
+            issue_codes(nsrc, 0, ncbase);
+          }, frags_step0);
+    half0(kBuf1);
+    // Pair npairs - 1, step 1: no refill, since its buffer (P1) stages the epilogue, and
+    // no fragment reads (the next item's are read after the epilogue, so that they do
+    // not hold registers through it).
+    half1(kBuf1, [&] { read_codes(0, 1, ncbase); }, [](uint8_t*) {}, [](const uint8_t*) {});
+    // Every wavefront has passed the last pair's barrier: nobody reads P1 any more.
+    big_epilogue<MODE>(it.g, acc, scales, (int64_t)it.tm * kBigTile, (int64_t)it.tn * kBigTile, P1, !it.partial);
+    if (!more) break;
+    item = next;
+    src = nsrc;
+    cbase = ncbase;
+    issue(src, 1, P1);  // after the epilogue's last barrier: nobody reads the staging tile
+    read_frags(0, P0, 0);  // pair 0 landed before the last pair's barrier
+    start_item();
+  }
+  // Outstanding at exit: the unused reload of the last item's first pair (into a buffer
+  // nobody reads) and the epilogue's stores.
+  wait_vmcnt<0>();
 }
 
 // ---------------------------------------------------------------------------------
@@ -1563,6 +1682,26 @@ __global__ __launch_bounds__(kThreads, 1) void fp8_gemm_mx128_kernel(GemmArgs g)
   big_epilogue<MODE>(g, acc, BigScales{}, m_base, n_base, lds0);
 }
 
+// Compute units of the current device (cached per device): the persistent pair
+// kernel launches at most this many workgroups, one per CU.
+int cu_count() {
+  static int cached[64];
+  int dev = 0;
+  if (hipGetDevice(&dev) != hipSuccess || dev < 0 || dev >= 64) return 256;
+  if (cached[dev] == 0) {
+    int n = 0;
+    if (hipDeviceGetAttribute(&n, hipDeviceAttributeMultiprocessorCount, dev) != hipSuccess || n < 8) n = 256;
+    cached[dev] = n & ~7;  // a multiple of 8 keeps item i on XCD i mod 8
+  }
+  return cached[dev];
+}
+
+// Persistent grid of the pair kernel for `items` work items.
+unsigned pair_grid(int64_t items) {
+  const int64_t cus = cu_count();
+  return (unsigned)(items < cus ? items : cus);
+}
+
 // The pair kernel over all K, with the tail split when the plan has one (whole rounds
 // of tiles, then the last round's tiles in K pieces and their fixed-order reduce).
 template <int MODE>
@@ -1573,14 +1712,16 @@ int launch_pair_tail(GemmArgs g, int64_t tiles, hipStream_t st, const char* op) 
   g.tail_split = tp.split;
   note_plan("pair tail=%d", tp.split);
   if (tp.split == 1) {
-    hipLaunchKernelGGL((fp8_gemm_pair_kernel<MODE>), dim3((unsigned)tiles), dim3(kThreads), 0, st, g);
+    g.items = (int)tiles;
+    hipLaunchKernelGGL((fp8_gemm_pair_kernel<MODE>), dim3(pair_grid(tiles)), dim3(kThreads), 0, st, g);
     return check_launch(op);
   }
   const size_t need = tail_workspace(tp);
   if (g.ws == nullptr || g.ws_bytes < need)
     return fail(AYK_EWORKSPACE, "%s: workspace of %zu bytes required, %zu given", op, need, g.ws_bytes);
-  const int64_t grid = (int64_t)tp.dp_tiles + (int64_t)tp.tail_tiles * tp.split;
-  hipLaunchKernelGGL((fp8_gemm_pair_kernel<MODE>), dim3((unsigned)grid), dim3(kThreads), 0, st, g);
+  const int64_t items = (int64_t)tp.dp_tiles + (int64_t)tp.tail_tiles * tp.split;
+  g.items = (int)items;
+  hipLaunchKernelGGL((fp8_gemm_pair_kernel<MODE>), dim3(pair_grid(items)), dim3(kThreads), 0, st, g);
   if (int rc = check_launch(op)) return rc;
   const int64_t threads = (int64_t)tp.tail_tiles * kBigTile * kBigTile / 4;
   hipLaunchKernelGGL(tail_split_reduce, dim3((unsigned)cdiv(threads, 256)), dim3(256), 0, st, g.ws, tp.tail_tiles,
@@ -1609,6 +1750,7 @@ int launch_big(GemmArgs g, hipStream_t st, const char* op) {
       }
       if (split == 1) return launch_pair_tail<MODE>(g, tiles, st, op);
       note_plan("pair split=%d", (int)split);
+      g.items = (int)tiles;  // one item per workgroup: grid (tiles, split)
       hipLaunchKernelGGL((fp8_gemm_pair_kernel<MODE>), dim3((unsigned)tiles, (unsigned)split), dim3(kThreads), 0, st, g);
       if (int rc = check_launch(op)) return rc;
       hipLaunchKernelGGL(block_split_reduce, dim3((unsigned)cdiv(g.M * g.N, 256)), dim3(256), 0, st, g.ws, g.M, g.N,
@@ -1629,7 +1771,9 @@ int launch_big(GemmArgs g, hipStream_t st, const char* op) {
     }
     if (split == 1 && MODE == MODE_SCALED) return launch_pair_tail<MODE>(g, tiles, st, op);
     note_plan("pair split=%d", (int)split);
-    hipLaunchKernelGGL((fp8_gemm_pair_kernel<MODE>), dim3((unsigned)tiles, (unsigned)split), dim3(kThreads), 0, st, g);
+    g.items = (int)tiles;
+    hipLaunchKernelGGL((fp8_gemm_pair_kernel<MODE>), dim3(split > 1 ? (unsigned)tiles : pair_grid(tiles), (unsigned)split),
+                       dim3(kThreads), 0, st, g);
     if (split > 1) {
       if (int rc = check_launch(op)) return rc;
       hipLaunchKernelGGL(block_split_reduce, dim3((unsigned)cdiv(g.M * g.N, 256)), dim3(256), 0, st, g.ws, g.M, g.N,
