@@ -737,6 +737,191 @@ __global__ __launch_bounds__(kThreads, 1) void fp8_gemm_big_kernel(GemmArgs g) {
 // pair is issued when the epilogue is done. Every item's MFMAs, loads and waits are
 // those of the single-tile kernel, so a tile's result is the same bit for bit.
 
+// Output scales and bias of one item of the persistent pair kernel, as loaded ahead of
+// its epilogue: each thread fetches one column's weight scale and bias (column
+// n_tile + tid) and the activation scales of its lane's four rows; the epilogue writes
+// the columns' values into an LDS table that every lane reads (a lane's 64 columns in
+// registers through the epilogue, 128 values with the bias, had made the kernel spill).
+struct PairScales {
+  float sa[4];  // activation scale of the lane's row in m-fragment j
+  float sb;     // weight scale of column n_tile + tid (1 without row scales)
+  float bias;   // bias of column n_tile + tid (0 without a bias)
+};
+template <int MODE>
+__device__ __attribute__((always_inline)) inline PairScales load_pair_scales(const GemmArgs& g, int64_t m_tile, int64_t n_tile) {
+  int tid = threadIdx.x;
+  asm volatile("" : "+v"(tid));  // not hoisted out of the item loop
+  const int lane = tid & 63, wm = (tid >> 6) & 1, frow = lane & 31;
+  PairScales ps;
+  ps.sb = 1.0f;
+  ps.bias = 0.0f;
+#pragma unroll
+  for (int j = 0; j < 4; ++j) ps.sa[j] = 1.0f;
+  const int64_t n = n_tile + tid;
+  const int64_t nc = n < g.N ? n : g.N - 1;  // a column past N loads column N - 1 (never stored)
+  if constexpr (row_scaled(MODE)) {
+    const float* sa_p = reinterpret_cast<const float*>(g.sa);
+#pragma unroll
+    for (int j = 0; j < 4; ++j) {
+      const int64_t m = m_tile + wm * 128 + j * 32 + frow;
+      ps.sa[j] = sa_p[g.sa_vec ? (m < g.M ? m : 0) : 0];
+    }
+    ps.sb = reinterpret_cast<const float*>(g.sb)[g.sb_vec ? nc : 0];
+  }
+  if (g.bias != nullptr) ps.bias = load_f32(g.bias, g.bias_dtype, nc);
+  return ps;
+}
+
+// Epilogue of the persistent pair kernel: as big_epilogue_impl (scaled, biased and
+// converted values staged through LDS, 16-byte coalesced stores), with the columns'
+// scales and bias read from an LDS table, each pass's staged chunks read into
+// registers before any of them is stored (so that the LDS reads pipeline), and
+// nontemporal stores for final outputs (NT; fp32 partials that a reduce reads back keep
+// plain stores). The staging tile and the table share the pair buffer `stage_lds`.
+template <int MODE, int OUT, bool BIAS, bool NT>
+__device__ __attribute__((always_inline)) inline void pair_epilogue_impl(const GemmArgs& g, const v16f (&acc)[4][4], const PairScales& ps,
+                                                                         int64_t m_tile, int64_t n_tile, uint8_t* stage_lds,
+                                                                         float* table) {
+  constexpr int EB = OutBytes<OUT>::v;
+  constexpr int kRowBytes = 256 * EB + 16;        // padded staging row
+  constexpr int kStageRows = EB == 4 ? 32 : 64;   // rows staged at once
+  constexpr int kPasses = 64 / kStageRows;        // fp32: one pass per row half (wm)
+  static_assert(kStageRows * kRowBytes <= kEpilogueLds, "staging tile must fit a pair buffer");
+  constexpr bool kScaled = row_scaled(MODE);
+  int tid = threadIdx.x;
+  asm volatile("" : "+v"(tid));  // lane addresses are not hoisted out of the item loop
+  const int lane = tid & 63, wave = tid >> 6;
+  const int wn = wave >> 1, wm = wave & 1, h = lane >> 5, frow = lane & 31;
+  float* sb_t = table;  // its own LDS object: its reads need not wait for staging writes
+  float* bias_t = table + 256;
+  // A tile inside M x N stores without bounds checks.
+  const bool whole = m_tile + 256 <= g.M && n_tile + 256 <= g.N;
+  if constexpr (kScaled || BIAS) {
+    if constexpr (kScaled) sb_t[tid] = ps.sb;
+    if constexpr (BIAS) bias_t[tid] = ps.bias;
+    lds_barrier();
+  }
+  constexpr int kChunksPerRow = 256 * EB / 16;
+  constexpr int kRowsPerStep = 256 / kChunksPerRow;
+  constexpr int kSteps = kStageRows / kRowsPerStep;
+  const int c = tid % kChunksPerRow, r_base = tid / kChunksPerRow;
+  const int64_t gn = n_tile + (int64_t)c * (16 / EB);
+#pragma unroll
+  for (int j = 0; j < 4; ++j) {
+#pragma unroll
+    for (int pass = 0; pass < kPasses; ++pass) {
+      if (kPasses == 1 || wm == pass) {
+        uint8_t* srow = stage_lds + ((kPasses == 1 ? wm * 32 : 0) + frow) * kRowBytes;
+        // Column group q = 4 i + grp; its table values are read one group ahead, so that
+        // their latency hides behind the previous group's arithmetic.
+        auto col = [&](int q) { return wn * 128 + (q >> 2) * 32 + (q & 3) * 8 + h * 4; };
+        float4 s4n = make_float4(1.0f, 1.0f, 1.0f, 1.0f), b4n = make_float4(0.0f, 0.0f, 0.0f, 0.0f);
+        if constexpr (kScaled) s4n = *reinterpret_cast<const float4*>(sb_t + col(0));
+        if constexpr (BIAS) b4n = *reinterpret_cast<const float4*>(bias_t + col(0));
+#pragma unroll
+        for (int i = 0; i < 4; ++i) {
+#pragma unroll
+          for (int grp = 0; grp < 4; ++grp) {
+            const int q = i * 4 + grp;
+            const int nl = col(q);  // column within the tile
+            const float4 s4 = s4n, b4 = b4n;
+            if (q + 1 < 16) {
+              if constexpr (kScaled) s4n = *reinterpret_cast<const float4*>(sb_t + col(q + 1));
+              if constexpr (BIAS) b4n = *reinterpret_cast<const float4*>(bias_t + col(q + 1));
+            }
+            const float sbv[4] = {s4.x, s4.y, s4.z, s4.w}, bv[4] = {b4.x, b4.y, b4.z, b4.w};
+            float v[4];
+#pragma unroll
+            for (int qq = 0; qq < 4; ++qq) {
+              float y = acc_value<MODE>(acc[i][j][grp * 4 + qq]);
+              if constexpr (kScaled) y = (y * ps.sa[j]) * sbv[qq];
+              v[qq] = BIAS ? y + bv[qq] : y;
+            }
+            if constexpr (OUT == AYK_F32) {
+              *reinterpret_cast<float4*>(srow + nl * 4) = make_float4(v[0], v[1], v[2], v[3]);
+            } else if constexpr (OUT == AYK_BF16) {
+              *reinterpret_cast<uint2*>(srow + nl * 2) = make_uint2(pack_bf16x2(v[0], v[1]), pack_bf16x2(v[2], v[3]));
+            } else {
+              uint16_t b[4];
+#pragma unroll
+              for (int qq = 0; qq < 4; ++qq) b[qq] = f32_to_f16_bits(v[qq]);
+              *reinterpret_cast<uint2*>(srow + nl * 2) =
+                  make_uint2((uint32_t)b[0] | ((uint32_t)b[1] << 16), (uint32_t)b[2] | ((uint32_t)b[3] << 16));
+            }
+          }
+        }
+      }
+      lds_barrier();  // the staging writes are visible
+      // Staged row r: with one pass, r < 32 is tile row j*32 + r (wm = 0) and r >= 32
+      // is 128 + j*32 + (r - 32) (wm = 1); with two passes, pass*128 + j*32 + r.
+      v4i val[kSteps];
+#pragma unroll
+      for (int t = 0; t < kSteps; ++t)
+        val[t] = *reinterpret_cast<const v4i*>(stage_lds + (t * kRowsPerStep + r_base) * kRowBytes + c * 16);
+      auto row_of = [&](int t) {
+        const int r = t * kRowsPerStep + r_base;
+        return m_tile + (kPasses == 1 ? (r < 32 ? j * 32 + r : 128 + j * 32 + (r - 32)) : pass * 128 + j * 32 + r);
+      };
+      if (whole) {
+        uint8_t* base = reinterpret_cast<uint8_t*>(g.out) + gn * EB;
+#pragma unroll
+        for (int t = 0; t < kSteps; ++t) {
+          uint8_t* dst = base + row_of(t) * g.ldo * EB;
+#ifdef AYK_EXP_NO_STORE
+          if (val[t][0] == 0x12345678 && val[t][1] == 0x7abcdef0)
+#endif
+          if constexpr (NT) __builtin_nontemporal_store(val[t], reinterpret_cast<v4i*>(dst));
+          else *reinterpret_cast<v4i*>(dst) = val[t];
+        }
+      } else {
+#pragma unroll
+      for (int t = 0; t < kSteps; ++t) {
+        const int64_t gm = row_of(t);
+        if (gm < g.M && gn < g.N) {
+          uint8_t* dst = reinterpret_cast<uint8_t*>(g.out) + (gm * g.ldo + gn) * EB;
+          if (gn + 16 / EB <= g.N) {
+#ifdef AYK_EXP_NO_STORE
+            if (val[t][0] == 0x12345678 && val[t][1] == 0x7abcdef0)
+#endif
+            if constexpr (NT) __builtin_nontemporal_store(val[t], reinterpret_cast<v4i*>(dst));
+            else *reinterpret_cast<v4i*>(dst) = val[t];
+          } else {  // N % 4 == 0: the first 8 bytes of the chunk are in range
+            *reinterpret_cast<uint2*>(dst) = make_uint2((uint32_t)val[t][0], (uint32_t)val[t][1]);
+          }
+        }
+      }
+      }
+      // Every lane has read its chunks of the staging tile before it is rewritten.
+      lds_barrier();
+    }
+  }
+}
+
+// The pair kernel's epilogue for one item: fp32 partials (no bias, plain stores) or
+// the final output in its dtype (nontemporal stores).
+template <int MODE>
+__device__ __attribute__((always_inline)) inline void pair_epilogue(const GemmArgs& g, bool partial, const v16f (&acc)[4][4],
+                                                                    const PairScales& ps, int64_t m_tile, int64_t n_tile,
+                                                                    uint8_t* stage_lds, float* table) {
+  if (partial) {
+    pair_epilogue_impl<MODE, AYK_F32, false, false>(g, acc, ps, m_tile, n_tile, stage_lds, table);
+  } else if (g.bias) {
+    if (g.out_dtype == AYK_BF16) pair_epilogue_impl<MODE, AYK_BF16, true, true>(g, acc, ps, m_tile, n_tile, stage_lds, table);
+    else if (g.out_dtype == AYK_F16) pair_epilogue_impl<MODE, AYK_F16, true, true>(g, acc, ps, m_tile, n_tile, stage_lds, table);
+    else pair_epilogue_impl<MODE, AYK_F32, true, true>(g, acc, ps, m_tile, n_tile, stage_lds, table);
+  } else {
+    if (g.out_dtype == AYK_BF16) pair_epilogue_impl<MODE, AYK_BF16, false, true>(g, acc, ps, m_tile, n_tile, stage_lds, table);
+    else if (g.out_dtype == AYK_F16) pair_epilogue_impl<MODE, AYK_F16, false, true>(g, acc, ps, m_tile, n_tile, stage_lds, table);
+    else pair_epilogue_impl<MODE, AYK_F32, false, true>(g, acc, ps, m_tile, n_tile, stage_lds, table);
+  }
+}
+
+#ifdef AYK_EXP_TS
+__device__ uint64_t g_exp_ts[256 * 16 * 4];
+#define EXP_TS(slot) do { if (threadIdx.x == 0 && blockIdx.y == 0 && blockIdx.x < 256 && exp_n < 16) g_exp_ts[(blockIdx.x * 16 + exp_n) * 4 + (slot)] = __builtin_amdgcn_s_memrealtime(); } while (0)
+#else
+#define EXP_TS(slot) do { } while (0)
+#endif
 // One work item of the pair kernel: the tile, its K range and where its result goes.
 struct PairItem {
   GemmArgs g;      // operand bases and K of the item's range; out / ldo / bias of its result
@@ -820,6 +1005,8 @@ __global__ __launch_bounds__(kThreads, 1) void fp8_gemm_pair_kernel(GemmArgs gin
   // stream (across items too), so a chunk is never loaded into the half being read.
   constexpr int kChunkBytes = 2 * kBigTile * 16;
   __shared__ __attribute__((aligned(1024))) uint8_t C[MODE == MODE_MX ? 2 * kChunkBytes : 16];
+  // The epilogue's table of the tile's column scales and bias ([2][256] fp32).
+  __shared__ __attribute__((aligned(16))) float T[512];
 
   const int tid = threadIdx.x, lane = tid & 63;
   const int wave_u = __builtin_amdgcn_readfirstlane(tid >> 6);  // keep descriptors in SGPRs
@@ -1027,6 +1214,10 @@ __global__ __launch_bounds__(kThreads, 1) void fp8_gemm_pair_kernel(GemmArgs gin
         for (int r = 0; r < 16; ++r) acc[i][j][r] = 0.0f;
     half0(kBuf0);  // pair 0, step 0
   };
+#ifdef AYK_EXP_TS
+  int exp_n = 0;
+#endif
+  EXP_TS(0);
   start_item();
 
   // The item loop's body starts with a half1 too (the wait), for the same reason as the
@@ -1050,27 +1241,35 @@ __global__ __launch_bounds__(kThreads, 1) void fp8_gemm_pair_kernel(GemmArgs gin
       half0(kBuf0);
     }
     // The next item (this one again when there is none: its loads then land unused).
+    EXP_TS(1);
     const int next = item + (int)gridDim.x;
     const bool more = next < gin.items;
     const Src nsrc = make_src(pair_item<MODE>(gin, more ? next : item, blockIdx.y));
     const int ncbase = (cbase + npairs / 4) & 1;  // MX: npairs == np, a multiple of 4
     const PairItem it = pair_item<MODE>(gin, item, blockIdx.y);
-    // Pair npairs - 2, step 1: its refill is this item's output scales (loaded one and a
-    // half pairs ahead of the epilogue) and the next item's pair 0 (and code chunk 0).
-    BigScales scales;
+    // Pair npairs - 2, step 1: its refill is the next item's pair 0 (and code chunk 0).
     half1(kBuf0, [&] { read_codes(npairs - 1, 1, (cbase + ((npairs - 1) >> 2)) & 1); },
           [&](uint8_t* cur) {
-            scales = load_big_scales<MODE>(it.g, (int64_t)it.tm * kBigTile, (int64_t)it.tn * kBigTile);
             issue(nsrc, 0, cur);
             issue_codes(nsrc, 0, ncbase);
           }, frags_step0);
     half0(kBuf1);
-    // Pair npairs - 1, step 1: no refill, since its buffer (P1) stages the epilogue, and
-    // no fragment reads (the next item's are read after the epilogue, so that they do
-    // not hold registers through it).
-    half1(kBuf1, [&] { read_codes(0, 1, ncbase); }, [](uint8_t*) {}, [](const uint8_t*) {});
+    // Pair npairs - 1, step 1: no direct loads, since its buffer (P1) stages the
+    // epilogue, and no fragment reads (the next item's are read after the epilogue, so
+    // that they do not hold registers through it); the epilogue's output scales and bias
+    // are loaded in their place.
+    PairScales scales;
+    half1(kBuf1, [&] { read_codes(0, 1, ncbase); },
+          [&](uint8_t*) { scales = load_pair_scales<MODE>(it.g, (int64_t)it.tm * kBigTile, (int64_t)it.tn * kBigTile); },
+          [](const uint8_t*) {});
     // Every wavefront has passed the last pair's barrier: nobody reads P1 any more.
-    big_epilogue<MODE>(it.g, acc, scales, (int64_t)it.tm * kBigTile, (int64_t)it.tn * kBigTile, P1, !it.partial);
+    EXP_TS(2);
+    pair_epilogue<MODE>(it.g, it.partial, acc, scales, (int64_t)it.tm * kBigTile, (int64_t)it.tn * kBigTile, P1, T);
+    EXP_TS(3);
+#ifdef AYK_EXP_TS
+    ++exp_n;
+    EXP_TS(0);
+#endif
     if (!more) break;
     item = next;
     src = nsrc;
@@ -1933,6 +2132,11 @@ int check_common(const char* op, const void* a, int64_t lda, const void* b, int6
 using namespace ayk;
 
 extern "C" {
+
+#ifdef AYK_EXP_TS
+int ayk_exp_read_ts(void* host) { return (int)hipMemcpyFromSymbol(host, HIP_SYMBOL(g_exp_ts), sizeof(g_exp_ts)); }
+int ayk_exp_clear_ts() { static uint64_t z[256 * 16 * 4]; return (int)hipMemcpyToSymbol(HIP_SYMBOL(g_exp_ts), z, sizeof(z)); }
+#endif
 
 size_t ayk_fp8_scaled_mm_workspace_bytes(int64_t M, int64_t N, int64_t K) {
   if (M < 1 || N < 1 || K < 1) return 0;
