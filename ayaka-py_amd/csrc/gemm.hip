@@ -737,6 +737,19 @@ __global__ __launch_bounds__(kThreads, 1) void fp8_gemm_big_kernel(GemmArgs g) {
 // pair is issued when the epilogue is done. Every item's MFMAs, loads and waits are
 // those of the single-tile kernel, so a tile's result is the same bit for bit.
 
+#ifdef AYK_EXP_TS
+__device__ uint64_t g_exp_ts[256 * 16 * 4];
+__device__ uint64_t g_exp_ts2[256 * 16 * 16];
+__device__ int g_exp_n[256];
+#define EXP_TS2(k) do { if (threadIdx.x == 0 && blockIdx.y == 0 && blockIdx.x < 256 && g_exp_n[blockIdx.x] < 16) g_exp_ts2[(blockIdx.x * 16 + g_exp_n[blockIdx.x]) * 16 + (k)] = __builtin_amdgcn_s_memrealtime(); } while (0)
+#else
+#define EXP_TS2(k) do { } while (0)
+#endif
+#ifdef AYK_EXP_TS
+#define EXP_TS(slot) do { if (threadIdx.x == 0 && blockIdx.y == 0 && blockIdx.x < 256 && exp_n < 16) g_exp_ts[(blockIdx.x * 16 + exp_n) * 4 + (slot)] = __builtin_amdgcn_s_memrealtime(); } while (0)
+#else
+#define EXP_TS(slot) do { } while (0)
+#endif
 // Output scales and bias of one item of the persistent pair kernel, as loaded ahead of
 // its epilogue: each thread fetches one column's weight scale and bias (column
 // n_tile + tid) and the activation scales of its lane's four rows; the epilogue writes
@@ -779,7 +792,7 @@ __device__ __attribute__((always_inline)) inline PairScales load_pair_scales(con
 // nontemporal stores for final outputs (NT; fp32 partials that a reduce reads back keep
 // plain stores). The staging tile and the table share the pair buffer `stage_lds`.
 template <int MODE, int OUT, bool BIAS, bool NT>
-__device__ __attribute__((always_inline)) inline void pair_epilogue_impl(const GemmArgs& g, const v16f (&acc)[4][4], const PairScales& ps,
+__device__ __attribute__((always_inline)) inline void pair_epilogue_impl(const GemmArgs& g, v16f (&acc)[4][4], const PairScales& ps,
                                                                          int64_t m_tile, int64_t n_tile, uint8_t* stage_lds,
                                                                          float* table) {
   constexpr int EB = OutBytes<OUT>::v;
@@ -808,6 +821,12 @@ __device__ __attribute__((always_inline)) inline void pair_epilogue_impl(const G
   const int64_t gn = n_tile + (int64_t)c * (16 / EB);
 #pragma unroll
   for (int j = 0; j < 4; ++j) {
+    // The slab's accumulators are pinned in the AGPRs up to here, so that they are read
+    // where they are used: copied out ahead of the epilogue, all 256 do not fit the VGPRs
+    // beside the rest, and their spills made each pass wait for the previous passes'
+    // stores.
+#pragma unroll
+    for (int i = 0; i < 4; ++i) asm volatile("" : "+a"(acc[i][j]));
 #pragma unroll
     for (int pass = 0; pass < kPasses; ++pass) {
       if (kPasses == 1 || wm == pass) {
@@ -851,7 +870,9 @@ __device__ __attribute__((always_inline)) inline void pair_epilogue_impl(const G
           }
         }
       }
+      EXP_TS2(j * 4 + 0);
       lds_barrier();  // the staging writes are visible
+      EXP_TS2(j * 4 + 1);
       // Staged row r: with one pass, r < 32 is tile row j*32 + r (wm = 0) and r >= 32
       // is 128 + j*32 + (r - 32) (wm = 1); with two passes, pass*128 + j*32 + r.
       v4i val[kSteps];
@@ -891,8 +912,10 @@ __device__ __attribute__((always_inline)) inline void pair_epilogue_impl(const G
         }
       }
       }
+      EXP_TS2(j * 4 + 2);
       // Every lane has read its chunks of the staging tile before it is rewritten.
       lds_barrier();
+      EXP_TS2(j * 4 + 3);
     }
   }
 }
@@ -900,7 +923,7 @@ __device__ __attribute__((always_inline)) inline void pair_epilogue_impl(const G
 // The pair kernel's epilogue for one item: fp32 partials (no bias, plain stores) or
 // the final output in its dtype (nontemporal stores).
 template <int MODE>
-__device__ __attribute__((always_inline)) inline void pair_epilogue(const GemmArgs& g, bool partial, const v16f (&acc)[4][4],
+__device__ __attribute__((always_inline)) inline void pair_epilogue(const GemmArgs& g, bool partial, v16f (&acc)[4][4],
                                                                     const PairScales& ps, int64_t m_tile, int64_t n_tile,
                                                                     uint8_t* stage_lds, float* table) {
   if (partial) {
@@ -916,12 +939,6 @@ __device__ __attribute__((always_inline)) inline void pair_epilogue(const GemmAr
   }
 }
 
-#ifdef AYK_EXP_TS
-__device__ uint64_t g_exp_ts[256 * 16 * 4];
-#define EXP_TS(slot) do { if (threadIdx.x == 0 && blockIdx.y == 0 && blockIdx.x < 256 && exp_n < 16) g_exp_ts[(blockIdx.x * 16 + exp_n) * 4 + (slot)] = __builtin_amdgcn_s_memrealtime(); } while (0)
-#else
-#define EXP_TS(slot) do { } while (0)
-#endif
 // One work item of the pair kernel: the tile, its K range and where its result goes.
 struct PairItem {
   GemmArgs g;      // operand bases and K of the item's range; out / ldo / bias of its result
@@ -1206,12 +1223,17 @@ __global__ __launch_bounds__(kThreads, 1) void fp8_gemm_pair_kernel(GemmArgs gin
   read_frags(0, P0, 0);
   read_codes(0, 0, 0);
   auto start_item = [&] __attribute__((always_inline)) {
+    // The zero comes out of an opaque statement ordered after the previous item's
+    // epilogue, so the new accumulators cannot be set up before the old ones are read
+    // (both sets at once do not fit the registers).
+    float zero = 0.0f;
+    asm volatile("" : "+v"(zero));
 #pragma unroll
     for (int i = 0; i < FN; ++i)
 #pragma unroll
       for (int j = 0; j < FM; ++j)
 #pragma unroll
-        for (int r = 0; r < 16; ++r) acc[i][j][r] = 0.0f;
+        for (int r = 0; r < 16; ++r) acc[i][j][r] = zero;
     half0(kBuf0);  // pair 0, step 0
   };
 #ifdef AYK_EXP_TS
@@ -1247,27 +1269,31 @@ __global__ __launch_bounds__(kThreads, 1) void fp8_gemm_pair_kernel(GemmArgs gin
     const Src nsrc = make_src(pair_item<MODE>(gin, more ? next : item, blockIdx.y));
     const int ncbase = (cbase + npairs / 4) & 1;  // MX: npairs == np, a multiple of 4
     const PairItem it = pair_item<MODE>(gin, item, blockIdx.y);
-    // Pair npairs - 2, step 1: its refill is the next item's pair 0 (and code chunk 0).
+    // Pair npairs - 2, step 1: its refill is this item's output scales and bias (one and
+    // a half pairs ahead of the epilogue) and the next item's pair 0 (and code chunk 0).
+    PairScales scales;
     half1(kBuf0, [&] { read_codes(npairs - 1, 1, (cbase + ((npairs - 1) >> 2)) & 1); },
           [&](uint8_t* cur) {
+            scales = load_pair_scales<MODE>(it.g, (int64_t)it.tm * kBigTile, (int64_t)it.tn * kBigTile);
             issue(nsrc, 0, cur);
             issue_codes(nsrc, 0, ncbase);
           }, frags_step0);
     half0(kBuf1);
     // Pair npairs - 1, step 1: no direct loads, since its buffer (P1) stages the
     // epilogue, and no fragment reads (the next item's are read after the epilogue, so
-    // that they do not hold registers through it); the epilogue's output scales and bias
-    // are loaded in their place.
-    PairScales scales;
-    half1(kBuf1, [&] { read_codes(0, 1, ncbase); },
-          [&](uint8_t*) { scales = load_pair_scales<MODE>(it.g, (int64_t)it.tm * kBigTile, (int64_t)it.tn * kBigTile); },
-          [](const uint8_t*) {});
+    // that they do not hold registers through it).
+    half1(kBuf1, [&] { read_codes(0, 1, ncbase); }, [](uint8_t*) {}, [](const uint8_t*) {});
     // Every wavefront has passed the last pair's barrier: nobody reads P1 any more.
     EXP_TS(2);
+#ifdef AYK_EXP_NO_EPI
+    for (int i = 0; i < 4; ++i) for (int j = 0; j < 4; ++j) asm volatile("" :: "a"(acc[i][j]));
+    if (acc[0][0][0] == 1.2345f && scales.sb == 7.0f)
+#endif
     pair_epilogue<MODE>(it.g, it.partial, acc, scales, (int64_t)it.tm * kBigTile, (int64_t)it.tn * kBigTile, P1, T);
     EXP_TS(3);
 #ifdef AYK_EXP_TS
     ++exp_n;
+    if (threadIdx.x == 0 && blockIdx.x < 256) g_exp_n[blockIdx.x] = exp_n;
     EXP_TS(0);
 #endif
     if (!more) break;
@@ -2135,6 +2161,8 @@ extern "C" {
 
 #ifdef AYK_EXP_TS
 int ayk_exp_read_ts(void* host) { return (int)hipMemcpyFromSymbol(host, HIP_SYMBOL(g_exp_ts), sizeof(g_exp_ts)); }
+int ayk_exp_read_ts2(void* host) { return (int)hipMemcpyFromSymbol(host, HIP_SYMBOL(g_exp_ts2), sizeof(g_exp_ts2)); }
+int ayk_exp_clear_n() { static int z[256]; return (int)hipMemcpyToSymbol(HIP_SYMBOL(g_exp_n), z, sizeof(z)); }
 int ayk_exp_clear_ts() { static uint64_t z[256 * 16 * 4]; return (int)hipMemcpyToSymbol(HIP_SYMBOL(g_exp_ts), z, sizeof(z)); }
 #endif
 
