@@ -791,6 +791,9 @@ __device__ __attribute__((always_inline)) inline PairScales load_pair_scales(con
 // registers before any of them is stored (so that the LDS reads pipeline), and
 // nontemporal stores for final outputs (NT; fp32 partials that a reduce reads back keep
 // plain stores). The staging tile and the table share the pair buffer `stage_lds`.
+// Cache policy of a nontemporal buffer store (the NT bit of gfx940+ stores).
+constexpr int kNtPolicy = 2;
+
 template <int MODE, int OUT, bool BIAS, bool NT>
 __device__ __attribute__((always_inline)) inline void pair_epilogue_impl(const GemmArgs& g, v16f (&acc)[4][4], const PairScales& ps,
                                                                          int64_t m_tile, int64_t n_tile, uint8_t* stage_lds,
@@ -807,8 +810,15 @@ __device__ __attribute__((always_inline)) inline void pair_epilogue_impl(const G
   const int wn = wave >> 1, wm = wave & 1, h = lane >> 5, frow = lane & 31;
   float* sb_t = table;  // its own LDS object: its reads need not wait for staging writes
   float* bias_t = table + 256;
-  // A tile inside M x N stores without bounds checks.
-  const bool whole = m_tile + 256 <= g.M && n_tile + 256 <= g.N;
+  // The output tile as a buffer: base at (m_tile, n_tile), records up to the end of the
+  // last row inside M (the launcher keeps 256 rows x ldo within 2 GB), and the columns
+  // inside N.
+  const int ldo_b = (int)(g.ldo * EB);
+  const int64_t rows_left = g.M - m_tile < 256 ? g.M - m_tile : 256;
+  const int cols_left = (int)(g.N - n_tile < 256 ? g.N - n_tile : 256);
+  const bool cols_whole = cols_left == 256;
+  const __amdgpu_buffer_rsrc_t out_rsrc =
+      uniform_rsrc(reinterpret_cast<uint8_t*>(g.out) + (m_tile * g.ldo + n_tile) * EB, (int32_t)((rows_left - 1) * ldo_b + cols_left * EB));
   if constexpr (kScaled || BIAS) {
     if constexpr (kScaled) sb_t[tid] = ps.sb;
     if constexpr (BIAS) bias_t[tid] = ps.bias;
@@ -818,7 +828,6 @@ __device__ __attribute__((always_inline)) inline void pair_epilogue_impl(const G
   constexpr int kRowsPerStep = 256 / kChunksPerRow;
   constexpr int kSteps = kStageRows / kRowsPerStep;
   const int c = tid % kChunksPerRow, r_base = tid / kChunksPerRow;
-  const int64_t gn = n_tile + (int64_t)c * (16 / EB);
 #pragma unroll
   for (int j = 0; j < 4; ++j) {
     // The slab's accumulators are pinned in the AGPRs up to here, so that they are read
@@ -879,38 +888,20 @@ __device__ __attribute__((always_inline)) inline void pair_epilogue_impl(const G
 #pragma unroll
       for (int t = 0; t < kSteps; ++t)
         val[t] = *reinterpret_cast<const v4i*>(stage_lds + (t * kRowsPerStep + r_base) * kRowBytes + c * 16);
-      auto row_of = [&](int t) {
-        const int r = t * kRowsPerStep + r_base;
-        return m_tile + (kPasses == 1 ? (r < 32 ? j * 32 + r : 128 + j * 32 + (r - 32)) : pass * 128 + j * 32 + r);
-      };
-      if (whole) {
-        uint8_t* base = reinterpret_cast<uint8_t*>(g.out) + gn * EB;
-#pragma unroll
-        for (int t = 0; t < kSteps; ++t) {
-          uint8_t* dst = base + row_of(t) * g.ldo * EB;
-#ifdef AYK_EXP_NO_STORE
-          if (val[t][0] == 0x12345678 && val[t][1] == 0x7abcdef0)
-#endif
-          if constexpr (NT) __builtin_nontemporal_store(val[t], reinterpret_cast<v4i*>(dst));
-          else *reinterpret_cast<v4i*>(dst) = val[t];
-        }
-      } else {
+      // Stored through a buffer resource over the tile's rows: a row past M lies past
+      // num_records and is dropped, offsets are 32-bit, and only the last column tile
+      // checks columns. Staged row r (thread row r_base + t kRowsPerStep) is tile row
+      // j*32 + r, or 128 + j*32 + (r - 32) past 32 (one pass); pass*128 + j*32 + r (two).
 #pragma unroll
       for (int t = 0; t < kSteps; ++t) {
-        const int64_t gm = row_of(t);
-        if (gm < g.M && gn < g.N) {
-          uint8_t* dst = reinterpret_cast<uint8_t*>(g.out) + (gm * g.ldo + gn) * EB;
-          if (gn + 16 / EB <= g.N) {
-#ifdef AYK_EXP_NO_STORE
-            if (val[t][0] == 0x12345678 && val[t][1] == 0x7abcdef0)
-#endif
-            if constexpr (NT) __builtin_nontemporal_store(val[t], reinterpret_cast<v4i*>(dst));
-            else *reinterpret_cast<v4i*>(dst) = val[t];
-          } else {  // N % 4 == 0: the first 8 bytes of the chunk are in range
-            *reinterpret_cast<uint2*>(dst) = make_uint2((uint32_t)val[t][0], (uint32_t)val[t][1]);
-          }
+        const int r = t * kRowsPerStep + r_base;
+        const int tile_row = kPasses == 1 ? (r < 32 ? j * 32 + r : 128 + j * 32 + (r - 32)) : pass * 128 + j * 32 + r;
+        const int voff = tile_row * ldo_b + c * 16;
+        if (cols_whole || c * (16 / EB) + 16 / EB <= cols_left) {
+          __builtin_amdgcn_raw_buffer_store_b128(val[t], out_rsrc, voff, 0, NT ? kNtPolicy : 0);
+        } else if (c * (16 / EB) < cols_left) {  // N % 4 == 0: the chunk's first 8 bytes
+          __builtin_amdgcn_raw_buffer_store_b64(__builtin_shufflevector(val[t], val[t], 0, 1), out_rsrc, voff, 0, 0);
         }
-      }
       }
       EXP_TS2(j * 4 + 2);
       // Every lane has read its chunks of the staging tile before it is rewritten.
@@ -1285,10 +1276,6 @@ __global__ __launch_bounds__(kThreads, 1) void fp8_gemm_pair_kernel(GemmArgs gin
     half1(kBuf1, [&] { read_codes(0, 1, ncbase); }, [](uint8_t*) {}, [](const uint8_t*) {});
     // Every wavefront has passed the last pair's barrier: nobody reads P1 any more.
     EXP_TS(2);
-#ifdef AYK_EXP_NO_EPI
-    for (int i = 0; i < 4; ++i) for (int j = 0; j < 4; ++j) asm volatile("" :: "a"(acc[i][j]));
-    if (acc[0][0][0] == 1.2345f && scales.sb == 7.0f)
-#endif
     pair_epilogue<MODE>(it.g, it.partial, acc, scales, (int64_t)it.tm * kBigTile, (int64_t)it.tn * kBigTile, P1, T);
     EXP_TS(3);
 #ifdef AYK_EXP_TS
@@ -2102,8 +2089,10 @@ int launch_gemm(const GemmArgs& g, hipStream_t st, const char* op) {
   // general kernel.
   if constexpr (MODE != MODE_BLOCK) {
   const int64_t out_bytes = g.out_dtype == AYK_F32 ? 4 : 2;
+  // (256 rows of the output, and of an fp32 partial [M, N], within 2 GB: the pair
+  // kernel's epilogue addresses a tile with 32-bit offsets.)
   const bool big_ok = g.K % (MODE == MODE_MX ? BK : kBigK) == 0 && g.M >= 256 && g.N >= 256 && g.N % 4 == 0 &&
-                      (g.ldo * out_bytes) % 16 == 0 && aligned16(g.out) &&
+                      (g.ldo * out_bytes) % 16 == 0 && aligned16(g.out) && g.ldo < (1 << 21) && g.N < (1 << 21) &&
                       (MODE == MODE_MX || (g.sa_dtype == AYK_F32 && g.sb_dtype == AYK_F32 &&
                                            (!g.sb_vec || aligned16(g.sb)))) &&
                       (g.bias == nullptr || (reinterpret_cast<uintptr_t>(g.bias) & 15) == 0);
