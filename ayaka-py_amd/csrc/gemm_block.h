@@ -28,6 +28,7 @@ struct Block256Args {
   int64_t ldo;
   float* ws;         // split-K partials [split, M, N] fp32
   size_t ws_bytes;
+  int nt_stores;     // store final outputs nontemporally (set by the kernels, not callers)
 };
 
 // Grouped (MoE) problem: expert e owns activation rows [expert_offsets[e], + M_e) of

@@ -147,7 +147,8 @@ __device__ __attribute__((always_inline)) inline void block256_epilogue(const Bl
       if (gm < g.M && gn < g.N) {
         uint8_t* out = static_cast<uint8_t*>(g.out) + (gm * g.ldo + gn) * EB;
         if (gn + 16 / EB <= g.N) {
-          *reinterpret_cast<uint4*>(out) = val;
+          if (g.nt_stores) __builtin_nontemporal_store(v4i{(int)val.x, (int)val.y, (int)val.z, (int)val.w}, reinterpret_cast<v4i*>(out));
+          else *reinterpret_cast<uint4*>(out) = val;
         } else {  // the row's last columns, element by element (an expert's N need not be a multiple of 4)
           const uint32_t vw[4] = {val.x, val.y, val.z, val.w};
           const int64_t left = g.N - gn;
@@ -397,6 +398,11 @@ __device__ __attribute__((always_inline)) inline void block256_tile(const Block2
 
   uint8_t* region = (wave_u < 4 ? P0 : P1) + (wave_u & 3) * kRegion;
   if (!rows_live) return;
+#ifdef AYK_EXP_NO_EPI
+  for (int i = 0; i < FN; ++i) for (int j = 0; j < FM; ++j) asm volatile("" :: "v"(U[i][j]));
+  asm volatile("" :: "v"(mu[0]), "v"(mu[1]));
+  return;
+#endif
   if (g.out_dtype == AYK_BF16) block256_epilogue_out<AYK_BF16>(g, U, mu, m_base, n_base, region);
   else if (g.out_dtype == AYK_F16) block256_epilogue_out<AYK_F16>(g, U, mu, m_base, n_base, region);
   else block256_epilogue_out<AYK_F32>(g, U, mu, m_base, n_base, region);
@@ -408,6 +414,7 @@ __global__ __launch_bounds__(kThreads, 1) void fp8_block256_kernel(Block256Args 
   __shared__ __attribute__((aligned(1024))) uint8_t P0[kPairBytes];
   __shared__ __attribute__((aligned(1024))) uint8_t P1[kPairBytes];
   Block256Args g = gin;
+  g.nt_stores = 1;
   int64_t k0 = 0, klen = gin.K;
   if (kps > 0) {
     k0 = (int64_t)blockIdx.y * kps;
@@ -416,6 +423,7 @@ __global__ __launch_bounds__(kThreads, 1) void fp8_block256_kernel(Block256Args 
     g.out = gin.ws + (int64_t)blockIdx.y * gin.M * gin.N;
     g.out_dtype = AYK_F32;
     g.ldo = gin.N;
+    g.nt_stores = 0;  // partials are read back by the reduce: keep them in L2
   }
   int tm, tn;
   big_tile_coords(blockIdx.x, tiles_m, (int)cdiv(g.N, kTile), tm, tn);
@@ -501,6 +509,7 @@ __global__ __launch_bounds__(kThreads, 1) void fp8_grouped_block256_kernel(Group
   }
   const int64_t kb_total = ga.k / kPairK;
   Block256Args g{};
+  g.nt_stores = 1;
   g.a = ga.a + p.off * ga.k;
   g.lda = ga.k;
   g.w = ga.b + (int64_t)e * ga.n * ga.k;
