@@ -737,19 +737,6 @@ __global__ __launch_bounds__(kThreads, 1) void fp8_gemm_big_kernel(GemmArgs g) {
 // pair is issued when the epilogue is done. Every item's MFMAs, loads and waits are
 // those of the single-tile kernel, so a tile's result is the same bit for bit.
 
-#ifdef AYK_EXP_TS
-__device__ uint64_t g_exp_ts[256 * 16 * 4];
-__device__ uint64_t g_exp_ts2[256 * 16 * 16];
-__device__ int g_exp_n[256];
-#define EXP_TS2(k) do { if (threadIdx.x == 0 && blockIdx.y == 0 && blockIdx.x < 256 && g_exp_n[blockIdx.x] < 16) g_exp_ts2[(blockIdx.x * 16 + g_exp_n[blockIdx.x]) * 16 + (k)] = __builtin_amdgcn_s_memrealtime(); } while (0)
-#else
-#define EXP_TS2(k) do { } while (0)
-#endif
-#ifdef AYK_EXP_TS
-#define EXP_TS(slot) do { if (threadIdx.x == 0 && blockIdx.y == 0 && blockIdx.x < 256 && exp_n < 16) g_exp_ts[(blockIdx.x * 16 + exp_n) * 4 + (slot)] = __builtin_amdgcn_s_memrealtime(); } while (0)
-#else
-#define EXP_TS(slot) do { } while (0)
-#endif
 // Output scales and bias of one item of the persistent pair kernel, as loaded ahead of
 // its epilogue: each thread fetches one column's weight scale and bias (column
 // n_tile + tid) and the activation scales of its lane's four rows; the epilogue writes
@@ -879,9 +866,7 @@ __device__ __attribute__((always_inline)) inline void pair_epilogue_impl(const G
           }
         }
       }
-      EXP_TS2(j * 4 + 0);
       lds_barrier();  // the staging writes are visible
-      EXP_TS2(j * 4 + 1);
       // Staged row r: with one pass, r < 32 is tile row j*32 + r (wm = 0) and r >= 32
       // is 128 + j*32 + (r - 32) (wm = 1); with two passes, pass*128 + j*32 + r.
       v4i val[kSteps];
@@ -903,10 +888,8 @@ __device__ __attribute__((always_inline)) inline void pair_epilogue_impl(const G
           __builtin_amdgcn_raw_buffer_store_b64(__builtin_shufflevector(val[t], val[t], 0, 1), out_rsrc, voff, 0, 0);
         }
       }
-      EXP_TS2(j * 4 + 2);
       // Every lane has read its chunks of the staging tile before it is rewritten.
       lds_barrier();
-      EXP_TS2(j * 4 + 3);
     }
   }
 }
@@ -1227,10 +1210,6 @@ __global__ __launch_bounds__(kThreads, 1) void fp8_gemm_pair_kernel(GemmArgs gin
         for (int r = 0; r < 16; ++r) acc[i][j][r] = zero;
     half0(kBuf0);  // pair 0, step 0
   };
-#ifdef AYK_EXP_TS
-  int exp_n = 0;
-#endif
-  EXP_TS(0);
   start_item();
 
   // The item loop's body starts with a half1 too (the wait), for the same reason as the
@@ -1254,7 +1233,6 @@ __global__ __launch_bounds__(kThreads, 1) void fp8_gemm_pair_kernel(GemmArgs gin
       half0(kBuf0);
     }
     // The next item (this one again when there is none: its loads then land unused).
-    EXP_TS(1);
     const int next = item + (int)gridDim.x;
     const bool more = next < gin.items;
     const Src nsrc = make_src(pair_item<MODE>(gin, more ? next : item, blockIdx.y));
@@ -1275,14 +1253,7 @@ __global__ __launch_bounds__(kThreads, 1) void fp8_gemm_pair_kernel(GemmArgs gin
     // that they do not hold registers through it).
     half1(kBuf1, [&] { read_codes(0, 1, ncbase); }, [](uint8_t*) {}, [](const uint8_t*) {});
     // Every wavefront has passed the last pair's barrier: nobody reads P1 any more.
-    EXP_TS(2);
     pair_epilogue<MODE>(it.g, it.partial, acc, scales, (int64_t)it.tm * kBigTile, (int64_t)it.tn * kBigTile, P1, T);
-    EXP_TS(3);
-#ifdef AYK_EXP_TS
-    ++exp_n;
-    if (threadIdx.x == 0 && blockIdx.x < 256) g_exp_n[blockIdx.x] = exp_n;
-    EXP_TS(0);
-#endif
     if (!more) break;
     item = next;
     src = nsrc;
@@ -2148,12 +2119,6 @@ using namespace ayk;
 
 extern "C" {
 
-#ifdef AYK_EXP_TS
-int ayk_exp_read_ts(void* host) { return (int)hipMemcpyFromSymbol(host, HIP_SYMBOL(g_exp_ts), sizeof(g_exp_ts)); }
-int ayk_exp_read_ts2(void* host) { return (int)hipMemcpyFromSymbol(host, HIP_SYMBOL(g_exp_ts2), sizeof(g_exp_ts2)); }
-int ayk_exp_clear_n() { static int z[256]; return (int)hipMemcpyToSymbol(HIP_SYMBOL(g_exp_n), z, sizeof(z)); }
-int ayk_exp_clear_ts() { static uint64_t z[256 * 16 * 4]; return (int)hipMemcpyToSymbol(HIP_SYMBOL(g_exp_ts), z, sizeof(z)); }
-#endif
 
 size_t ayk_fp8_scaled_mm_workspace_bytes(int64_t M, int64_t N, int64_t K) {
   if (M < 1 || N < 1 || K < 1) return 0;

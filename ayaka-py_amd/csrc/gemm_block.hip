@@ -398,11 +398,6 @@ __device__ __attribute__((always_inline)) inline void block256_tile(const Block2
 
   uint8_t* region = (wave_u < 4 ? P0 : P1) + (wave_u & 3) * kRegion;
   if (!rows_live) return;
-#ifdef AYK_EXP_NO_EPI
-  for (int i = 0; i < FN; ++i) for (int j = 0; j < FM; ++j) asm volatile("" :: "v"(U[i][j]));
-  asm volatile("" :: "v"(mu[0]), "v"(mu[1]));
-  return;
-#endif
   if (g.out_dtype == AYK_BF16) block256_epilogue_out<AYK_BF16>(g, U, mu, m_base, n_base, region);
   else if (g.out_dtype == AYK_F16) block256_epilogue_out<AYK_F16>(g, U, mu, m_base, n_base, region);
   else block256_epilogue_out<AYK_F32>(g, U, mu, m_base, n_base, region);
