@@ -778,6 +778,17 @@ __device__ __attribute__((always_inline)) inline PairScales load_pair_scales(con
 // registers before any of them is stored (so that the LDS reads pipeline), and
 // nontemporal stores for final outputs (NT; fp32 partials that a reduce reads back keep
 // plain stores). The staging tile and the table share the pair buffer `stage_lds`.
+// An accumulator element read out of its AGPR where the epilogue uses it. The read is
+// an opaque instruction, so the compiler neither copies the 256 accumulators into VGPRs
+// ahead of the epilogue (they do not fit beside the rest; their spills made every pass
+// wait for the previous passes' stores) nor moves them between AGPRs.
+template <int MODE>
+__device__ inline float acc_read(float a) {
+  float v;
+  asm volatile("v_accvgpr_read_b32 %0, %1" : "=v"(v) : "a"(a));
+  return acc_value<MODE>(v);
+}
+
 // Cache policy of a nontemporal buffer store (the NT bit of gfx940+ stores).
 constexpr int kNtPolicy = 2;
 
@@ -795,6 +806,10 @@ __device__ __attribute__((always_inline)) inline void pair_epilogue_impl(const G
   asm volatile("" : "+v"(tid));  // lane addresses are not hoisted out of the item loop
   const int lane = tid & 63, wave = tid >> 6;
   const int wn = wave >> 1, wm = wave & 1, h = lane >> 5, frow = lane & 31;
+  // The accumulator reads below are opaque to the compiler's hazard tracking: wait out
+  // the longest MFMA-result-to-VALU-read latency (19 wait states for a 16-pass MFMA)
+  // behind the kernel's last MFMA explicitly.
+  asm volatile("s_nop 7\n\ts_nop 7\n\ts_nop 7" ::: "memory");
   float* sb_t = table;  // its own LDS object: its reads need not wait for staging writes
   float* bias_t = table + 256;
   // The output tile as a buffer: base at (m_tile, n_tile), records up to the end of the
@@ -817,12 +832,6 @@ __device__ __attribute__((always_inline)) inline void pair_epilogue_impl(const G
   const int c = tid % kChunksPerRow, r_base = tid / kChunksPerRow;
 #pragma unroll
   for (int j = 0; j < 4; ++j) {
-    // The slab's accumulators are pinned in the AGPRs up to here, so that they are read
-    // where they are used: copied out ahead of the epilogue, all 256 do not fit the VGPRs
-    // beside the rest, and their spills made each pass wait for the previous passes'
-    // stores.
-#pragma unroll
-    for (int i = 0; i < 4; ++i) asm volatile("" : "+a"(acc[i][j]));
 #pragma unroll
     for (int pass = 0; pass < kPasses; ++pass) {
       if (kPasses == 1 || wm == pass) {
@@ -848,7 +857,7 @@ __device__ __attribute__((always_inline)) inline void pair_epilogue_impl(const G
             float v[4];
 #pragma unroll
             for (int qq = 0; qq < 4; ++qq) {
-              float y = acc_value<MODE>(acc[i][j][grp * 4 + qq]);
+              float y = acc_read<MODE>(acc[i][j][grp * 4 + qq]);
               if constexpr (kScaled) y = (y * ps.sa[j]) * sbv[qq];
               v[qq] = BIAS ? y + bv[qq] : y;
             }
@@ -857,9 +866,15 @@ __device__ __attribute__((always_inline)) inline void pair_epilogue_impl(const G
             } else if constexpr (OUT == AYK_BF16) {
               *reinterpret_cast<uint2*>(srow + nl * 2) = make_uint2(pack_bf16x2(v[0], v[1]), pack_bf16x2(v[2], v[3]));
             } else {
+              // The fp32 value is rounded to fp16 on its own (torch's cast of the fp32
+              // result): left free, the compiler fuses the last multiply into the
+              // conversion (v_fma_mixlo_f16, one rounding), which differs at fp16 ties.
               uint16_t b[4];
 #pragma unroll
-              for (int qq = 0; qq < 4; ++qq) b[qq] = f32_to_f16_bits(v[qq]);
+              for (int qq = 0; qq < 4; ++qq) {
+                asm volatile("" : "+v"(v[qq]));
+                b[qq] = f32_to_f16_bits(v[qq]);
+              }
               *reinterpret_cast<uint2*>(srow + nl * 2) =
                   make_uint2((uint32_t)b[0] | ((uint32_t)b[1] << 16), (uint32_t)b[2] | ((uint32_t)b[3] << 16));
             }

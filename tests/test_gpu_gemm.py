@@ -273,6 +273,29 @@ def test_decode_batch_scales_not_16_byte_aligned(gpu):
     assert_linear_close(out, ref, "blockwise decode batch, offset scales")
 
 
+@pytest.mark.parametrize("m,n,k,rowwise,with_bias", [(2048, 4096, 1024, True, True), (1300, 11712, 1536, False, False),
+                                                    (4096, 37888, 512, True, False)])
+def test_fp8_scaled_mm_half_outputs_are_the_fp32_result_rounded(gpu, m, n, k, rowwise, with_bias):
+    """The 16-bit outputs of the 256 x 256 kernel are its fp32 result rounded once to
+    nearest even (torch's cast), bit for bit: no step of the epilogue may fold a multiply
+    into the conversion (one rounding of the exact product differs at fp16 ties)."""
+    from ayaka.kernel.hip import fp8_scaled_mm
+
+    _say(f"fp8_scaled_mm 16-bit outputs vs rounded fp32 m={m} n={n} k={k} rowwise={rowwise} bias={with_bias}")
+    g = torch.Generator(device=gpu).manual_seed(m + n)
+    a = (torch.randn(m, k, device=gpu, generator=g) * 40).clamp(-448, 448).to(FP8)
+    w = (torch.randn(n, k, device=gpu, generator=g) * 40).clamp(-448, 448).to(FP8)
+    sa = torch.rand(m, device=gpu, generator=g) * 0.01 + 1e-3
+    sb = torch.rand(n, device=gpu, generator=g) * 0.01 + 1e-3
+    if not rowwise:
+        sa, sb = sa[:1].reshape(()), sb[:1].reshape(())
+    bias = torch.randn(n, device=gpu, generator=g).float() if with_bias else None
+    y32 = fp8_scaled_mm(a, w.t(), sa, sb, bias, out=torch.empty(m, n, dtype=torch.float32, device=gpu))
+    for dt in (torch.float16, torch.bfloat16):
+        y = fp8_scaled_mm(a, w.t(), sa, sb, bias, out=torch.empty(m, n, dtype=dt, device=gpu))
+        assert torch.equal(y.view(torch.int16), y32.to(dt).view(torch.int16)), f"{dt} output is not the rounded fp32 result"
+
+
 # 276 tiles of 256 x 256: one whole round, then a last round of 20 tiles that the pair
 # kernel splits over K (three 512-K pieces each) into the workspace, ragged M and N.
 TAIL_MNK = (1300, 11712, 1536)
