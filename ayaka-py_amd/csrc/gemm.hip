@@ -86,6 +86,11 @@ struct GemmArgs {
 __device__ inline v16f mfma(const v8i& wa, const v8i& ab, const v16f& c, int sw, int sa) {
   return __builtin_amdgcn_mfma_scale_f32_32x32x64_f8f6f4(wa, ab, c, 0, 0, 0, sw, 0, sa);
 }
+// The same with the scale codes taken from byte SEL of the scale registers.
+template <int SEL>
+__device__ inline v16f mfma_sel(const v8i& wa, const v8i& ab, const v16f& c, int sw, int sa) {
+  return __builtin_amdgcn_mfma_scale_f32_32x32x64_f8f6f4(wa, ab, c, 0, 0, SEL, sw, SEL, sa);
+}
 typedef int v16i __attribute__((ext_vector_type(16)));
 typedef int v4i __attribute__((ext_vector_type(4)));
 // One 64-K step of a 32x32 tile in the mode's arithmetic. INT8: two
@@ -1115,16 +1120,16 @@ __global__ __launch_bounds__(kThreads, 1) void fp8_gemm_pair_kernel(GemmArgs gin
   // MXFP8: the codes of a fragment row for one pair are one dword (four 32-K blocks)
   // of its chunk row in C. Those of pair p + 1 are read during pair p into the second
   // set and moved to the first at the pair's end. Step half t of the pair uses block
-  // 2 t + h in lane half h: the dword shifted right by 8 (2 t + h) (the MFMA reads the
-  // low byte of its scale operands).
+  // 2 t + h in lane half h: the dword is shifted right by 8 h once when read, and the
+  // MFMA's scale byte select takes byte 2 t.
   uint32_t wc[2][FN], ac[2][FM];
   auto read_codes = [&](int p, int set, int half) {
     if constexpr (MODE == MODE_MX) {
       const int base = half * kChunkBytes + (p & 3) * 4;
 #pragma unroll
-      for (int i = 0; i < FN; ++i) wc[set][i] = *reinterpret_cast<const uint32_t*>(C + (base + (wn * 128 + i * 32 + frow) * 16));
+      for (int i = 0; i < FN; ++i) wc[set][i] = *reinterpret_cast<const uint32_t*>(C + (base + (wn * 128 + i * 32 + frow) * 16)) >> (8 * h);
 #pragma unroll
-      for (int j = 0; j < FM; ++j) ac[set][j] = *reinterpret_cast<const uint32_t*>(C + (base + (256 + wm * 128 + j * 32 + frow) * 16));
+      for (int j = 0; j < FM; ++j) ac[set][j] = *reinterpret_cast<const uint32_t*>(C + (base + (256 + wm * 128 + j * 32 + frow) * 16)) >> (8 * h);
     }
   };
   auto next_codes = [&] {
@@ -1141,8 +1146,10 @@ __global__ __launch_bounds__(kThreads, 1) void fp8_gemm_pair_kernel(GemmArgs gin
 #pragma unroll
       for (int i = 0; i < FN; ++i) {
         if constexpr (MODE == MODE_MX) {
-          const int sh = 8 * (2 * set + h);  // fragment set `set` holds step half t = set
-          acc[i][j] = mfma(wf[set][i], af[set][j], acc[i][j], (int)(wc[0][i] >> sh), (int)(ac[0][j] >> sh));
+          // The code dwords hold blocks h, h + 2 in bytes 0, 2 (shifted by 8 h when read):
+          // step half t = set takes byte 2 t through the MFMA's scale byte select.
+          if (set == 0) acc[i][j] = mfma_sel<0>(wf[0][i], af[0][j], acc[i][j], (int)wc[0][i], (int)ac[0][j]);
+          else acc[i][j] = mfma_sel<2>(wf[1][i], af[1][j], acc[i][j], (int)wc[0][i], (int)ac[0][j]);
         } else {
           acc[i][j] = mma<MODE>(wf[set][i], af[set][j], acc[i][j], kScaleOne, kScaleOne);
         }
