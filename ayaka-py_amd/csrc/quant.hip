@@ -213,6 +213,15 @@ __device__ inline float floor_amax(float amax) {
   return amax < 1e-10f ? 1e-10f : amax;
 }
 
+// A 16-byte vector of an activation row read once and not again: a nontemporal load, so
+// that the stream does not displace from the caches what the GEMM reads next (its
+// weights, and the quantized activation this kernel writes). Per-token K = 3584 at
+// M = 4096: 3.15 -> 3.54 TB/s.
+__device__ inline uint4 load_stream(const uint4* p) {
+  typedef int nt4 __attribute__((ext_vector_type(4)));
+  const nt4 t = __builtin_nontemporal_load(reinterpret_cast<const nt4*>(p));
+  return make_uint4((uint32_t)t[0], (uint32_t)t[1], (uint32_t)t[2], (uint32_t)t[3]);
+}
 // ------------------------------------------------------------ rowwise (a1)
 // One 256-thread block per row. VPT > 0 keeps VPT 16-byte vectors per thread in
 // registers (one HBM read of x); VPT == 0 walks the row twice (very long rows).
@@ -235,7 +244,7 @@ __global__ __launch_bounds__(kQuantThreads) void per_token_quant_vec_kernel(
     for (int i = 0; i < VPT; ++i) {
       const int64_t v = threadIdx.x + (int64_t)i * kQuantThreads;
       if (v < nvec) {
-        cache[i] = xr[v];
+        cache[i] = load_stream(xr + v);
         bits = absbits_max<T>(cache[i], bits);
       }
     }
@@ -297,7 +306,7 @@ __global__ __launch_bounds__(kQuantThreads) void per_token_quant_wave_kernel(
 #pragma unroll
   for (int i = 0; i < VPT; ++i) {
     const int64_t v = lane + (int64_t)i * kWave;
-    if (v < nvec) cache[i] = xr[v];
+    if (v < nvec) cache[i] = load_stream(xr + v);
   }
   float f[V];
   uint32_t bits = 0;

@@ -138,6 +138,16 @@ def _cfg2_projections(layers, launches_per_graph=24):
         gbs = _gemv_bytes(n, k) / (mean * 1e-3) / 1e9
         rows[name] = {"N": n, "K": k, "us": round(mean * 1e3, 2), "GB/s": round(gbs, 1),
                       "frac": round(gbs / HBM_PEAK_GBS, 4)}
+    # Per-launch floor: a kernel node that does (almost) nothing -- a one-element fill --
+    # in the same kind of graph. Each projection's time above that floor is its streaming
+    # time; the floor is paid once per kernel of a decode step however fast the kernel.
+    tiny = torch.empty(1, dtype=torch.float32, device=layers[0][4].device)
+    floor, _ = _graph_per_launch(lambda i: tiny.zero_(), launches_per_graph)
+    rows["launch_floor_us"] = round(floor * 1e3, 2)
+    for name, *_ in layers:
+        r = rows[name]
+        r["us_above_floor"] = round(r["us"] - rows["launch_floor_us"], 2)
+        r["GB/s_above_floor"] = round(_gemv_bytes(r["N"], r["K"]) / (r["us_above_floor"] * 1e-6) / 1e9, 1)
     return rows
 
 
