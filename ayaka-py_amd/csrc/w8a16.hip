@@ -573,6 +573,21 @@ typedef uint32_t v4u __attribute__((ext_vector_type(4)));
 template <int NB, int NS>
 __device__ inline void stage_reads(v4u (&b)[NB], uint32_t (&w)[NS], const uint32_t (&ab)[NB], const uint32_t (&as)[NS]);
 template <>
+__device__ inline void stage_reads<3, 1>(v4u (&b)[3], uint32_t (&w)[1], const uint32_t (&ab)[3], const uint32_t (&as)[1]) {
+  asm volatile(AYK_R128(0, 4) AYK_R128(1, 5) AYK_R128(2, 6) AYK_R32(3, 7) "s_waitcnt lgkmcnt(0)"
+               : "=&v"(b[0]), "=&v"(b[1]), "=&v"(b[2]), "=&v"(w[0])
+               : "v"(ab[0]), "v"(ab[1]), "v"(ab[2]), "v"(as[0])
+               : "memory");
+}
+template <>
+__device__ inline void stage_reads<5, 1>(v4u (&b)[5], uint32_t (&w)[1], const uint32_t (&ab)[5], const uint32_t (&as)[1]) {
+  asm volatile(AYK_R128(0, 6) AYK_R128(1, 7) AYK_R128(2, 8) AYK_R128(3, 9) AYK_R128(4, 10) AYK_R32(5, 11)
+               "s_waitcnt lgkmcnt(0)"
+               : "=&v"(b[0]), "=&v"(b[1]), "=&v"(b[2]), "=&v"(b[3]), "=&v"(b[4]), "=&v"(w[0])
+               : "v"(ab[0]), "v"(ab[1]), "v"(ab[2]), "v"(ab[3]), "v"(ab[4]), "v"(as[0])
+               : "memory");
+}
+template <>
 __device__ inline void stage_reads<4, 2>(v4u (&b)[4], uint32_t (&w)[2], const uint32_t (&ab)[4], const uint32_t (&as)[2]) {
   asm volatile(AYK_R128(0, 6) AYK_R128(1, 7) AYK_R128(2, 8) AYK_R128(3, 9) AYK_R32(4, 10) AYK_R32(5, 11)
                "s_waitcnt lgkmcnt(0)"
@@ -620,7 +635,7 @@ __device__ inline v4f mfma16x16(const v8s& a, const v8s& b, const v4f& c) {
   }
 }
 
-template <bool BF16, bool ROW_SCALE, int RT, int XJ, int D>
+template <bool BF16, bool ROW_SCALE, int RT, int XJ>
 __global__ __launch_bounds__(kRsWaves * kWave) void w8a16_rows_kernel(RsArgs a) {
   constexpr int R = 16 * RT;
   constexpr int MP = 8 * XJ;                 // activation rows staged (M rounded up to 8)
@@ -634,8 +649,9 @@ __global__ __launch_bounds__(kRsWaves * kWave) void w8a16_rows_kernel(RsArgs a) 
   constexpr int kDma = R / (4 * kRsWaves);   // weight load instructions per wavefront per stage
   constexpr int kSDma = ROW_SCALE ? 0 : RT;  // scale load instructions per wavefront per stage
   static_assert(R % (4 * kRsWaves) == 0, "whole load instructions per wavefront");
+  constexpr int kOps = kDma + XJ + kSDma;  // vector-memory instructions per stage and wavefront
   static_assert(R * (kRsStageK / 16) == kRsWaves * kSDma * kWave || ROW_SCALE, "scale entries per stage");
-  static_assert(D == 4, "four stage buffers");
+  constexpr int D = 4;  // stage buffers (a deeper ring measured no faster)
   // Four distinct LDS objects for the ring, and the per-row scale words (lane i of the
   // one load writes word i).
   __shared__ __attribute__((aligned(1024))) uint8_t B0[kStageBytes];
@@ -661,7 +677,6 @@ __global__ __launch_bounds__(kRsWaves * kWave) void w8a16_rows_kernel(RsArgs a) 
   // Weight DMA: load instruction j (0 .. kDma - 1) of wavefront w covers rows
   // 4 (w kDma + j) + lane / 16; lane fetches the logical chunk that lands at physical
   // chunk lane % 16 of its row.
-  constexpr int kOps = kDma + XJ + kSDma;  // vector-memory instructions per stage and wavefront
   const uint8_t* dsrc[kDma + XJ];
   int dlds[kDma + XJ];
 #pragma unroll
@@ -847,9 +862,10 @@ __global__ __launch_bounds__(256) void w8a16_rows_reduce(RsArgs a, int split) {
   a.out[m * a.ldo + n] = round16<BF16>(v);
 }
 
-// Launch plan from the shapes alone (the workspace query reproduces it). R = 64 rows
-// per workgroup for M > 16 when that still gives >= 384 workgroups (the activation
-// stage is then shared by more rows), else 32. K is split across workgroups only while
+// Launch plan from the shapes alone (the workspace query reproduces it). R = 16 rows
+// per workgroup when K is too short to split and those workgroups are one per CU (up
+// to 16 activation rows: two per CU); else R = 64 for M > 16 when that still gives
+// >= 384 workgroups (the activation stage is then shared by more rows), else 32. K is split across workgroups only while
 // each split keeps >= 4096 K and there are < 512 workgroups: a split costs a second
 // launch and fp32 partials, which measured slower than fewer workgroups at K = 4096
 // (Llama-3-8B qkv / o / gate_up) and faster at K = 14336 (down, split 2).
@@ -863,7 +879,13 @@ RsPlan rows_plan(int64_t M, int64_t N, int64_t K, int64_t bx) {
   const bool row_scale = bx >= K;
   if (M < 2 || M > 32 || N < 1 || K < kRsStageK || K % kRsStageK || K >= (int64_t(1) << 31) || (!row_scale && bx % 16)) return p;
   p.xj = (int)cdiv(M, 8);
-  p.rt = M > 16 && cdiv(N, 64) >= 384 ? 4 : 2;
+  // 16 rows per workgroup re-read the activations more often per weight byte, but the
+  // extra workgroups put every CU to work: Llama-3-8B o (K = 4096) at M = 16
+  // 9.5 -> 7.3 us, at M = 32 10.9 -> 8.2 us; qkv at M = 16 9.8 -> 8.4 us (at M = 32,
+  // 1.5 workgroups per CU, slower); with a K split (down, K = 14336) slower.
+  const int64_t rows16 = cdiv(N, 16);
+  const bool narrow = K < 2 * 4096 && (rows16 <= 256 || (M <= 16 && rows16 <= 512));
+  p.rt = narrow ? 1 : (M > 16 && cdiv(N, 64) >= 384 ? 4 : 2);
   const int64_t tiles = cdiv(N, 16 * p.rt);
   int64_t split = 1;
   while (tiles * split < 512 && K / (split * 2) >= 4096 && (K / kRsStageK) % (split * 2) == 0) split *= 2;
@@ -876,29 +898,26 @@ size_t rows_workspace(const RsPlan& p, int64_t M, int64_t N) {
   return p.ok && p.split > 1 ? (size_t)p.split * (size_t)M * (size_t)N * sizeof(float) : 0;
 }
 
+template <bool BF16, bool ROW_SCALE, int RT>
+void launch_rows_rt(const RsPlan& p, const RsArgs& a, hipStream_t st) {
+  const dim3 grid((unsigned)cdiv(a.N, 16 * RT), (unsigned)p.split), block(kRsWaves * kWave);
+  switch (p.xj) {
+    case 1: hipLaunchKernelGGL((w8a16_rows_kernel<BF16, ROW_SCALE, RT, 1>), grid, block, 0, st, a); break;
+    case 2: hipLaunchKernelGGL((w8a16_rows_kernel<BF16, ROW_SCALE, RT, 2>), grid, block, 0, st, a); break;
+    case 3: hipLaunchKernelGGL((w8a16_rows_kernel<BF16, ROW_SCALE, RT, 3>), grid, block, 0, st, a); break;
+    default: hipLaunchKernelGGL((w8a16_rows_kernel<BF16, ROW_SCALE, RT, 4>), grid, block, 0, st, a); break;
+  }
+}
 template <bool BF16, bool ROW_SCALE>
 void launch_rows_kernel(const RsPlan& p, const RsArgs& a, hipStream_t st) {
-  const dim3 grid((unsigned)cdiv(a.N, 16 * p.rt), (unsigned)p.split), block(kRsWaves * kWave);
-  constexpr int D = 4;
-  if (p.rt == 4) {
-    switch (p.xj) {
-      case 1: hipLaunchKernelGGL((w8a16_rows_kernel<BF16, ROW_SCALE, 4, 1, D>), grid, block, 0, st, a); break;
-      case 2: hipLaunchKernelGGL((w8a16_rows_kernel<BF16, ROW_SCALE, 4, 2, D>), grid, block, 0, st, a); break;
-      case 3: hipLaunchKernelGGL((w8a16_rows_kernel<BF16, ROW_SCALE, 4, 3, D>), grid, block, 0, st, a); break;
-      default: hipLaunchKernelGGL((w8a16_rows_kernel<BF16, ROW_SCALE, 4, 4, D>), grid, block, 0, st, a); break;
-    }
-  } else {
-    switch (p.xj) {
-      case 1: hipLaunchKernelGGL((w8a16_rows_kernel<BF16, ROW_SCALE, 2, 1, D>), grid, block, 0, st, a); break;
-      case 2: hipLaunchKernelGGL((w8a16_rows_kernel<BF16, ROW_SCALE, 2, 2, D>), grid, block, 0, st, a); break;
-      case 3: hipLaunchKernelGGL((w8a16_rows_kernel<BF16, ROW_SCALE, 2, 3, D>), grid, block, 0, st, a); break;
-      default: hipLaunchKernelGGL((w8a16_rows_kernel<BF16, ROW_SCALE, 2, 4, D>), grid, block, 0, st, a); break;
-    }
-  }
+  if (p.rt == 4) launch_rows_rt<BF16, ROW_SCALE, 4>(p, a, st);
+  else if (p.rt == 2) launch_rows_rt<BF16, ROW_SCALE, 2>(p, a, st);
+  else launch_rows_rt<BF16, ROW_SCALE, 1>(p, a, st);
 }
 
 template <bool BF16>
 int launch_rows(const RsPlan& p, RsArgs a, size_t ws_bytes, hipStream_t st) {
+  note_plan("w8a16 rows rt=%d xj=%d split=%d", p.rt, p.xj, p.split);
   a.k_per_split = p.kps;
   if (p.split > 1) {
     const size_t need = rows_workspace(p, a.M, a.N);
@@ -1345,6 +1364,7 @@ bool launch_stream_kernel(const StPlan& p, const RsArgs& a, hipStream_t st) {
 
 template <bool BF16>
 int launch_stream(const StPlan& p, RsArgs a, size_t ws_bytes, hipStream_t st) {
+  note_plan("w8a16 stream mp=%d tw=%d ks=%d split=%d", p.mp, p.tw, p.ks, p.split);
   a.k_per_split = p.kps;
   if (p.split > 1) {
     const size_t need = stream_workspace(p, a.M, a.N);

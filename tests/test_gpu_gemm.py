@@ -801,6 +801,32 @@ def test_weight_only_gemm_stream(gpu, m, n, k, case, xdt):
     assert_linear_close(y, ref, "weight_only_gemm stream")
 
 
+# Narrow decode projections (K too short to split) run the row-stream kernel with 16
+# weight rows per workgroup while those workgroups fit one per CU (two up to 16 rows):
+# every staged activation row count (8, 16, 24, 32), ragged N, every scale layout, fp16.
+# Each case asserts the plan; a longer K keeps the 32-row workgroups and its K split.
+@pytest.mark.parametrize("m,n,k,case,xdt,plan", [
+    (6, 300, 768, "channel", torch.bfloat16, "w8a16 rows rt=1 xj=1 split=1"),
+    (10, 4096, 4096, "channel_e8m0", torch.bfloat16, "w8a16 rows rt=1 xj=2 split=1"),
+    (16, 6144, 4096, "block128", torch.float16, "w8a16 rows rt=1 xj=2 split=1"),
+    (20, 1000, 1024, "e8m0_32", torch.bfloat16, "w8a16 rows rt=1 xj=3 split=1"),
+    (32, 4090, 2048, "block128", torch.bfloat16, "w8a16 rows rt=1 xj=4 split=1"),
+    (32, 6144, 4096, "channel", torch.float16, "w8a16 rows rt=2 xj=4 split=1"),
+    (32, 4096, 14336, "channel", torch.bfloat16, "w8a16 rows rt=2 xj=4 split=2"),
+])
+def test_weight_only_gemm_rows_plans(gpu, m, n, k, case, xdt, plan):
+    from ayaka.kernel.hip import fp8_weight_only_gemm
+
+    _say(f"fp8_weight_only_gemm rows m={m} n={n} k={k} case={case} x={xdt}")
+    w, scale, by, bx, sdt = _weight_only_operands(n, k, case)
+    x = torch.randn(m, k, generator=_gen(2)).to(xdt)
+    y = fp8_weight_only_gemm(x.to(gpu), w.to(gpu), scale.to(gpu), -(-k // bx), by, bx, sdt)
+    assert _plan() == plan
+    ref = ora.fp8_weight_only_gemm(x, w, scale, -(-k // bx), by, bx, sdt)
+    assert y.dtype == xdt and y.shape == (m, n)
+    assert_linear_close(y, ref, "weight_only_gemm rows")
+
+
 # ------------------------------------------------------------------ linear entry points
 @pytest.mark.parametrize("m", [1, 8, 40])
 @pytest.mark.parametrize("recipe", ["w8a8_rowwise", "w8a8_dynamic_per_tensor", "w8a8_block128"])
