@@ -34,13 +34,17 @@ from ayaka.kernel.hip._host import require_cuda, require_dtype, require_tensor
 from ayaka.kernel.hip.gemm.fp8_gemm import fp8_blockwise_mm, fp8_scaled_mm
 from ayaka.kernel.hip.gemm.fp8_gemv import fp8_weight_only_gemv
 from ayaka.kernel.hip.gemm.fp8_w8a16_gemm import fp8_weight_only_gemm
-from ayaka.kernel.hip.quant.fp8_quant import per_token_group_quant_fp8, per_token_quant_fp8, static_quant_fp8
+from ayaka.kernel.hip.quant.fp8_quant import (per_token_group_quant_fp8, per_token_group_quant_fp8_colmajor,
+                                              per_token_quant_fp8, static_quant_fp8)
 from ayaka.utils.math_utils import div_ceil
 
 __all__ = ["fp8_block_linear", "fp8_pertensor_linear", "fp8_rowwise_linear"]
 
 #: K (and N) extent of one block scale in the block-128 checkpoint contract.
 _SCALE_TILE = 128
+# Row counts up to this run the decode-batch GEMM kernels, which read row-major
+# activation scales in 16-byte chunks; larger ones the tiled kernels.
+_DECODE_BATCH_ROWS = 64
 
 
 @dataclass(frozen=True)
@@ -158,6 +162,13 @@ def fp8_block_linear(
         return act.shaped(act.weight_only(weight, weight_scale, _SCALE_TILE, _SCALE_TILE, scale_dtype), bias)
     if act.inner % _SCALE_TILE:
         raise ValueError(f"K={act.inner} must be divisible by 128 for the blockwise W8A8 path")
+    if act.rows > _DECODE_BATCH_ROWS:
+        # Prefill sizes: the quantizer writes the scales column-major, one cache line per
+        # 32 rows for the GEMM's per-block scale reads (same values, same result bits).
+        quantized, group_scale = per_token_group_quant_fp8_colmajor(act.matrix, _SCALE_TILE)
+        result = fp8_blockwise_mm(quantized, weight, group_scale, weight_scale, bias=bias, out=act.empty_output(),
+                                  a_scale_col_major=True)
+        return act.shaped(result)
     quantized, group_scale = per_token_group_quant_fp8(act.matrix, _SCALE_TILE)
     result = fp8_blockwise_mm(quantized, weight, group_scale, weight_scale, bias=bias, out=act.empty_output())
     return act.shaped(result)

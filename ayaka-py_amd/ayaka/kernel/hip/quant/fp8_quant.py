@@ -93,6 +93,37 @@ def per_token_group_quant_fp8(x: torch.Tensor, group_size: int = 128) -> tuple[t
     return y, scale
 
 
+def _per_token_group_quant_colmajor_fake(x: torch.Tensor, group_size: int = _GROUP) -> tuple[torch.Tensor, torch.Tensor]:
+    k = x.shape[-1]
+    rows = math.prod(x.shape[:-1]) if x.ndim > 1 else 1
+    return fake_tensor(x, shape=(rows, k), dtype=FP8), fake_tensor(x, shape=(k // group_size, rows), dtype=torch.float32)
+
+
+@custom_op(name="per_token_group_quant_fp8_colmajor", fake_impl=_per_token_group_quant_colmajor_fake)
+def per_token_group_quant_fp8_colmajor(x: torch.Tensor, group_size: int = 128) -> tuple[torch.Tensor, torch.Tensor]:
+    """``per_token_group_quant_fp8`` with the scales stored ``[K // group_size, M]``.
+
+    The same codes and scale values, bit for bit; only the scale table is transposed,
+    the layout ``fp8_blockwise_mm(..., a_scale_col_major=True)`` reads at one cache line
+    per 32 rows. Not part of the reference's operator set (its quantizer writes
+    ``[M, K // group_size]`` only); the block-128 linear uses it at prefill sizes.
+    """
+    _validate_input(x, "x")
+    _check_group_size(group_size, pow2=True)
+    k = int(x.shape[-1])
+    if k % group_size:
+        raise ValueError(f"K={k} must be divisible by group_size={group_size}")
+    x2d = _rows_2d(x)
+    rows = int(x2d.shape[0])
+    y = torch.empty((rows, k), dtype=FP8, device=x.device)
+    scale = torch.empty((k // group_size, rows), dtype=torch.float32, device=x.device)
+    if rows:
+        _lib.call("ayk_per_token_group_quant_fp8_strided", x2d.data_ptr(), _lib.dtype_code(x.dtype), rows, k,
+                  x2d.stride(0) if rows > 1 else k, group_size, y.data_ptr(), k, scale.data_ptr(), 1, rows,
+                  _lib.stream_of(x))
+    return y, scale
+
+
 # ---------------------------------------------------------------- MXFP8
 def _per_token_group_quant_mxfp8_fake(x: torch.Tensor, group_size: int = _MX_GROUP) -> tuple[torch.Tensor, torch.Tensor]:
     k = x.shape[-1]

@@ -415,7 +415,7 @@ constexpr int kGroupSlots = 2;
 template <typename T, int GL, int VPL, bool MX>
 __global__ __launch_bounds__(kQuantThreads) void group_quant_vec_kernel(
     const typename T::storage* __restrict__ x, int64_t rows, int64_t k, int64_t ldx,
-    int64_t group, uint8_t* __restrict__ q, int64_t ldq, void* __restrict__ scale_out) {
+    int64_t group, uint8_t* __restrict__ q, int64_t ldq, void* __restrict__ scale_out, int64_t srs, int64_t sgs) {
   constexpr int V = Vec16<T>::N;
   const int64_t gpr = k / group;
   const int64_t span = (int64_t)gridDim.x * kQuantThreads;
@@ -453,7 +453,7 @@ __global__ __launch_bounds__(kQuantThreads) void group_quant_vec_kernel(
     uint8_t* qg = q + row[u] * ldq + g[u] * group;
     if constexpr (MX) {
       const MxScale ms = mx_scale(amax);
-      if (lig == 0) reinterpret_cast<uint8_t*>(scale_out)[row[u] * gpr + g[u]] = ms.code;
+      if (lig == 0) reinterpret_cast<uint8_t*>(scale_out)[row[u] * srs + g[u] * sgs] = ms.code;
       if (finite && !ms.zero) {  // an all-zero group is written as +0 codes below
 #pragma unroll
         for (int j = 0; j < VPL; ++j) {
@@ -482,7 +482,7 @@ __global__ __launch_bounds__(kQuantThreads) void group_quant_vec_kernel(
       }
     } else {
       const float sc = floor_amax(amax) / kE4M3Max;
-      if (lig == 0) reinterpret_cast<float*>(scale_out)[row[u] * gpr + g[u]] = sc;
+      if (lig == 0) reinterpret_cast<float*>(scale_out)[row[u] * srs + g[u] * sgs] = sc;
       if (finite) {
         const float r = 1.0f / sc;
 #pragma unroll
@@ -506,7 +506,7 @@ __global__ __launch_bounds__(kQuantThreads) void group_quant_vec_kernel(
 template <typename T, bool MX>
 __global__ __launch_bounds__(kQuantThreads) void group_quant_scalar_kernel(
     const typename T::storage* __restrict__ x, int64_t rows, int64_t k, int64_t ldx,
-    int64_t group, uint8_t* __restrict__ q, int64_t ldq, void* __restrict__ scale_out) {
+    int64_t group, uint8_t* __restrict__ q, int64_t ldq, void* __restrict__ scale_out, int64_t srs, int64_t sgs) {
   const int64_t gpr = k / group;
   const int64_t gi = (int64_t)blockIdx.x * kQuantThreads + threadIdx.x;
   if (gi >= rows * gpr) return;
@@ -517,13 +517,13 @@ __global__ __launch_bounds__(kQuantThreads) void group_quant_scalar_kernel(
   for (int64_t i = 0; i < group; ++i) amax = nanmax(amax, fabsf(to_f32<T>(xg[i])));
   if constexpr (MX) {
     const MxScale ms = mx_scale(amax);
-    reinterpret_cast<uint8_t*>(scale_out)[gi] = ms.code;
+    reinterpret_cast<uint8_t*>(scale_out)[row * srs + g * sgs] = ms.code;
     for (int64_t i = 0; i < group; ++i) {
       qg[i] = ms.zero ? (uint8_t)0 : e4m3_encode(clamp_e4m3(to_f32<T>(xg[i]) * ms.inv));
     }
   } else {
     const float s = floor_amax(amax) / kE4M3Max;
-    reinterpret_cast<float*>(scale_out)[gi] = s;
+    reinterpret_cast<float*>(scale_out)[row * srs + g * sgs] = s;
     for (int64_t i = 0; i < group; ++i) qg[i] = e4m3_encode(clamp_e4m3(to_f32<T>(xg[i]) / s));
   }
 }
@@ -607,8 +607,9 @@ int launch_per_token(const void* x, int64_t rows, int64_t k, int64_t ldx, void* 
 }
 
 template <typename T, bool MX>
+// Scale of (row, group g) at scale[row * srs + g * sgs].
 int launch_group(const void* x, int64_t rows, int64_t k, int64_t ldx, int64_t group, void* q,
-                 int64_t ldq, void* scale, hipStream_t st) {
+                 int64_t ldq, void* scale, int64_t srs, int64_t sgs, hipStream_t st) {
   using S = typename T::storage;
   constexpr int V = Vec16<T>::N;
   const S* xs = static_cast<const S*>(x);
@@ -621,7 +622,7 @@ int launch_group(const void* x, int64_t rows, int64_t k, int64_t ldx, int64_t gr
   if (!vec_ok) {
     const dim3 grid((unsigned)cdiv(groups, kQuantThreads));
     hipLaunchKernelGGL((group_quant_scalar_kernel<T, MX>), grid, dim3(kQuantThreads), 0, st, xs,
-                       rows, k, ldx, group, qb, ldq, scale);
+                       rows, k, ldx, group, qb, ldq, scale, srs, sgs);
     return check_launch(MX ? "per_token_group_quant_mxfp8" : "per_token_group_quant_fp8");
   }
   const int gl = (int)(vecs < 64 ? vecs : 64);
@@ -629,7 +630,7 @@ int launch_group(const void* x, int64_t rows, int64_t k, int64_t ldx, int64_t gr
   const dim3 grid((unsigned)cdiv(groups * gl, (int64_t)kQuantThreads * kGroupSlots)), block(kQuantThreads);
 #define AYK_GQ(GL, VPL)                                                                          \
   hipLaunchKernelGGL((group_quant_vec_kernel<T, GL, VPL, MX>), grid, block, 0, st, xs, rows, k, \
-                     ldx, group, qb, ldq, scale)
+                     ldx, group, qb, ldq, scale, srs, sgs)
   switch (gl) {
     case 1: AYK_GQ(1, 1); break;
     case 2: AYK_GQ(2, 1); break;
@@ -718,14 +719,30 @@ static int group_args(const char* op, int x_dtype, int64_t rows, int64_t k, int6
 int ayk_per_token_group_quant_fp8(const void* x, int x_dtype, int64_t rows, int64_t k,
                                   int64_t ldx, int64_t group, void* q, int64_t ldq,
                                   float* scale, ayk_stream_t stream) {
+  return ayk_per_token_group_quant_fp8_strided(x, x_dtype, rows, k, ldx, group, q, ldq, scale, group > 0 ? k / group : 0, 1,
+                                               stream);
+}
+
+int ayk_per_token_group_quant_fp8_strided(const void* x, int x_dtype, int64_t rows, int64_t k,
+                                          int64_t ldx, int64_t group, void* q, int64_t ldq,
+                                          float* scale, int64_t scale_row_stride, int64_t scale_group_stride,
+                                          ayk_stream_t stream) {
   if (int rc = group_args("per_token_group_quant_fp8", x_dtype, rows, k, ldx, group, ldq, true)) return rc;
+  const int64_t gpr = k / group;
+  const bool rowmajor = scale_group_stride == 1 && scale_row_stride >= gpr;
+  const bool colmajor = scale_row_stride == 1 && scale_group_stride >= rows;
+  if (!rowmajor && !colmajor) {
+    return fail(AYK_EINVAL, "per_token_group_quant_fp8: scale strides (%lld, %lld) must lay out [rows, k/group] or [k/group, rows]",
+                (long long)scale_row_stride, (long long)scale_group_stride);
+  }
   if (rows == 0) return AYK_OK;
   if (int rc = check_device()) return rc;
   hipStream_t st = static_cast<hipStream_t>(stream);
+  const int64_t srs = scale_row_stride, sgs = scale_group_stride;
   switch (x_dtype) {
-    case AYK_BF16: return launch_group<BF16T, false>(x, rows, k, ldx, group, q, ldq, scale, st);
-    case AYK_F16: return launch_group<F16T, false>(x, rows, k, ldx, group, q, ldq, scale, st);
-    default: return launch_group<F32T, false>(x, rows, k, ldx, group, q, ldq, scale, st);
+    case AYK_BF16: return launch_group<BF16T, false>(x, rows, k, ldx, group, q, ldq, scale, srs, sgs, st);
+    case AYK_F16: return launch_group<F16T, false>(x, rows, k, ldx, group, q, ldq, scale, srs, sgs, st);
+    default: return launch_group<F32T, false>(x, rows, k, ldx, group, q, ldq, scale, srs, sgs, st);
   }
 }
 
@@ -737,9 +754,9 @@ int ayk_per_token_group_quant_mxfp8(const void* x, int x_dtype, int64_t rows, in
   if (int rc = check_device()) return rc;
   hipStream_t st = static_cast<hipStream_t>(stream);
   switch (x_dtype) {
-    case AYK_BF16: return launch_group<BF16T, true>(x, rows, k, ldx, group, q, ldq, code, st);
-    case AYK_F16: return launch_group<F16T, true>(x, rows, k, ldx, group, q, ldq, code, st);
-    default: return launch_group<F32T, true>(x, rows, k, ldx, group, q, ldq, code, st);
+    case AYK_BF16: return launch_group<BF16T, true>(x, rows, k, ldx, group, q, ldq, code, k / group, 1, st);
+    case AYK_F16: return launch_group<F16T, true>(x, rows, k, ldx, group, q, ldq, code, k / group, 1, st);
+    default: return launch_group<F32T, true>(x, rows, k, ldx, group, q, ldq, code, k / group, 1, st);
   }
 }
 

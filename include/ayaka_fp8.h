@@ -80,6 +80,17 @@ int ayk_per_token_group_quant_fp8(const void* x, int x_dtype, int64_t rows, int6
                                   int64_t ldx, int64_t group, void* q, int64_t ldq,
                                   float* scale, ayk_stream_t stream);
 
+/* per_token_group_quant_fp8 with the scale table's layout given by strides: the scale of
+ * (row m, group g) is stored at scale[m * scale_row_stride + g * scale_group_stride],
+ * which must describe [rows, k/group] (group stride 1) or [k/group, rows] (row stride 1).
+ * No counterpart in the reference, whose quantizer writes row-major scales only: the
+ * column-major table is the layout the block-128 GEMM reads fastest at prefill sizes
+ * (fp8_blockwise_mm's sa_col_major), written directly instead of transposed afterwards. */
+int ayk_per_token_group_quant_fp8_strided(const void* x, int x_dtype, int64_t rows, int64_t k,
+                                          int64_t ldx, int64_t group, void* q, int64_t ldq,
+                                          float* scale, int64_t scale_row_stride, int64_t scale_group_stride,
+                                          ayk_stream_t stream);
+
 /* Replaces ayaka::per_token_group_quant_mxfp8 (fp8_quant.py:374; oracle quant.py:40-56).
  * code[m, g] = 0 for an all-zero group, else clamp(ceil(log2(amax/448)), -126, 127) + 127.
  * group: positive, divides k. */

@@ -827,6 +827,24 @@ def test_weight_only_gemm_rows_plans(gpu, m, n, k, case, xdt, plan):
     assert_linear_close(y, ref, "weight_only_gemm rows")
 
 
+@pytest.mark.parametrize("m,n,k", [(300, 512, 1024), (4096, 768, 2048), (65, 384, 1024)])
+def test_block_linear_column_major_scales_match_row_major(gpu, m, n, k):
+    """Above 64 rows the block-128 linear quantizes with column-major scales; its output
+    equals the row-major composition bit for bit (the same scale values, read in another
+    layout, in the same K order)."""
+    from ayaka.kernel.hip import fp8_block_linear, fp8_blockwise_mm, per_token_group_quant_fp8
+
+    _say(f"fp8_block_linear column-major scales m={m} n={n} k={k}")
+    x = torch.randn(m, k, generator=_gen(4)).to(torch.bfloat16).to(gpu)
+    w = _fp8((n, k), seed=5).to(gpu)
+    ws = (torch.rand(n // 128, k // 128, generator=_gen(6)) * 1e-3 + 1e-4).to(gpu)
+    bias = torch.randn(n, generator=_gen(7)).to(torch.bfloat16).to(gpu)
+    y = fp8_block_linear(x, w, ws, bias)
+    q, s = per_token_group_quant_fp8(x, 128)
+    ref = fp8_blockwise_mm(q, w, s, ws, bias=bias, out=torch.empty(m, n, dtype=torch.bfloat16, device=gpu))
+    assert torch.equal(y.view(torch.int16), ref.view(torch.int16))
+
+
 # ------------------------------------------------------------------ linear entry points
 @pytest.mark.parametrize("m", [1, 8, 40])
 @pytest.mark.parametrize("recipe", ["w8a8_rowwise", "w8a8_dynamic_per_tensor", "w8a8_block128"])

@@ -88,6 +88,22 @@ def test_group_quant_bit_exact(gpu, dtype, m, k, group):
 
 
 @pytest.mark.parametrize("dtype", DTYPES)
+@pytest.mark.parametrize("m,k,group", [(300, 7168, 128), (65, 18432, 128), (3, 64, 16), (5, 12, 4), (1, 256, 128)])
+def test_group_quant_column_major_scales(gpu, dtype, m, k, group):
+    """The column-major variant writes the same codes and the same scales, transposed
+    (vector kernel, and the scalar kernel for groups of fewer than 8 elements)."""
+    from ayaka.kernel.hip.quant.fp8_quant import per_token_group_quant_fp8_colmajor
+
+    _say(f"per_token_group_quant_fp8_colmajor dtype={dtype} m={m} k={k} group={group}")
+    x = _activation(m, k, dtype, seed=3 * k + group)
+    q, s_t = per_token_group_quant_fp8_colmajor(x.to(gpu), group)
+    rq, rs = ora.per_token_group_quant(x, group)
+    assert s_t.shape == (k // group, m) and s_t.is_contiguous()
+    assert _bits_equal(s_t.t(), rs), "scales differ"
+    assert _bits_equal(q, rq), "codes differ"
+
+
+@pytest.mark.parametrize("dtype", DTYPES)
 @pytest.mark.parametrize("m,k,group", [(1, 32, 32), (64, 8192, 32), (3, 28672, 32), (2, 96, 96), (2, 64, 64), (5, 40, 8)])
 def test_mx_quant_bit_exact(gpu, dtype, m, k, group):
     from ayaka.kernel.hip import per_token_group_quant_mxfp8

@@ -316,6 +316,12 @@ def test_c_abi_rejects_bad_arguments_without_a_gpu():
     assert b"bad shape" in lib.ayk_last_error()
     assert lib.ayk_per_token_group_quant_fp8(None, _lib.AYK_BF16, 4, 128, 128, 96, None, 128, None, None) == _lib.AYK_EINVAL
     assert b"power of two" in lib.ayk_last_error()
+    # scale strides that describe neither [rows, k/group] nor [k/group, rows]
+    assert lib.ayk_per_token_group_quant_fp8_strided(None, _lib.AYK_BF16, 4, 256, 256, 128, None, 256, None, 1, 1,
+                                                     None) == _lib.AYK_EINVAL
+    assert b"scale strides" in lib.ayk_last_error()
+    assert lib.ayk_per_token_group_quant_fp8_strided(None, _lib.AYK_BF16, 4, 256, 256, 128, None, 256, None, 2, 3,
+                                                     None) == _lib.AYK_EINVAL
     assert lib.ayk_fp8_scaled_mm(None, 40, None, 40, 4, 4, 40, None, 0, 0, None, 0, 0, None, 0, None, 2, 4, None, 0, None) == _lib.AYK_EINVAL
     assert b"multiple of 16" in lib.ayk_last_error()
     assert lib.ayk_mxfp8_scaled_mm(None, 48, None, 1, None, 48, None, 1, 2, 2, 48, None, 0, None, 2, 2, None, 0, None) == _lib.AYK_EINVAL
