@@ -64,7 +64,7 @@ SIGNATURES: dict[str, list[Any]] = {
     "ayk_fp8_scaled_mm_workspace_bytes": [_l, _l, _l],
     "ayk_fp8_blockwise_mm": [_p, _l, _p, _l, _l, _l, _l, _p, _i, _i, _p, _i, _p, _i, _p, _i, _l, _p, _z, _p],
     "ayk_fp8_blockwise_mm_workspace_bytes": [_l, _l, _l],
-    "ayk_fp8_grouped_blockwise_mm": [_p, _p, _p, _p, _p, _p, _l, _l, _l, _l, _p, _i, _p],
+    "ayk_fp8_grouped_blockwise_mm": [_p, _p, _p, _p, _p, _p, _p, _l, _l, _l, _l, _p, _i, _p],
     "ayk_int8_scaled_mm": [_p, _l, _p, _l, _l, _l, _l, _p, _p, _p, _i, _p, _i, _l, _p, _z, _p],
     "ayk_int8_scaled_mm_workspace_bytes": [_l, _l, _l],
     "ayk_kv_cache_write": [_p, _p, _i, _l, _l, _l, _p, _p, _i, _l, _p, _f, _f, _p],

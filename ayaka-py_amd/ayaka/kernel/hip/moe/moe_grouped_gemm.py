@@ -31,6 +31,8 @@ from ayaka.kernel.hip import _lib
 __all__ = ["fp8_blockwise_scaled_grouped_mm", "get_group_gemm_starts"]
 
 SCALE_BLOCK = 128
+# Row count from which the activation scales are handed to the kernel column-major.
+COLUMN_MAJOR_SCALES_MIN_ROWS = 4096
 _OUT_DTYPES = (torch.bfloat16, torch.float16)
 
 
@@ -179,6 +181,9 @@ def fp8_blockwise_scaled_grouped_mm(
             get_group_gemm_starts(expert_offsets, a_ptrs, b_ptrs, out_ptrs, a_scales_ptrs, b_scales_ptrs, a, b,
                                   output, scales_a, scales_b, layout_sfa, layout_sfb, problem_sizes, problem_sizes,
                                   False)
-        _lib.call("ayk_fp8_grouped_blockwise_mm", a.data_ptr(), b.data_ptr(), scales_a.data_ptr(),
+        # Large batches: experts over the whole K read the activation scales transposed
+        # ([K/128, M_total], 32 rows per cache line), copied once here; the same values.
+        sa_t = scales_a.t().contiguous() if m_total >= COLUMN_MAJOR_SCALES_MIN_ROWS else None
+        _lib.call("ayk_fp8_grouped_blockwise_mm", a.data_ptr(), b.data_ptr(), scales_a.data_ptr(), _lib.ptr(sa_t),
                   scales_b.data_ptr(), problem_sizes.data_ptr(), expert_offsets.data_ptr(), num_experts, m_total, n,
                   k, output.data_ptr(), _lib.dtype_code(output.dtype), _lib.stream_of(output))

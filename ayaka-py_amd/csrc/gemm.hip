@@ -2048,7 +2048,7 @@ Block256Args block256_args(const GemmArgs& g) {
   b.w = g.w; b.ldw = g.ldw;
   b.M = g.M; b.N = g.N; b.K = g.K;
   b.sa = static_cast<const float*>(g.sa);
-  b.ld_sa = g.ld_sa > 0 ? g.ld_sa : g.K / 128;
+  b.ld_sa = g.sa_vec ? g.M : (g.ld_sa > 0 ? g.ld_sa : g.K / 128);
   b.sa_col_major = g.sa_vec;
   b.sb = g.sb; b.sb_dtype = g.sb_dtype;
   b.ld_sb = g.ld_sb > 0 ? g.ld_sb : cdiv(g.K, 128);
@@ -2239,7 +2239,8 @@ int ayk_fp8_blockwise_mm(const void* a, int64_t lda, const void* b, int64_t ldb,
 // the weights. The 256 x 256 block-128 kernel's grouped form (gemm_block.hip) takes one
 // tile of one expert per workgroup; the launch is an upper bound on the tile count (no
 // host synchronisation).
-int ayk_fp8_grouped_blockwise_mm(const void* a, const void* b, const float* scales_a, const float* scales_b,
+int ayk_fp8_grouped_blockwise_mm(const void* a, const void* b, const float* scales_a, const float* scales_a_t,
+                                 const float* scales_b,
                                  const int32_t* problem_sizes, const int32_t* expert_offsets, int64_t num_experts,
                                  int64_t m_total, int64_t n, int64_t k, void* out, int out_dtype,
                                  ayk_stream_t stream) {
@@ -2254,7 +2255,7 @@ int ayk_fp8_grouped_blockwise_mm(const void* a, const void* b, const float* scal
   if (!a || !b || !scales_a || !scales_b || !problem_sizes || !expert_offsets || !out)
     return fail(AYK_EINVAL, "%s: missing operand", op);
   if (!aligned16(a) || !aligned16(b) || !aligned16(out) || (reinterpret_cast<uintptr_t>(scales_a) & 3) ||
-      (reinterpret_cast<uintptr_t>(scales_b) & 3))
+      (reinterpret_cast<uintptr_t>(scales_b) & 3) || (reinterpret_cast<uintptr_t>(scales_a_t) & 3))
     return fail(AYK_EINVAL, "%s: operands must be 16-byte aligned (scales 4-byte)", op);
   if (k > 0x7FFFFFFF || n * k > ((int64_t)1 << 31)) return fail(AYK_EINVAL, "%s: expert weight too large", op);
   if (int rc = check_device()) return rc;
@@ -2262,6 +2263,7 @@ int ayk_fp8_grouped_blockwise_mm(const void* a, const void* b, const float* scal
   gb.a = static_cast<const uint8_t*>(a);
   gb.b = static_cast<const uint8_t*>(b);
   gb.sa = scales_a;
+  gb.sa_t = scales_a_t;
   gb.sb = scales_b;
   gb.out = out;
   gb.out_dtype = out_dtype;

@@ -15,8 +15,8 @@ struct Block256Args {
   const uint8_t* w;  // [N, K] e4m3, row stride ldw
   int64_t ldw;
   int64_t M, N, K;
-  const float* sa;   // fp32 activation scales: [M, ld_sa] (sa_col_major = 0) or [KB, M]
-  int64_t ld_sa;     // row stride of sa in elements (row-major form)
+  const float* sa;   // fp32 activation scales: [M, ld_sa] (sa_col_major = 0) or [KB, ld_sa]
+  int64_t ld_sa;     // row stride of sa in elements (row-major), or K-block stride (column-major)
   int sa_col_major;
   const void* sb;    // weight scales [ceil(N / 128), ld_sb], fp32 / fp16 / bf16
   int sb_dtype;
@@ -38,7 +38,8 @@ struct Block256Args {
 struct Grouped256Args {
   const uint8_t* a;
   const uint8_t* b;
-  const float* sa;
+  const float* sa;    // [m_total, k / 128]
+  const float* sa_t;  // nullptr, or the same table transposed: [k / 128, m_total]
   const float* sb;
   void* out;
   int out_dtype;

@@ -226,7 +226,7 @@ __device__ __attribute__((always_inline)) inline void block256_tile(const Block2
   const int64_t nbs = cdiv(g.N, 128);
   const int64_t nb = (n_base + wn * 128) / 128 < nbs ? (n_base + wn * 128) / 128 : nbs - 1;
   const int sb_size = g.sb_dtype == AYK_F32 ? 4 : 2;
-  const int64_t sa_elems = g.sa_col_major ? cdiv(g.K, 128) * g.M : g.M * g.ld_sa;
+  const int64_t sa_elems = g.sa_col_major ? (cdiv(g.K, 128) - 1) * g.ld_sa + g.M : g.M * g.ld_sa;
   const __amdgpu_buffer_rsrc_t sa_rsrc = uniform_rsrc(g.sa, (int32_t)(sa_elems * 4 < 0x7FFFFFFF ? sa_elems * 4 : 0x7FFFFFFF));
   // sb through a descriptor on its 4-byte-aligned span: a 16-bit scale is read as the
   // aligned dword that holds it, which never leaves that span.
@@ -243,7 +243,7 @@ __device__ __attribute__((always_inline)) inline void block256_tile(const Block2
     const int64_t mi = m < g.M ? m : g.M - 1;
     sa_off[j] = (uint32_t)((g.sa_col_major ? mi : mi * g.ld_sa) * 4);
   }
-  const uint32_t sa_kstride = (uint32_t)((g.sa_col_major ? g.M : 1) * 4);
+  const uint32_t sa_kstride = (uint32_t)((g.sa_col_major ? g.ld_sa : 1) * 4);
   struct Scales {
     uint32_t sa[FM];
     uint32_t sb;   // the dword holding sb[nb, kb]
@@ -513,10 +513,18 @@ __global__ __launch_bounds__(kThreads, 1) void fp8_grouped_block256_kernel(Group
   g.N = p.n;
   g.K = p.k;
   // The reference's pointer tables: expert e's scales start at row off_e of sa and at
-  // block row e (n / 128) of sb, both with row stride K_e / 128.
-  g.sa = ga.sa + p.off * kb_total;
-  g.ld_sa = p.k / kPairK;
-  g.sa_col_major = 0;
+  // block row e (n / 128) of sb, both with row stride K_e / 128. An expert over the
+  // whole K reads the transposed copy instead when there is one (the same values: row
+  // off_e + r, block kb), from column off_e with K-block stride m_total.
+  if (ga.sa_t != nullptr && p.k == ga.k) {
+    g.sa = ga.sa_t + p.off;
+    g.ld_sa = ga.m_total;
+    g.sa_col_major = 1;
+  } else {
+    g.sa = ga.sa + p.off * kb_total;
+    g.ld_sa = p.k / kPairK;
+    g.sa_col_major = 0;
+  }
   g.sb = ga.sb + (int64_t)e * (ga.n / kPairK) * kb_total;
   g.sb_dtype = AYK_F32;
   g.ld_sb = p.k / kPairK;

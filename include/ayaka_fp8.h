@@ -162,11 +162,14 @@ size_t ayk_fp8_blockwise_mm_workspace_bytes(int64_t M, int64_t N, int64_t K);
  * [expert_offsets[e], + problem_sizes[e][0]) of out:
  *   out[m, n] = sum_kb scales_a[m, kb] * scales_b[e][n / 128][kb] * (a[m, kb] . b[e][n, kb])
  * with a [m_total, k] e4m3, b memory [E][n][k] e4m3, scales_a [m_total, k/128] fp32,
+ * scales_a_t nullptr or the same table transposed, [k/128, m_total] (no counterpart in
+ * the reference: experts over the whole k read it, at one cache line per 32 rows),
  * scales_b [E][n/128][k/128] fp32, out [m_total, n] bf16/fp16 (row stride n); rows of no
  * expert are not written. problem_sizes [E, 3] int32 (M_e, N_e, K_e) and expert_offsets
  * [E] int32 are read on the device (clamped to the operands). n % 128 == 0,
  * k % 128 == 0, 16-byte aligned a/b/out. */
-int ayk_fp8_grouped_blockwise_mm(const void* a, const void* b, const float* scales_a, const float* scales_b,
+int ayk_fp8_grouped_blockwise_mm(const void* a, const void* b, const float* scales_a, const float* scales_a_t,
+                                 const float* scales_b,
                                  const int32_t* problem_sizes, const int32_t* expert_offsets, int64_t num_experts,
                                  int64_t m_total, int64_t n, int64_t k, void* out, int out_dtype,
                                  ayk_stream_t stream);

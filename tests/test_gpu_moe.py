@@ -172,3 +172,24 @@ def test_grouped_mm_contract(gpu):
         call(b=base["b"][:, :, :128].contiguous())
     with pytest.raises(ValueError, match="CUDA"):
         call(a=base["a"].cpu())
+
+
+@pytest.mark.parametrize("partial", [False, True])
+def test_grouped_mm_transposed_scales_match(gpu, monkeypatch, partial):
+    """From COLUMN_MAJOR_SCALES_MIN_ROWS rows the wrapper hands the kernel a transposed
+    copy of scales_a as well: experts over the whole K read it, others (K_e < K, whose
+    rows the reference addresses with row stride K_e / 128) keep the original table.
+    The output is bit-identical to the row-major-only launch."""
+    import ayaka.kernel.hip.moe.moe_grouped_gemm as G
+
+    counts, n, k = [130, 0, 77, 256, 5], 512, 1024
+    _say(f"grouped mm transposed scales partial={partial}")
+    a, b, sa, sb, ps, off = _problem(counts, n, k, seed=31)
+    if partial:
+        ps[2, 2] = 640  # expert 2 over K_e = 640 < K
+    outs = []
+    for rows in (1 << 40, 1):
+        monkeypatch.setattr(G, "COLUMN_MAJOR_SCALES_MIN_ROWS", rows)
+        out, _ = _run(gpu, a, b, sa, sb, ps, off, torch.bfloat16)
+        outs.append(out.cpu())
+    assert torch.equal(outs[0].view(torch.int16), outs[1].view(torch.int16))
