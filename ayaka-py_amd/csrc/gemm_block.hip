@@ -209,7 +209,13 @@ __device__ __attribute__((always_inline)) inline void block256_tile(const Block2
   const __amdgpu_buffer_rsrc_t rsrc = uniform_rsrc((side == 0 ? g.w : g.a) + win.base_offset + k0, win.records);
   const int voff_e = (lane >> 3) * ld_u + (((lane & 7) ^ ((lane >> 4) & 7)) << 4);
   const int voff_o = (lane >> 3) * ld_u + (((lane & 7) ^ ((4 + (lane >> 4)) & 7)) << 4);
+  // A wavefront whose 64 rows all lie past M (activations) or N (weights) loads nothing:
+  // its LDS rows feed only MFMAs whose results are never stored (a wavefront with no
+  // live activation row skips its MFMAs; a weight row past N makes an output column
+  // past N). MoE tiles with at most 128 expert rows thus issue a quarter fewer loads.
+  const bool loads_live = (side == 0 ? n_base : m_base) + 64 * (wave_u & 3) < (side == 0 ? g.N : g.M);
   auto issue = [&](int p, uint8_t* dst) {
+    if (!loads_live) return;
     const int kb = block_of(p);
 #pragma unroll
     for (int jj = 0; jj < kDma; ++jj) {
