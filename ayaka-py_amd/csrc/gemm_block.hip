@@ -391,8 +391,6 @@ __device__ __attribute__((always_inline)) inline void block256_tile(const Block2
         __builtin_amdgcn_sched_group_barrier(kSchedValu, 16, 0);
         __builtin_amdgcn_sched_group_barrier(kSchedDsRead, 1, 0);
       }
-    } else {
-      read_frags(0, nxt, 0);
     }
   };
   for (int p = 0; p < npairs; p += 2) {
