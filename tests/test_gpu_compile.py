@@ -35,7 +35,7 @@ def _layer(recipe, gpu, g):
     return method, layer
 
 
-@pytest.mark.parametrize("m", [1, 7, 64])
+@pytest.mark.parametrize("m", [1, 7, 64, 100])  # 100: the tiled GEMMs (block-128: column-major scales)
 @pytest.mark.parametrize("recipe", list(CONFIGS))
 def test_compiled_apply_matches_eager(gpu, recipe, m):
     print(f"torch.compile fullgraph recipe={recipe} m={m}", flush=True)
