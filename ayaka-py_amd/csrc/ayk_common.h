@@ -182,6 +182,29 @@ __device__ inline void store_f32(void* p, int dtype, int64_t i, float v) {
   }
 }
 
+// Fixed-order sum of `split` fp32 partial planes ([split][M][N], 16-byte aligned,
+// N % 4 == 0) at elements i .. i + 3 of one row, plus bias, rounded once into out:
+// bit for bit the sum v = 0, v += plane 0, v += plane 1, ..., with the planes' loads
+// issued four at a time (a load-add chain per plane serialises their latencies).
+__device__ inline void split_sum_store4(const float* __restrict__ part, int64_t M, int64_t N, int split, int64_t i,
+                                        const void* __restrict__ bias, int bias_dtype, void* __restrict__ out,
+                                        int out_dtype, int64_t ldo) {
+  const float4* p = reinterpret_cast<const float4*>(part + i);
+  const int64_t st = M * N / 4;
+  float4 v = make_float4(0.0f, 0.0f, 0.0f, 0.0f);
+  auto add = [&](const float4& a) { v.x += a.x; v.y += a.y; v.z += a.z; v.w += a.w; };
+  int s = 0;
+  for (; s + 4 <= split; s += 4) {
+    const float4 a = p[s * st], b = p[(s + 1) * st], c = p[(s + 2) * st], d = p[(s + 3) * st];
+    add(a); add(b); add(c); add(d);
+  }
+  for (; s < split; ++s) add(p[s * st]);
+  const int64_t m = i / N, n = i - m * N;
+  const float o[4] = {v.x, v.y, v.z, v.w};
+#pragma unroll
+  for (int q = 0; q < 4; ++q) store_f32(out, out_dtype, m * ldo + n + q, bias ? o[q] + load_f32(bias, bias_dtype, n + q) : o[q]);
+}
+
 // Four e4m3 bytes packed in one dword -> four floats (hardware OCP converter).
 __device__ inline void e4m3x4_to_f32(uint32_t w, float* out) {
   typedef float v2f __attribute__((ext_vector_type(2)));
@@ -301,6 +324,31 @@ __device__ inline float wave_sum_dpp(float v) {
 __host__ __device__ constexpr int64_t cdiv(int64_t a, int64_t b) { return (a + b - 1) / b; }
 
 inline bool aligned16(const void* p) { return (reinterpret_cast<uintptr_t>(p) & 15u) == 0; }
+
+// The K-split reduce four elements per thread (split_sum_store4).
+namespace {
+__global__ __launch_bounds__(256) void split_reduce4_kernel(const float* __restrict__ part, int64_t M, int64_t N, int split,
+                                                           const void* __restrict__ bias, int bias_dtype,
+                                                           void* __restrict__ out, int out_dtype, int64_t ldo) {
+  const int64_t i = ((int64_t)blockIdx.x * 256 + threadIdx.x) * 4;
+  if (i >= M * N) return;
+  split_sum_store4(part, M, N, split, i, bias, bias_dtype, out, out_dtype, ldo);
+}
+}  // namespace
+// Launch the fixed-order reduce of [split][M][N] fp32 partials: four elements per
+// thread when N % 4 == 0 and the partials are 16-byte aligned, else `scalar` (one
+// element per thread, the same sum).
+template <typename ScalarKernel>
+inline void launch_split_reduce(ScalarKernel scalar, const float* part, int64_t M, int64_t N, int split, const void* bias,
+                                int bias_dtype, void* out, int out_dtype, int64_t ldo, hipStream_t st) {
+  if (N % 4 == 0 && aligned16(part)) {
+    hipLaunchKernelGGL(split_reduce4_kernel, dim3((unsigned)((M * N / 4 + 255) / 256)), dim3(256), 0, st, part, M, N, split,
+                       bias, bias_dtype, out, out_dtype, ldo);
+  } else {
+    hipLaunchKernelGGL(scalar, dim3((unsigned)((M * N + 255) / 256)), dim3(256), 0, st, part, M, N, split, bias, bias_dtype,
+                       out, out_dtype, ldo);
+  }
+}
 
 // Error state of the C ABI (defined in capi.hip).
 int fail(int status, const char* fmt, ...);

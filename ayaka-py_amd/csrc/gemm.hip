@@ -1608,10 +1608,15 @@ __global__ __launch_bounds__(256) void tail_split_reduce(const float* __restrict
   const int64_t m = (int64_t)tm * kBigTile + r, n = (int64_t)tn * kBigTile + c;
   if (m >= M || n >= N) return;
   float4 v = *reinterpret_cast<const float4*>(part + i);
-  for (int y = 1; y < split; ++y) {
-    const float4 p = *reinterpret_cast<const float4*>(part + ((int64_t)y * tail_tiles + t) * kTileElems + within);
-    v.x += p.x; v.y += p.y; v.z += p.z; v.w += p.w;
+  // Pieces 1 .. split - 1 in order, their loads issued four at a time.
+  auto piece = [&](int y) { return *reinterpret_cast<const float4*>(part + ((int64_t)y * tail_tiles + t) * kTileElems + within); };
+  auto add = [&](const float4& p) { v.x += p.x; v.y += p.y; v.z += p.z; v.w += p.w; };
+  int y = 1;
+  for (; y + 4 <= split; y += 4) {
+    const float4 a = piece(y), b = piece(y + 1), c4 = piece(y + 2), d = piece(y + 3);
+    add(a); add(b); add(c4); add(d);
   }
+  for (; y < split; ++y) add(piece(y));
   float o[4] = {v.x, v.y, v.z, v.w};
 #pragma unroll
   for (int q = 0; q < 4; ++q) {
@@ -1958,8 +1963,8 @@ int launch_big(GemmArgs g, hipStream_t st, const char* op) {
       g.items = (int)tiles;  // one item per workgroup: grid (tiles, split)
       hipLaunchKernelGGL((fp8_gemm_pair_kernel<MODE>), dim3((unsigned)tiles, (unsigned)split), dim3(kThreads), 0, st, g);
       if (int rc = check_launch(op)) return rc;
-      hipLaunchKernelGGL(block_split_reduce, dim3((unsigned)cdiv(g.M * g.N, 256)), dim3(256), 0, st, g.ws, g.M, g.N,
-                         (int)split, g.bias, g.bias_dtype, g.out, g.out_dtype, g.ldo);
+      launch_split_reduce(block_split_reduce, g.ws, g.M, g.N, (int)split, g.bias, g.bias_dtype, g.out, g.out_dtype,
+                          g.ldo, st);
     } else {
       note_plan("mx128");
       hipLaunchKernelGGL((fp8_gemm_mx128_kernel<MODE>), dim3((unsigned)tiles), dim3(kThreads), 0, st, g);
@@ -1981,8 +1986,8 @@ int launch_big(GemmArgs g, hipStream_t st, const char* op) {
                        dim3(kThreads), 0, st, g);
     if (split > 1) {
       if (int rc = check_launch(op)) return rc;
-      hipLaunchKernelGGL(block_split_reduce, dim3((unsigned)cdiv(g.M * g.N, 256)), dim3(256), 0, st, g.ws, g.M, g.N,
-                         (int)split, g.bias, g.bias_dtype, g.out, g.out_dtype, g.ldo);
+      launch_split_reduce(block_split_reduce, g.ws, g.M, g.N, (int)split, g.bias, g.bias_dtype, g.out, g.out_dtype,
+                          g.ldo, st);
     }
   } else {
     note_plan("big");
@@ -2007,8 +2012,8 @@ int launch_block_big(GemmArgs g, hipStream_t st, const char* op) {
   hipLaunchKernelGGL(fp8_gemm_block_split_kernel, dim3((unsigned)tiles, (unsigned)split), dim3(kBlkThreads), 0, st, g,
                      g.K / split, g.ws);
   if (int rc = check_launch(op)) return rc;
-  hipLaunchKernelGGL(block_split_reduce, dim3((unsigned)cdiv(g.M * g.N, 256)), dim3(256), 0, st, g.ws, g.M, g.N,
-                     (int)split, g.bias, g.bias_dtype, g.out, g.out_dtype, g.ldo);
+  launch_split_reduce(block_split_reduce, g.ws, g.M, g.N, (int)split, g.bias, g.bias_dtype, g.out, g.out_dtype,
+                          g.ldo, st);
   return check_launch(op);
 }
 
@@ -2030,8 +2035,8 @@ int launch_cfg(GemmArgs g, hipStream_t st, const char* op) {
   hipLaunchKernelGGL((fp8_gemm_kernel<MODE, BN, BM, WN, WM>), dim3((unsigned)tiles, (unsigned)split), dim3(kThreads), 0, st, g);
   if (int rc = check_launch(op)) return rc;
   if (split > 1) {
-    hipLaunchKernelGGL(block_split_reduce, dim3((unsigned)cdiv(g.M * g.N, 256)), dim3(256), 0, st, g.ws, g.M, g.N,
-                       (int)split, g.bias, g.bias_dtype, g.out, g.out_dtype, g.ldo);
+    launch_split_reduce(block_split_reduce, g.ws, g.M, g.N, (int)split, g.bias, g.bias_dtype, g.out, g.out_dtype,
+                          g.ldo, st);
     return check_launch(op);
   }
   return AYK_OK;

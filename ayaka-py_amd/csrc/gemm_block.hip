@@ -591,8 +591,7 @@ int block256_launch(const Block256Args& g, hipStream_t st, const char* op) {
   hipLaunchKernelGGL(fp8_block256_kernel, dim3((unsigned)tiles, (unsigned)split), dim3(kThreads), 0, st, g, tiles_m,
                      block256_kps(g.K, split));
   if (int rc = check_launch(op)) return rc;
-  hipLaunchKernelGGL(block256_reduce, dim3((unsigned)cdiv(g.M * g.N, 256)), dim3(256), 0, st, g.ws, g.M, g.N, (int)split,
-                     g.bias, g.bias_dtype, g.out, g.out_dtype, g.ldo);
+  launch_split_reduce(block256_reduce, g.ws, g.M, g.N, (int)split, g.bias, g.bias_dtype, g.out, g.out_dtype, g.ldo, st);
   return check_launch(op);
 }
 

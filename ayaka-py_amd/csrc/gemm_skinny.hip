@@ -653,8 +653,7 @@ int skinny_fp8_launch(const SkinnyFp8Args& g, hipStream_t st, const char* op) {
   if (!launched) return fail(AYK_EINVAL, "%s: no decode-batch kernel for this plan", op);
   if (int rc = check_launch(op)) return rc;
   if (p.split > 1) {
-    hipLaunchKernelGGL(skinny_reduce, dim3((unsigned)cdiv(g.M * g.N, 256)), dim3(256), 0, st, g.ws, g.M, g.N, p.split,
-                       g.bias, g.bias_dtype, g.out, g.out_dtype, g.ldo);
+    launch_split_reduce(skinny_reduce, g.ws, g.M, g.N, p.split, g.bias, g.bias_dtype, g.out, g.out_dtype, g.ldo, st);
     return check_launch(op);
   }
   return AYK_OK;
