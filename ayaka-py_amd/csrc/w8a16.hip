@@ -865,7 +865,8 @@ __global__ __launch_bounds__(256) void w8a16_rows_reduce(RsArgs a, int split) {
 // Launch plan from the shapes alone (the workspace query reproduces it). R = 16 rows
 // per workgroup when K is too short to split and those workgroups are one per CU (up
 // to 16 activation rows: two per CU); else R = 64 for M > 16 when that still gives
-// >= 384 workgroups (the activation stage is then shared by more rows), else 32. K is split across workgroups only while
+// >= 384 workgroups (the activation stage is then shared by more rows), else 32. K is
+// split across workgroups only while
 // each split keeps >= 4096 K and there are < 512 workgroups: a split costs a second
 // launch and fp32 partials, which measured slower than fewer workgroups at K = 4096
 // (Llama-3-8B qkv / o / gate_up) and faster at K = 14336 (down, split 2).
