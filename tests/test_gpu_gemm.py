@@ -98,7 +98,9 @@ MNK = [(8, 3072, 1024), (17, 300, 256), (64, 256, 384), (200, 1000, 1024), (256,
        # 256x256 kernel with 1, 5 and 19 K stages of 64: steps padded to a multiple of four
        (256, 256, 64), (400, 300, 320), (260, 1028, 1216),
        # its 128-byte-row variant (K % 128 == 0) with 1 and 3 pairs of stages: pairs padded to even
-       (256, 260, 128), (512, 512, 384)]  # from (300, 520, 1024) on: the 256x256 kernels
+       (256, 260, 128), (512, 512, 384),  # from (300, 520, 1024) on: the 256x256 kernels
+       # K splits whose N is not a multiple of 4: the one-element-per-thread reduce
+       (300, 1002, 8192), (40, 1002, 8192)]
 
 
 @pytest.mark.parametrize("m,n,k", MNK)
