@@ -178,7 +178,7 @@ def test_mxfp8_scaled_mm_split_k(gpu, m, n, k):
 # a different plan: rows per wavefront (32 or 64), activation tiles (M <= 32 or <= 64),
 # K parts per row group (1, 2, 4), activation chunk of 2 or 4 pairs, grid K split.
 SKINNY_MNK = [
-    (2, 3000, 2048),     # 32 rows, 4 K parts, ragged N
+    (5, 3000, 2048),     # 32 rows, 4 K parts, ragged N (2-4 rows take the GEMV-shaped kernel)
     (8, 24576, 2048),    # 32 rows, whole K, two workgroups per CU
     (16, 57344, 1024),   # 64 rows per wavefront, chunks of 4 pairs
     (8, 14336, 2048),    # 64 rows per wavefront, 4 K parts
@@ -845,6 +845,31 @@ def test_block_linear_column_major_scales_match_row_major(gpu, m, n, k):
     q, s = per_token_group_quant_fp8(x, 128)
     ref = fp8_blockwise_mm(q, w, s, ws, bias=bias, out=torch.empty(m, n, dtype=torch.bfloat16, device=gpu))
     assert torch.equal(y.view(torch.int16), ref.view(torch.int16))
+
+
+# 2-4 rows of the fp32-scaled GEMM against a small weight take the GEMV-shaped kernel
+# (VALU fmas of exact fp8 products); 5 rows and up keep the MFMA decode-batch kernel.
+@pytest.mark.parametrize("m,n,k,rowwise,out_dtype,with_bias,plan", [
+    (2, 4096, 4096, True, torch.bfloat16, True, "rows_gemv"),
+    (3, 1001, 2048, False, torch.float16, False, "rows_gemv"),
+    (4, 6144, 2048, True, torch.float32, True, "rows_gemv"),
+    (2, 300, 256, True, torch.bfloat16, True, "rows_gemv"),
+    (5, 3072, 1024, True, torch.bfloat16, True, "skinny"),
+])
+def test_fp8_scaled_mm_small_batch_plans(gpu, m, n, k, rowwise, out_dtype, with_bias, plan):
+    from ayaka.kernel.hip import fp8_scaled_mm
+
+    _say(f"fp8_scaled_mm small batch m={m} n={n} k={k} rowwise={rowwise} out={out_dtype}")
+    a = _fp8((m, k), seed=m + 7, scale=40)
+    w = _fp8((n, k), seed=n + 7, scale=40)
+    sa = (torch.rand(m, generator=_gen(1)) * 0.01 + 1e-3) if rowwise else torch.tensor(0.004)
+    sb = (torch.rand(n, generator=_gen(2)) * 0.01 + 1e-3) if rowwise else torch.tensor(0.002)
+    bias = torch.randn(n, generator=_gen(3)).to(torch.bfloat16) if with_bias else None
+    ref = ora.fp8_scaled_mm(a, w, sa, sb, bias)
+    out = torch.empty(m, n, dtype=out_dtype, device=gpu)
+    fp8_scaled_mm(a.to(gpu), w.to(gpu).t(), sa.to(gpu), sb.to(gpu), bias.to(gpu) if with_bias else None, out=out)
+    assert _plan().startswith(plan)
+    assert_linear_close(out, ref, "fp8_scaled_mm small batch")
 
 
 # ------------------------------------------------------------------ linear entry points
