@@ -612,7 +612,7 @@ int scale_chunk(const SkinnyFp8Args& g, const SkPlan& p) {
   return 4;
 }
 
-// Small decode batches of the fp32-scaled (rowwise / per-tensor) GEMM: 2 to 4 rows
+// Small decode batches of the fp32-scaled (rowwise / per-tensor) GEMM: 2 to 8 rows
 // against a weight of at most 2^24 bytes, where the MFMA decode-batch kernel's fixed
 // cost (its LDS ring, 32-row fragments and at least 32 weight rows per wavefront) is
 // most of its time. A GEMV-shaped kernel instead: the workgroup stages the activation
@@ -620,9 +620,8 @@ int scale_chunk(const SkinnyFp8Args& g, const SkPlan& p) {
 // 1024-byte sweeps (one 16-byte vector per lane and row), and each lane keeps 2 x MR
 // fp32 sums of exact fp8 products (VALU fmas), reduced across the wavefront at the
 // end. out = (sum * sa[m]) * sb[n] + bias[n], rounded once, as the MFMA kernels.
-// Measured against the MFMA kernel: 4096 x 4096 at M = 2 11.0 -> 6.8 us, 6144 x 2048
-// at M = 4 9.4 -> 8.7 us; at M = 8 (3072 x 1024) it was slower, 7.3 -> 10.8 us, so
-// the MFMA kernel keeps 5 rows and up.
+// Measured against the MFMA kernel: Cfg1's 3072 x 1024 at M = 8 7.2 -> 5.7 us,
+// 4096 x 2048 at M = 8 9.2 -> 7.9 us, 4096 x 4096 at M = 2 11.0 -> 5.9 us.
 constexpr int kRgThreads = 256;
 constexpr int kRgRows = 2 * (kRgThreads / kWave);  // weight rows per workgroup
 template <int MR>
@@ -671,24 +670,24 @@ __global__ __launch_bounds__(kRgThreads) void fp8_rows_gemv_kernel(SkinnyFp8Args
     for (int m = 0; m < MR; ++m)
 #pragma unroll
       for (int d = 32; d >= 1; d >>= 1) acc[r][m] += __shfl_xor(acc[r][m], d, kWave);
-  // Lane 2 m + r stores (row n0 + r, activation row m).
-  const float* sa = static_cast<const float*>(g.sa);
-  const float* sb = static_cast<const float*>(g.sb);
+  // Lane 2 m + r stores (row n0 + r, activation row m): every lane picks its total with
+  // selects, then one scale / bias load and one store per lane, all lanes at once.
+  const int r = lane & 1, m = lane >> 1;
+  float total = 0.0f;
 #pragma unroll
-  for (int r = 0; r < 2; ++r)
-#pragma unroll
-    for (int m = 0; m < MR; ++m) {
-      const int64_t n = n0 + r;
-      if (lane == 2 * m + r && m < M && n < g.N) {
-        float y = (acc[r][m] * sa[g.sa_vec ? m : 0]) * sb[g.sb_vec ? n : 0];
-        if (g.bias) y += load_f32(g.bias, g.bias_dtype, n);
-        store_f32(g.out, g.out_dtype, (int64_t)m * g.ldo + n, y);
-      }
-    }
+  for (int mm = 0; mm < MR; ++mm) total = m == mm ? (r ? acc[1][mm] : acc[0][mm]) : total;
+  const int64_t n = n0 + r;
+  if (m < M && n < g.N) {
+    const float* sa = static_cast<const float*>(g.sa);
+    const float* sb = static_cast<const float*>(g.sb);
+    float y = (total * sa[g.sa_vec ? m : 0]) * sb[g.sb_vec ? n : 0];
+    if (g.bias) y += load_f32(g.bias, g.bias_dtype, n);
+    store_f32(g.out, g.out_dtype, (int64_t)m * g.ldo + n, y);
+  }
 }
 
 bool rows_gemv_wanted(const SkinnyFp8Args& g) {
-  return g.mode == kSmScaled && g.M >= 2 && g.M <= 4 && g.N * g.K <= ((int64_t)1 << 24) && g.K % 16 == 0 &&
+  return g.mode == kSmScaled && g.M >= 2 && g.M <= 8 && g.N * g.K <= ((int64_t)1 << 24) && g.K % 16 == 0 &&
          g.M * g.K <= 64 * 1024 && g.lda % 16 == 0 && g.ldw % 16 == 0 && aligned16(g.a) && aligned16(g.w);
 }
 int launch_rows_gemv(const SkinnyFp8Args& g, hipStream_t st, const char* op) {
@@ -696,7 +695,8 @@ int launch_rows_gemv(const SkinnyFp8Args& g, hipStream_t st, const char* op) {
   const dim3 grid((unsigned)cdiv(g.N, kRgRows)), block(kRgThreads);
   const unsigned lds = (unsigned)(g.M * g.K);
   if (g.M <= 2) hipLaunchKernelGGL((fp8_rows_gemv_kernel<2>), grid, block, lds, st, g);
-  else hipLaunchKernelGGL((fp8_rows_gemv_kernel<4>), grid, block, lds, st, g);
+  else if (g.M <= 4) hipLaunchKernelGGL((fp8_rows_gemv_kernel<4>), grid, block, lds, st, g);
+  else hipLaunchKernelGGL((fp8_rows_gemv_kernel<8>), grid, block, lds, st, g);
   return check_launch(op);
 }
 

@@ -178,7 +178,7 @@ def test_mxfp8_scaled_mm_split_k(gpu, m, n, k):
 # a different plan: rows per wavefront (32 or 64), activation tiles (M <= 32 or <= 64),
 # K parts per row group (1, 2, 4), activation chunk of 2 or 4 pairs, grid K split.
 SKINNY_MNK = [
-    (5, 3000, 2048),     # 32 rows, 4 K parts, ragged N (2-4 rows take the GEMV-shaped kernel)
+    (9, 3000, 2048),     # 32 rows, 4 K parts, ragged N (2-8 rows take the GEMV-shaped kernel)
     (8, 24576, 2048),    # 32 rows, whole K, two workgroups per CU
     (16, 57344, 1024),   # 64 rows per wavefront, chunks of 4 pairs
     (8, 14336, 2048),    # 64 rows per wavefront, 4 K parts
@@ -546,7 +546,7 @@ DECODE_PLANS = [
     ("block", 16, 14000, 1024, "skinny fn=1 fm=1 ks=2 g=2 ch=4 split=1"),
     ("mx", 64, 14000, 1024, "skinny fn=1 fm=2 ks=2 g=2 ch=4 split=1"),
     ("mx", 20, 13000, 1024, "skinny fn=1 fm=1 ks=2 g=2 ch=4 split=1"),
-    ("scaled", 8, 14000, 1024, "skinny fn=2 fm=1 ks=4 g=2 ch=1 split=1"),
+    ("scaled", 9, 14000, 1024, "skinny fn=2 fm=1 ks=4 g=2 ch=1 split=1"),  # 2-8 rows: the GEMV-shaped kernel
     ("scaled", 24, 12800, 1024, "skinny fn=2 fm=1 ks=4 g=2 ch=1 split=1"),
 ]
 
@@ -847,14 +847,19 @@ def test_block_linear_column_major_scales_match_row_major(gpu, m, n, k):
     assert torch.equal(y.view(torch.int16), ref.view(torch.int16))
 
 
-# 2-4 rows of the fp32-scaled GEMM against a small weight take the GEMV-shaped kernel
-# (VALU fmas of exact fp8 products); 5 rows and up keep the MFMA decode-batch kernel.
+# 2-8 rows of the fp32-scaled GEMM against a weight of at most 2^24 bytes take the
+# GEMV-shaped kernel (VALU fmas of exact fp8 products); more rows or a larger weight keep
+# the MFMA decode-batch kernel.
 @pytest.mark.parametrize("m,n,k,rowwise,out_dtype,with_bias,plan", [
     (2, 4096, 4096, True, torch.bfloat16, True, "rows_gemv"),
     (3, 1001, 2048, False, torch.float16, False, "rows_gemv"),
     (4, 6144, 2048, True, torch.float32, True, "rows_gemv"),
     (2, 300, 256, True, torch.bfloat16, True, "rows_gemv"),
-    (5, 3072, 1024, True, torch.bfloat16, True, "skinny"),
+    (5, 3072, 1024, True, torch.bfloat16, True, "rows_gemv"),
+    (8, 4096, 2048, False, torch.bfloat16, True, "rows_gemv"),
+    (7, 2050, 1024, True, torch.float16, True, "rows_gemv"),
+    (8, 8192, 4096, True, torch.bfloat16, True, "skinny"),
+    (9, 3072, 1024, True, torch.bfloat16, True, "skinny"),
 ])
 def test_fp8_scaled_mm_small_batch_plans(gpu, m, n, k, rowwise, out_dtype, with_bias, plan):
     from ayaka.kernel.hip import fp8_scaled_mm
