@@ -57,6 +57,7 @@ SIGNATURES: dict[str, list[Any]] = {
     "ayk_device_supported": [_i],
     "ayk_per_token_quant_fp8": [_p, _i, _l, _l, _l, _p, _l, _p, _p],
     "ayk_per_token_group_quant_fp8": [_p, _i, _l, _l, _l, _l, _p, _l, _p, _p],
+    "ayk_fp8_rowwise_linear_small": [_p, _i, _l, _l, _p, _l, _l, _l, _p, _i, _p, _i, _p, _i, _l, _p],
     "ayk_per_token_group_quant_fp8_strided": [_p, _i, _l, _l, _l, _l, _p, _l, _p, _l, _l, _p],
     "ayk_per_token_group_quant_mxfp8": [_p, _i, _l, _l, _l, _l, _p, _l, _p, _p],
     "ayk_static_quant_fp8": [_p, _i, _l, _p, _i, _p, _p],

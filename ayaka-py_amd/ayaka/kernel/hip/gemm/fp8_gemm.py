@@ -26,7 +26,7 @@ from ayaka.kernel.hip._host import prepare_output, require_last_dim_stride1
 from ayaka.kernel.ops import custom_op
 from ayaka.utils.math_utils import div_ceil
 
-__all__ = ["fp8_blockwise_mm", "fp8_scaled_mm"]
+__all__ = ["fp8_blockwise_mm", "fp8_rowwise_linear_small", "fp8_scaled_mm"]
 
 _BACKENDS = ("triton", "auto", "cublaslt")
 
@@ -111,6 +111,66 @@ def fp8_scaled_mm(
         _lib.ptr(ws), nbytes, _lib.stream_of(a),
     )
     return result
+
+
+# ------------------------------------------------------------------ fused small batch
+_SMALL_ROWS = (2, 8)
+_SMALL_WEIGHT_BYTES = 1 << 24
+
+
+def rowwise_small_applies(x: torch.Tensor, weight: torch.Tensor, weight_scale: torch.Tensor) -> bool:
+    """Whether ``fp8_rowwise_linear_small`` takes this product: 2 to 8 rows, a weight of at
+    most 2^24 bytes with 16-byte rows, an fp32 scalar or ``[N]`` weight scale, and rows of
+    x that the kernel can stage in LDS (``M * K <= 64 KiB``) with 16-byte loads. Shapes,
+    dtypes and strides only (traceable); base addresses are checked by the op."""
+    rows, k = int(x.shape[0]), int(x.shape[1])
+    n = int(weight.shape[0])
+    return (_SMALL_ROWS[0] <= rows <= _SMALL_ROWS[1] and n * k <= _SMALL_WEIGHT_BYTES and k % 16 == 0
+            and rows * k <= 64 * 1024 and x.dtype in (torch.bfloat16, torch.float16, torch.float32)
+            and x.stride(1) == 1 and (x.stride(0) * x.element_size()) % 16 == 0
+            and weight.dtype == FP8 and weight.stride(1) == 1 and weight.stride(0) % 16 == 0
+            and weight_scale.dtype == torch.float32 and weight_scale.numel() in (1, n) and weight_scale.is_contiguous())
+
+
+def _fp8_rowwise_linear_small_fake(x, weight, weight_scale, bias=None):
+    return torch.empty((x.shape[0], weight.shape[0]), dtype=x.dtype, device=x.device)
+
+
+@custom_op(name="fp8_rowwise_linear_small", fake_impl=_fp8_rowwise_linear_small_fake)
+def fp8_rowwise_linear_small(
+    x: torch.Tensor,
+    weight: torch.Tensor,
+    weight_scale: torch.Tensor,
+    bias: torch.Tensor | None = None,
+) -> torch.Tensor:
+    """Per-token quantization of ``x`` and the rowwise product in one launch, for 2 to 8 rows.
+
+    The result equals ``fp8_scaled_mm(*per_token_quant_fp8(x), weight.t(), ...)`` (the
+    reference's ``fp8_rowwise_linear`` at ``fp8_linear.py:168``) bit for bit; the two
+    launches become one. Not part of the reference's operator set; ``fp8_rowwise_linear``
+    uses it where ``rowwise_small_applies`` holds.
+
+    Args:
+        x: ``[M, K]`` bf16 / fp16 / fp32; weight: ``[N, K]`` e4m3; weight_scale: fp32
+        scalar or ``[N]``; bias: optional ``[N]``. Returns ``[M, N]`` in ``x``'s dtype.
+    """
+    if not rowwise_small_applies(x, weight, weight_scale):
+        raise ValueError("fp8_rowwise_linear_small: shape, dtype or layout outside its contract")
+    validate_bias(bias, x, int(weight.shape[0]))
+    rows, k, n = int(x.shape[0]), int(x.shape[1]), int(weight.shape[0])
+    if x.data_ptr() % 16 or weight.data_ptr() % 16:  # views at odd offsets: the two launches
+        from ayaka.kernel.hip.quant.fp8_quant import per_token_quant_fp8
+
+        q, s = per_token_quant_fp8(x)
+        return fp8_scaled_mm(q, weight.t(), s, weight_scale, bias, out=torch.empty((rows, n), dtype=x.dtype, device=x.device))
+    out = torch.empty((rows, n), dtype=x.dtype, device=x.device)
+    _lib.call(
+        "ayk_fp8_rowwise_linear_small", x.data_ptr(), _lib.dtype_code(x.dtype), int(x.stride(0)), rows,
+        weight.data_ptr(), int(weight.stride(0)), n, k, weight_scale.data_ptr(), int(weight_scale.numel() != 1),
+        _lib.ptr(bias), _lib.dtype_code(bias.dtype) if bias is not None else 0,
+        out.data_ptr(), _lib.dtype_code(out.dtype), n, _lib.stream_of(x),
+    )
+    return out
 
 
 # ------------------------------------------------------------------ block-128

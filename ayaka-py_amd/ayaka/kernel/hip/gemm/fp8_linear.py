@@ -31,7 +31,8 @@ import torch
 
 from ayaka.kernel.hip._common import require_fp8_dtype, validate_bias, validate_operand
 from ayaka.kernel.hip._host import require_cuda, require_dtype, require_tensor
-from ayaka.kernel.hip.gemm.fp8_gemm import fp8_blockwise_mm, fp8_scaled_mm
+from ayaka.kernel.hip.gemm.fp8_gemm import (fp8_blockwise_mm, fp8_rowwise_linear_small, fp8_scaled_mm,
+                                            rowwise_small_applies)
 from ayaka.kernel.hip.gemm.fp8_gemv import fp8_weight_only_gemv
 from ayaka.kernel.hip.gemm.fp8_w8a16_gemm import fp8_weight_only_gemm
 from ayaka.kernel.hip.quant.fp8_quant import (per_token_group_quant_fp8, per_token_group_quant_fp8_colmajor,
@@ -142,6 +143,9 @@ def fp8_rowwise_linear(
     act = _Activation.of(x, weight, bias)
     if act.rows == 1:
         return act.shaped(act.channel_scaled(weight, weight_scale), bias)
+    if rowwise_small_applies(act.matrix, weight, weight_scale):
+        # 2-8 rows against a small weight: quantizer and GEMM in one launch (same bits)
+        return act.shaped(fp8_rowwise_linear_small(act.matrix, weight, weight_scale, bias))
     quantized, token_scale = per_token_quant_fp8(act.matrix)
     result = fp8_scaled_mm(quantized, weight.t(), token_scale, weight_scale, bias=bias, out=act.empty_output(),
                            backend="auto")

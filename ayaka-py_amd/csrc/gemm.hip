@@ -2179,6 +2179,30 @@ int ayk_fp8_scaled_mm(const void* a, int64_t lda, const void* b, int64_t ldb, in
   return launch_gemm<MODE_SCALED>(g, static_cast<hipStream_t>(stream), op);
 }
 
+int ayk_fp8_rowwise_linear_small(const void* x, int x_dtype, int64_t ldx, int64_t M, const void* w, int64_t ldw,
+                                 int64_t N, int64_t K, const float* scale_b, int sb_per_col, const void* bias,
+                                 int bias_dtype, void* out, int out_dtype, int64_t ldo, ayk_stream_t stream) {
+  const char* op = "fp8_rowwise_linear_small";
+  if (M < 0 || N < 0 || K < 1) return fail(AYK_EINVAL, "%s: bad shape", op);
+  if (!x || !w || !scale_b || !out) return fail(AYK_EINVAL, "%s: missing operand", op);
+  if (!is_float_dtype(out_dtype) || (bias && !is_float_dtype(bias_dtype)) || ldo < N)
+    return fail(AYK_EINVAL, "%s: bad output or bias", op);
+  if (M == 0 || N == 0) return AYK_OK;
+  SkinnyFp8Args g{};
+  g.mode = 0;
+  g.w = static_cast<const uint8_t*>(w);
+  g.ldw = ldw;
+  g.M = M; g.N = N; g.K = K;
+  g.sa_vec = 1;
+  g.sb = scale_b; g.sb_vec = sb_per_col;
+  g.bias = bias; g.bias_dtype = bias_dtype;
+  g.out = out; g.out_dtype = out_dtype; g.ldo = ldo;
+  if (!rows_gemv_quant_supported(g, x_dtype, ldx, x))
+    return fail(AYK_EINVAL, "%s: needs 2-8 rows, N * K <= 2^24, K %% 16 == 0, M * K <= 64 KiB and 16-byte aligned rows", op);
+  if (int rc = check_device()) return rc;
+  return rows_gemv_quant_launch(g, x, x_dtype, ldx, static_cast<hipStream_t>(stream), op);
+}
+
 size_t ayk_int8_scaled_mm_workspace_bytes(int64_t M, int64_t N, int64_t K) {
   (void)M; (void)N; (void)K;
   return 0;  // the INT8 GEMM never splits K (its int32 sums stay exact)

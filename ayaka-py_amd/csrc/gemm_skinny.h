@@ -39,5 +39,10 @@ bool skinny_fp8_supported(const SkinnyFp8Args& g);
 size_t skinny_fp8_workspace(int64_t M, int64_t N, int64_t K, int mode);
 // Launch (the kernel and, with a K split, the fixed-order reduce). Returns an ayk_status.
 int skinny_fp8_launch(const SkinnyFp8Args& g, hipStream_t st, const char* op);
+// Per-token quantization of a bf16 / fp16 / fp32 activation (x, row stride ldx in
+// elements) fused with the 2-8-row GEMM (g.a, g.lda, g.sa unused). Returns an ayk_status.
+bool rows_gemv_quant_supported(const SkinnyFp8Args& g, int x_dtype, int64_t ldx, const void* x);
+int rows_gemv_quant_launch(const SkinnyFp8Args& g, const void* x, int x_dtype, int64_t ldx, hipStream_t st,
+                           const char* op);
 
 }  // namespace ayk

@@ -32,6 +32,7 @@
 
 #include "ayk_common.h"
 #include "gemm_util.h"
+#include "quant_math.h"
 
 namespace ayk {
 namespace {
@@ -624,16 +625,50 @@ int scale_chunk(const SkinnyFp8Args& g, const SkPlan& p) {
 // 4096 x 2048 at M = 8 9.2 -> 7.9 us, 4096 x 4096 at M = 2 11.0 -> 5.9 us.
 constexpr int kRgThreads = 256;
 constexpr int kRgRows = 2 * (kRgThreads / kWave);  // weight rows per workgroup
-template <int MR>
-__global__ __launch_bounds__(kRgThreads) void fp8_rows_gemv_kernel(SkinnyFp8Args g) {
+// QUANT: the activation arrives in bf16 / fp16 / fp32 (T, at x with row stride ldx in
+// elements) and the workgroup quantizes it per token itself, with the per-token
+// quantizer's arithmetic (quant_math.h: magnitude-bit amax, clamp_min(1e-10) / 448,
+// Markstein quotient or IEEE division for non-finite rows), into the same e4m3 bytes
+// and fp32 scales that per_token_quant_fp8 writes; the product is then the one the
+// unfused pair of launches computes, bit for bit.
+template <int MR, bool QUANT, typename T>
+__global__ __launch_bounds__(kRgThreads) void fp8_rows_gemv_kernel(SkinnyFp8Args g, const void* x, int64_t ldx) {
   extern __shared__ __attribute__((aligned(16))) uint8_t xs[];  // [M][K] e4m3
+  __shared__ float sas[QUANT ? MR : 1];                       // per-token scales (QUANT)
   const int tid = threadIdx.x, lane = tid & (kWave - 1);
   const int wave = __builtin_amdgcn_readfirstlane(tid / kWave);
   const int K = (int)g.K, M = (int)g.M;
-  // Stage the activation rows (rows past M are never read).
-  for (int i = tid; i < M * (K / 16); i += kRgThreads) {
-    const int m = i / (K / 16), c = i - m * (K / 16);
-    reinterpret_cast<uint4*>(xs)[i] = *reinterpret_cast<const uint4*>(g.a + (int64_t)m * g.lda + 16 * c);
+  if constexpr (QUANT) {
+    constexpr int V = Vec16<T>::N;
+    const int nvec = K / V;
+    for (int m = wave; m < M; m += kRgThreads / kWave) {  // one wavefront per row
+      const uint4* xr = reinterpret_cast<const uint4*>(static_cast<const typename T::storage*>(x) + (int64_t)m * ldx);
+      uint32_t bits = 0;
+      for (int v = lane; v < nvec; v += kWave) bits = absbits_max<T>(xr[v], bits);
+      bits = wave_max_u32<kWave>(absbits_f32<T>(bits));
+      const float sc = floor_amax(u2f(bits)) / kE4M3Max;
+      if (lane == 0) sas[m] = sc;
+      float f[V];
+      if (bits < kInfBits) {  // wavefront-uniform
+        const float r = 1.0f / sc;
+        for (int v = lane; v < nvec; v += kWave) {
+          unpack16<T>(xr[v], f);
+          store_quant_finite<V>(xs + m * K + v * V, f, sc, r);
+        }
+      } else {
+        const Divisor dv = make_divisor(sc);
+        for (int v = lane; v < nvec; v += kWave) {
+          unpack16<T>(xr[v], f);
+          store_quant<V>(xs + m * K + v * V, f, dv);
+        }
+      }
+    }
+  } else {
+    // Stage the activation rows (rows past M are never read).
+    for (int i = tid; i < M * (K / 16); i += kRgThreads) {
+      const int m = i / (K / 16), c = i - m * (K / 16);
+      reinterpret_cast<uint4*>(xs)[i] = *reinterpret_cast<const uint4*>(g.a + (int64_t)m * g.lda + 16 * c);
+    }
   }
   const int64_t n0 = (int64_t)blockIdx.x * kRgRows + 2 * wave;
   const int64_t r0 = n0 < g.N ? n0 : g.N - 1, r1 = n0 + 1 < g.N ? n0 + 1 : g.N - 1;  // rows past N re-read N - 1
@@ -680,7 +715,8 @@ __global__ __launch_bounds__(kRgThreads) void fp8_rows_gemv_kernel(SkinnyFp8Args
   if (m < M && n < g.N) {
     const float* sa = static_cast<const float*>(g.sa);
     const float* sb = static_cast<const float*>(g.sb);
-    float y = (total * sa[g.sa_vec ? m : 0]) * sb[g.sb_vec ? n : 0];
+    const float sam = QUANT ? sas[m] : sa[g.sa_vec ? m : 0];
+    float y = (total * sam) * sb[g.sb_vec ? n : 0];
     if (g.bias) y += load_f32(g.bias, g.bias_dtype, n);
     store_f32(g.out, g.out_dtype, (int64_t)m * g.ldo + n, y);
   }
@@ -694,10 +730,18 @@ int launch_rows_gemv(const SkinnyFp8Args& g, hipStream_t st, const char* op) {
   note_plan("rows_gemv");
   const dim3 grid((unsigned)cdiv(g.N, kRgRows)), block(kRgThreads);
   const unsigned lds = (unsigned)(g.M * g.K);
-  if (g.M <= 2) hipLaunchKernelGGL((fp8_rows_gemv_kernel<2>), grid, block, lds, st, g);
-  else if (g.M <= 4) hipLaunchKernelGGL((fp8_rows_gemv_kernel<4>), grid, block, lds, st, g);
-  else hipLaunchKernelGGL((fp8_rows_gemv_kernel<8>), grid, block, lds, st, g);
+  if (g.M <= 2) hipLaunchKernelGGL((fp8_rows_gemv_kernel<2, false, BF16T>), grid, block, lds, st, g, nullptr, 0);
+  else if (g.M <= 4) hipLaunchKernelGGL((fp8_rows_gemv_kernel<4, false, BF16T>), grid, block, lds, st, g, nullptr, 0);
+  else hipLaunchKernelGGL((fp8_rows_gemv_kernel<8, false, BF16T>), grid, block, lds, st, g, nullptr, 0);
   return check_launch(op);
+}
+template <typename T>
+void launch_rows_gemv_quant(const SkinnyFp8Args& g, const void* x, int64_t ldx, hipStream_t st) {
+  const dim3 grid((unsigned)cdiv(g.N, kRgRows)), block(kRgThreads);
+  const unsigned lds = (unsigned)(g.M * g.K);
+  if (g.M <= 2) hipLaunchKernelGGL((fp8_rows_gemv_kernel<2, true, T>), grid, block, lds, st, g, x, ldx);
+  else if (g.M <= 4) hipLaunchKernelGGL((fp8_rows_gemv_kernel<4, true, T>), grid, block, lds, st, g, x, ldx);
+  else hipLaunchKernelGGL((fp8_rows_gemv_kernel<8, true, T>), grid, block, lds, st, g, x, ldx);
 }
 
 }  // namespace
@@ -746,6 +790,26 @@ int skinny_fp8_launch(const SkinnyFp8Args& g, hipStream_t st, const char* op) {
     return check_launch(op);
   }
   return AYK_OK;
+}
+
+bool rows_gemv_quant_supported(const SkinnyFp8Args& g, int x_dtype, int64_t ldx, const void* x) {
+  const int64_t es = x_dtype == AYK_F32 ? 4 : 2;
+  SkinnyFp8Args q = g;
+  q.mode = kSmScaled;
+  q.a = static_cast<const uint8_t*>(x);  // alignment of the activation rows, as for e4m3 rows
+  q.lda = ldx * es;
+  return (x_dtype == AYK_BF16 || x_dtype == AYK_F16 || x_dtype == AYK_F32) && ldx >= g.K && rows_gemv_wanted(q);
+}
+
+int rows_gemv_quant_launch(const SkinnyFp8Args& g, const void* x, int x_dtype, int64_t ldx, hipStream_t st,
+                           const char* op) {
+  if (!rows_gemv_quant_supported(g, x_dtype, ldx, x))
+    return fail(AYK_EINVAL, "%s: needs 2-8 rows, N * K <= 2^24, K %% 16 == 0, M * K <= 64 KiB, 16-byte aligned rows", op);
+  note_plan("rows_gemv quant");
+  if (x_dtype == AYK_BF16) launch_rows_gemv_quant<BF16T>(g, x, ldx, st);
+  else if (x_dtype == AYK_F16) launch_rows_gemv_quant<F16T>(g, x, ldx, st);
+  else launch_rows_gemv_quant<F32T>(g, x, ldx, st);
+  return check_launch(op);
 }
 
 }  // namespace ayk

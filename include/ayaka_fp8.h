@@ -127,6 +127,19 @@ int ayk_fp8_scaled_mm(const void* a, int64_t lda, const void* b, int64_t ldb,
  * the largest any of these needs for the shape. */
 size_t ayk_fp8_scaled_mm_workspace_bytes(int64_t M, int64_t N, int64_t K);
 
+/* fp8_rowwise_linear (gemm/fp8_linear.py:168) for 2 to 8 activation rows in one launch:
+ * per-token quantization of x (bf16 / fp16 / fp32, row stride ldx in elements) with the
+ * arithmetic of ayk_per_token_quant_fp8, then out = (q @ w^T) * s_token * scale_b + bias,
+ * the same result bit for bit as the two launches. No counterpart in the reference,
+ * which launches the quantizer and the GEMM separately. Requires 2 <= M <= 8,
+ * N * K <= 2^24, K % 16 == 0, M * K <= 64 KiB, 16-byte aligned rows of x and w.
+ * scale_b: fp32 scalar (sb_per_col = 0) or [N]. */
+int ayk_fp8_rowwise_linear_small(const void* x, int x_dtype, int64_t ldx, int64_t M,
+                                 const void* w, int64_t ldw, int64_t N, int64_t K,
+                                 const float* scale_b, int sb_per_col, const void* bias,
+                                 int bias_dtype, void* out, int out_dtype, int64_t ldo,
+                                 ayk_stream_t stream);
+
 /* Replaces ayaka::int8_scaled_mm (gemm/int8_gemm.py:134; oracle reference/gemm.py:192-211).
  * out = float(a @ b^T, int32 accumulation) * scale_a[m] * scale_b[n] + bias, with a the
  * [M, K] int8 activation and b the [N, K] int8 weight; scale_a [M] and scale_b [N] fp32.

@@ -877,6 +877,41 @@ def test_fp8_scaled_mm_small_batch_plans(gpu, m, n, k, rowwise, out_dtype, with_
     assert_linear_close(out, ref, "fp8_scaled_mm small batch")
 
 
+# 2-8 rows of the rowwise linear against a small weight: per-token quantization fused
+# into the GEMV-shaped kernel, bit-identical to the quantizer launch followed by the
+# GEMM; a NaN row and an infinite row take the quantizer's IEEE-division path.
+@pytest.mark.parametrize("m,n,k,xdt,scalar_scale,with_bias", [
+    (8, 3072, 1024, torch.bfloat16, False, True),
+    (2, 4096, 4096, torch.float16, True, False),
+    (5, 1000, 2048, torch.float32, False, True),
+    (3, 300, 256, torch.bfloat16, False, False),
+])
+def test_rowwise_linear_small_fused_quant_is_bit_identical(gpu, m, n, k, xdt, scalar_scale, with_bias):
+    from ayaka.kernel.hip import fp8_scaled_mm, per_token_quant_fp8
+    from ayaka.kernel.hip.gemm.fp8_gemm import fp8_rowwise_linear_small
+
+    _say(f"fp8_rowwise_linear_small m={m} n={n} k={k} x={xdt}")
+    x = (torch.randn(m, k, generator=_gen(11)) * 3).to(xdt)
+    x[m - 1, 5] = float("nan")
+    if m > 2:
+        x[1, 7] = float("inf")
+    w = _fp8((n, k), seed=12, scale=40)
+    ws = torch.tensor(0.003) if scalar_scale else torch.rand(n, generator=_gen(13)) * 0.01 + 1e-3
+    bias = torch.randn(n, generator=_gen(14)).to(xdt) if with_bias else None
+    xg, wg, sg = x.to(gpu), w.to(gpu), ws.to(gpu)
+    bg = bias.to(gpu) if with_bias else None
+    fused = fp8_rowwise_linear_small(xg, wg, sg, bg)
+    assert _plan() == "rows_gemv quant"
+    q, s = per_token_quant_fp8(xg)
+    two = fp8_scaled_mm(q, wg.t(), s, sg, bg, out=torch.empty(m, n, dtype=xdt, device=gpu))
+    view = torch.int32 if xdt == torch.float32 else torch.int16
+    assert torch.equal(fused.view(view), two.view(view))
+    # and against the oracle on the rows without a non-finite element
+    ref = ora.fp8_scaled_mm(q.cpu(), w, s.cpu(), ws, bias)
+    rows = [i for i in range(m) if torch.isfinite(x[i]).all()]
+    assert_linear_close(fused[rows].cpu(), ref[rows], "fp8_rowwise_linear_small")
+
+
 # ------------------------------------------------------------------ linear entry points
 @pytest.mark.parametrize("m", [1, 8, 40])
 @pytest.mark.parametrize("recipe", ["w8a8_rowwise", "w8a8_dynamic_per_tensor", "w8a8_block128"])
