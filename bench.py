@@ -2,11 +2,14 @@
 
 Headline (``value``): BASELINE.json configs[1] -- W8A16 rowwise decode GEMV on the four
 Llama-3-8B projections (qkv 6144x4096, o 4096x4096, gate_up 28672x4096, down 4096x14336)
-at M = 1. One step runs all four projections through ``ayaka::fp8_weight_only_gemv`` as
-``FP8W8A16LinearMethod.apply`` calls it, replayed as one HIP graph; ``value`` is the
-step's algorithmic bytes (fp8 weights + fp32 row scales + bf16 x and out) over its wall
-time, in GB/s. Inputs are resident in HBM before timing; three weight copies (654 MB)
-rotate across steps so the 256 MB MALL cannot serve them.
+at M = 1. One step is one decode token through the model's 32 layers: each layer's four
+projections run through ``ayaka::fp8_weight_only_gemv`` as ``FP8W8A16LinearMethod.apply``
+calls it, and the step (128 launches) is one HIP graph, as a serving loop captures its
+forward pass. Every layer has its own weights (7.0 GB in all, so the 256 MB MALL cannot
+serve them); ``value`` is the step's algorithmic bytes (fp8 weights + fp32 row scales +
+bf16 x and out) over its wall time, in GB/s. Inputs are resident in HBM before timing.
+``graph_per_layer`` times the same projections with one graph per layer instead, which
+pays the graph launch once per four kernels.
 
 ``roofline`` is the dominant kernel (the gate_up GEMV): a graph of back-to-back launches
 replayed between two events on its stream, divided by the launch count.
@@ -44,6 +47,7 @@ HBM_PEAK_GBS = 8000.0
 FP8_PEAK_TFLOPS = 5000.0
 CFG2_SHAPES = [("qkv", 6144, 4096), ("o", 4096, 4096), ("gate_up", 28672, 4096), ("down", 4096, 14336)]
 COPIES = 3
+LAYERS = 32  # Llama-3-8B num_hidden_layers: the decode step's graph holds all of them
 POINT_WARMUP, POINT_REPS = 25, 100
 ROTATE_BYTES = 640 << 20  # decode points rotate weight copies totalling at least this much
 
@@ -56,8 +60,8 @@ def _make_cfg2(device, seed=0):
     g = torch.Generator(device=device).manual_seed(seed)
     layers = []
     for name, n, k in CFG2_SHAPES:
-        copies = []
-        for _ in range(COPIES):
+        copies = []  # layer l's weights and row scales at copies[l]
+        for _ in range(LAYERS):
             wf = torch.randn(n, k, generator=g, device=device) * 0.02
             copies.append(wl.quant_rows(wf))
             del wf
@@ -66,13 +70,19 @@ def _make_cfg2(device, seed=0):
     return layers
 
 
-def _gemv_step(layers, step, out_bufs):
+def _gemv_step(layers, layer, out_bufs):
+    """The four projections of one layer."""
     from ayaka.kernel.hip import fp8_weight_only_gemv
 
-    c = step % COPIES
     for (name, n, k, copies, x), out in zip(layers, out_bufs):
-        w, s = copies[c]
+        w, s = copies[layer % len(copies)]
         fp8_weight_only_gemv(x, w, s, 1, 1, k, "float32", out=out)
+
+
+def _decode_step(layers, out_bufs):
+    """One decode token: the four projections of every layer."""
+    for layer in range(LAYERS):
+        _gemv_step(layers, layer, out_bufs)
 
 
 def _capture(fn):
@@ -657,30 +667,46 @@ def main() -> int:
         return 0
     layers = _make_cfg2(device)
     outs = [torch.empty(n, dtype=torch.bfloat16, device=device) for _, n, _, _, _ in layers]
-    step_bytes = sum(_gemv_bytes(n, k) for _, n, k, _, _ in layers)
+    layer_bytes = sum(_gemv_bytes(n, k) for _, n, k, _, _ in layers)
+    step_bytes = LAYERS * layer_bytes
 
     # Eager (one Python dispatch per projection): host-bound at decode sizes.
-    for i in range(args.warmup):
-        _gemv_step(layers, i, outs)
+    for _ in range(max(1, args.warmup // 5)):
+        _decode_step(layers, outs)
     torch.cuda.synchronize()
+    eager_steps = max(1, args.steps // 5)
     t0 = time.perf_counter()
-    for i in range(args.steps):
-        _gemv_step(layers, i, outs)
+    for _ in range(eager_steps):
+        _decode_step(layers, outs)
     torch.cuda.synchronize()
-    eager_ms = (time.perf_counter() - t0) * 1e3 / args.steps
+    eager_ms = (time.perf_counter() - t0) * 1e3 / eager_steps
 
-    # Graph mode: each step (the four projections on one weight copy) is a HIP graph,
-    # replayed back to back as a decode loop does; copies rotate every step.
-    graphs = [_capture(lambda c=c: _gemv_step(layers, c, outs)) for c in range(COPIES)]
-    for i in range(args.warmup):
-        graphs[i % COPIES].replay()
+    # One graph per layer (four kernels each), replayed layer after layer.
+    layer_graphs = [_capture(lambda c=c: _gemv_step(layers, c, outs)) for c in range(LAYERS)]
+    for g_ in layer_graphs:
+        g_.replay()
     torch.cuda.synchronize()
     t0 = time.perf_counter()
-    for i in range(args.steps):
-        graphs[i % COPIES].replay()
+    for _ in range(max(1, args.steps // 5)):
+        for g_ in layer_graphs:
+            g_.replay()
+    torch.cuda.synchronize()
+    per_layer_graph_ms = (time.perf_counter() - t0) * 1e3 / max(1, args.steps // 5)
+    del layer_graphs
+
+    # The decode step as a serving loop runs it: the whole step is one HIP graph,
+    # replayed back to back.
+    graph = _capture(lambda: _decode_step(layers, outs))
+    for _ in range(args.warmup):
+        graph.replay()
+    torch.cuda.synchronize()
+    t0 = time.perf_counter()
+    for _ in range(args.steps):
+        graph.replay()
     torch.cuda.synchronize()
     ms_per_step = (time.perf_counter() - t0) * 1e3 / args.steps
     value = step_bytes / (ms_per_step * 1e-3) / 1e9
+    del graph
 
     n, k, avg_ms, med_ms = _time_dominant(layers)
     achieved = _gemv_bytes(n, k) / (avg_ms * 1e-3) / 1e9
@@ -697,9 +723,12 @@ def main() -> int:
         "vs_baseline": None,
         "dtype": "e4m3 weights x bf16 activations, fp32 accumulate",
         "data": "synthetic (seeded N(0,0.02) weights, per-row e4m3 quant; N(0,1) activations with 1% x20 outlier channels)",
-        "config": {"workload": "BASELINE configs[1]: W8A16 rowwise GEMV, Llama-3-8B decode, M=1, qkv+o+gate_up+down",
-                   "shapes_NK": [[n_, k_] for _, n_, k_ in CFG2_SHAPES], "weight_copies_rotated": COPIES,
-                   "launch": "one HIP graph per step (4 projections)"},
+        "config": {"workload": "BASELINE configs[1]: W8A16 rowwise GEMV, Llama-3-8B decode, M=1, qkv+o+gate_up+down of each of the 32 layers",
+                   "shapes_NK": [[n_, k_] for _, n_, k_ in CFG2_SHAPES], "layers": LAYERS,
+                   "launch": "one HIP graph per decode step (32 layers x 4 projections)"},
+        "graph_per_layer": {"ms_per_step": round(per_layer_graph_ms, 5),
+                            "value": round(step_bytes / (per_layer_graph_ms * 1e-3) / 1e9, 1),
+                            "note": "one HIP graph per layer (4 projections), 32 replays per step"},
         "eager": {"ms_per_step": round(eager_ms, 5), "value": round(step_bytes / (eager_ms * 1e-3) / 1e9, 1),
                   "note": "one Python op dispatch per projection, no graph"},
         "roofline": {"bound": "hbm", "kernel": "gemv_stream_kernel (gate_up 28672x4096)", "achieved": round(achieved, 1),
@@ -708,7 +737,7 @@ def main() -> int:
                      "bytes_per_launch": _gemv_bytes(n, k), "traffic": _measured_traffic()},
         "cfg2_m1_projections": _cfg2_projections(layers),
     }
-    del graphs, layers, outs
+    del layers, outs
     torch.cuda.empty_cache()
     if not args.no_gemm:
         configs = _bench_configs(device)
