@@ -48,6 +48,10 @@ def _fp8(shape, seed, scale=1.0):
         (3072, 1024, 3072, 1024, "float32"),  # one scalar scale broadcast
         (300, 4096, 1, 4096, "float32"),
         (4096, 14336, 1, 14336, "float32"),  # Cfg2 down (split-K)
+        (4098, 1024, 1, 1024, "float32"),  # streaming: 2049 one-pair wavefronts, 3 idle
+        (6147, 2048, 1, 2048, "float32"),  # streaming, ragged last pair
+        (8190, 1024, 1, 1024, "float32"),  # streaming: 4095 one-pair wavefronts
+        (8194, 1024, 1, 1024, "float32"),  # streaming: 4097 pairs, three per wavefront
         (520, 7168, 128, 128, "float32"),  # block-128 decode
         (700, 1792, 128, 128, "bfloat16"),
         (256, 2048, 1, 32, "e8m0"),  # per-32 UE8M0
