@@ -639,25 +639,64 @@ __global__ __launch_bounds__(kRgThreads) void fp8_rows_gemv_kernel(SkinnyFp8Args
   const int wave = __builtin_amdgcn_readfirstlane(tid / kWave);
   const int K = (int)g.K, M = (int)g.M;
   if constexpr (QUANT) {
+    // Wavefront w quantizes rows w and w + 4. The loads of both rows are issued before
+    // any reduction, and the first kHeld vectors per lane of each row stay in registers
+    // for the quantizing pass (a second read only past kHeld * 64 vectors), so the
+    // prologue is one memory round trip rather than two per row.
     constexpr int V = Vec16<T>::N;
+    constexpr int kWaves = kRgThreads / kWave;
+    constexpr int kRowsPerWave = (MR + kWaves - 1) / kWaves;
+    constexpr int kHeld = 4;
     const int nvec = K / V;
-    for (int m = wave; m < M; m += kRgThreads / kWave) {  // one wavefront per row
+    uint4 held[kRowsPerWave][kHeld];
+#pragma unroll
+    for (int rr = 0; rr < kRowsPerWave; ++rr) {
+      const int m = wave + kWaves * rr;
+      const uint4* xr = reinterpret_cast<const uint4*>(static_cast<const typename T::storage*>(x) + (int64_t)(m < M ? m : 0) * ldx);
+#pragma unroll
+      for (int h = 0; h < kHeld; ++h) {
+        const int v = lane + kWave * h;
+        held[rr][h] = m < M && v < nvec ? xr[v] : make_uint4(0, 0, 0, 0);
+      }
+    }
+#pragma unroll
+    for (int rr = 0; rr < kRowsPerWave; ++rr) {
+      const int m = wave + kWaves * rr;
+      if (m >= M) continue;  // wavefront-uniform
       const uint4* xr = reinterpret_cast<const uint4*>(static_cast<const typename T::storage*>(x) + (int64_t)m * ldx);
       uint32_t bits = 0;
-      for (int v = lane; v < nvec; v += kWave) bits = absbits_max<T>(xr[v], bits);
+#pragma unroll
+      for (int h = 0; h < kHeld; ++h) bits = absbits_max<T>(held[rr][h], bits);  // zeros past the row add nothing
+      for (int v = lane + kWave * kHeld; v < nvec; v += kWave) bits = absbits_max<T>(xr[v], bits);
       bits = wave_max_u32<kWave>(absbits_f32<T>(bits));
       const float sc = floor_amax(u2f(bits)) / kE4M3Max;
       if (lane == 0) sas[m] = sc;
       float f[V];
       if (bits < kInfBits) {  // wavefront-uniform
         const float r = 1.0f / sc;
-        for (int v = lane; v < nvec; v += kWave) {
+#pragma unroll
+        for (int h = 0; h < kHeld; ++h) {
+          const int v = lane + kWave * h;
+          if (v < nvec) {
+            unpack16<T>(held[rr][h], f);
+            store_quant_finite<V>(xs + m * K + v * V, f, sc, r);
+          }
+        }
+        for (int v = lane + kWave * kHeld; v < nvec; v += kWave) {
           unpack16<T>(xr[v], f);
           store_quant_finite<V>(xs + m * K + v * V, f, sc, r);
         }
       } else {
         const Divisor dv = make_divisor(sc);
-        for (int v = lane; v < nvec; v += kWave) {
+#pragma unroll
+        for (int h = 0; h < kHeld; ++h) {
+          const int v = lane + kWave * h;
+          if (v < nvec) {
+            unpack16<T>(held[rr][h], f);
+            store_quant<V>(xs + m * K + v * V, f, dv);
+          }
+        }
+        for (int v = lane + kWave * kHeld; v < nvec; v += kWave) {
           unpack16<T>(xr[v], f);
           store_quant<V>(xs + m * K + v * V, f, dv);
         }
@@ -747,6 +786,10 @@ void launch_rows_gemv_quant(const SkinnyFp8Args& g, const void* x, int64_t ldx, 
 }  // namespace
 
 bool skinny_fp8_supported(const SkinnyFp8Args& g) {
+  const bool out_ok = g.out_dtype == AYK_F32 || g.out_dtype == AYK_BF16 || g.out_dtype == AYK_F16;
+  // The GEMV-shaped kernel has rules of its own (any K % 16 == 0), so that the unfused
+  // quantizer + GEMM pair takes the same kernel as the fused small-batch linear.
+  if (rows_gemv_wanted(g)) return out_ok;
   const SkPlan p = skinny_plan(g.M, g.N, g.K, g.mode);
   if (!p.ok) return false;
   if (g.lda % 16 || g.ldw % 16 || !aligned16(g.a) || !aligned16(g.w)) return false;
@@ -760,7 +803,7 @@ bool skinny_fp8_supported(const SkinnyFp8Args& g) {
         (!g.sa_vec && g.ld_sa < g.K / 128))
       return false;
   }
-  return g.out_dtype == AYK_F32 || g.out_dtype == AYK_BF16 || g.out_dtype == AYK_F16;
+  return out_ok;
 }
 
 size_t skinny_fp8_workspace(int64_t M, int64_t N, int64_t K, int mode) {

@@ -889,6 +889,8 @@ def test_fp8_scaled_mm_small_batch_plans(gpu, m, n, k, rowwise, out_dtype, with_
     (2, 4096, 4096, torch.float16, True, False),
     (5, 1000, 2048, torch.float32, False, True),
     (3, 300, 256, torch.bfloat16, False, False),
+    (6, 520, 8192, torch.bfloat16, True, True),  # two rows on some wavefronts, long rows
+    (7, 264, 1040, torch.float16, False, False),  # a row length that is no multiple of 64 vectors
 ])
 def test_rowwise_linear_small_fused_quant_is_bit_identical(gpu, m, n, k, xdt, scalar_scale, with_bias):
     from ayaka.kernel.hip import fp8_scaled_mm, per_token_quant_fp8
