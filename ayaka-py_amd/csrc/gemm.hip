@@ -81,6 +81,10 @@ struct GemmArgs {
   // 256 x 256 pair kernel: work items (tiles, plus tail pieces); a workgroup runs items
   // blockIdx.x, blockIdx.x + gridDim.x, ...
   int items;
+  // 256 x 256 pair kernel, K split of every tile (kps > 0): with kpieces > 0 the grid is
+  // one-dimensional and workgroup b takes K piece b % kpieces of tile b / kpieces;
+  // 0: grid (tiles, pieces).
+  int kpieces;
 };
 
 __device__ inline v16f mfma(const v8i& wa, const v8i& ab, const v16f& c, int sw, int sa) {
@@ -1206,8 +1210,13 @@ __global__ __launch_bounds__(kThreads, 1) void fp8_gemm_pair_kernel(GemmArgs gin
   auto frags_step0 = [&](const uint8_t* buf) __attribute__((always_inline)) { read_frags(0, buf, 0); };
   constexpr std::integral_constant<int, 0> kBuf0{};
   constexpr std::integral_constant<int, 1> kBuf1{};
-  int item = blockIdx.x;
-  Src src = make_src(pair_item<MODE>(gin, item, blockIdx.y));
+  // Piece-major K splits: workgroups are dealt to the XCDs round-robin (b % 8), so with
+  // a multiple of 8 pieces every tile of one piece runs on one XCD and the piece's
+  // operand slices (its K range of the weight and of the activation) are fetched into
+  // that XCD's L2 once, instead of once per XCD that runs one of its tiles.
+  const int piece = gin.kpieces > 0 ? (int)(blockIdx.x % (unsigned)gin.kpieces) : (int)blockIdx.y;
+  int item = gin.kpieces > 0 ? (int)(blockIdx.x / (unsigned)gin.kpieces) : (int)blockIdx.x;
+  Src src = make_src(pair_item<MODE>(gin, item, piece));
   int cbase = 0;  // C half of the item's code chunk 0
   // Prologue: pairs 0 and 1 in flight (pair 0's codes between them), pair 0 visible,
   // step (0, 0)'s fragments in set 0.
@@ -1257,9 +1266,9 @@ __global__ __launch_bounds__(kThreads, 1) void fp8_gemm_pair_kernel(GemmArgs gin
     // The next item (this one again when there is none: its loads then land unused).
     const int next = item + (int)gridDim.x;
     const bool more = next < gin.items;
-    const Src nsrc = make_src(pair_item<MODE>(gin, more ? next : item, blockIdx.y));
+    const Src nsrc = make_src(pair_item<MODE>(gin, more ? next : item, piece));
     const int ncbase = (cbase + npairs / 4) & 1;  // MX: npairs == np, a multiple of 4
-    const PairItem it = pair_item<MODE>(gin, item, blockIdx.y);
+    const PairItem it = pair_item<MODE>(gin, item, piece);
     // Pair npairs - 2, step 1: its refill is this item's output scales and bias (one and
     // a half pairs ahead of the epilogue) and the next item's pair 0 (and code chunk 0).
     PairScales scales;
@@ -1679,6 +1688,11 @@ int64_t scaled_split(int64_t M, int64_t N, int64_t K, int bm, int bn) {
   return cdiv(K, kps);
 }
 int64_t scaled_kps(int64_t K, int64_t split) { return cdiv(K / 128, split) * 128; }
+// The pair kernel's K split, launched piece-major: a planned split of 8 or more is
+// rounded down to a multiple of 8, so that each piece's tiles share one XCD (its L2).
+// Qwen2 down at M = 512 (28 tiles): 9 pieces over all eight XCDs fetched 2.2x the
+// unique operand bytes (each XCD re-read the activation slices of every piece).
+int64_t xcd_pieces(int64_t planned) { return planned >= 8 ? planned / 8 * 8 : planned; }
 
 // Tail split of the 256 x 256 pair kernel (launches of more than one round): when the
 // last round would hold at most a third of a round of tiles, those tiles are split over
@@ -1949,7 +1963,7 @@ int launch_big(GemmArgs g, hipStream_t st, const char* op) {
   if constexpr (MODE == MODE_MX) {
     if (g.K % 512 == 0 && g.ld_sa % 16 == 0 && g.ld_sb % 16 == 0 && aligned16(g.sa) && aligned16(g.sb)) {
       // K per split in whole chunks of four 128-K pairs (keeps the code rows 16-byte aligned)
-      const int64_t planned = scaled_split(g.M, g.N, g.K, kBigTile, kBigTile);
+      const int64_t planned = xcd_pieces(scaled_split(g.M, g.N, g.K, kBigTile, kBigTile));
       const int64_t kps = planned > 1 ? cdiv(g.K / 512, planned) * 512 : g.K;
       const int64_t split = cdiv(g.K, kps);
       g.kps = split > 1 ? kps : 0;
@@ -1960,8 +1974,9 @@ int launch_big(GemmArgs g, hipStream_t st, const char* op) {
       }
       if (split == 1) return launch_pair_tail<MODE>(g, tiles, st, op);
       note_plan("pair split=%d", (int)split);
-      g.items = (int)tiles;  // one item per workgroup: grid (tiles, split)
-      hipLaunchKernelGGL((fp8_gemm_pair_kernel<MODE>), dim3((unsigned)tiles, (unsigned)split), dim3(kThreads), 0, st, g);
+      g.items = (int)tiles;  // one item per workgroup, piece-major
+      g.kpieces = (int)split;
+      hipLaunchKernelGGL((fp8_gemm_pair_kernel<MODE>), dim3((unsigned)(tiles * split)), dim3(kThreads), 0, st, g);
       if (int rc = check_launch(op)) return rc;
       launch_split_reduce(block_split_reduce, g.ws, g.M, g.N, (int)split, g.bias, g.bias_dtype, g.out, g.out_dtype,
                           g.ldo, st);
@@ -1971,18 +1986,19 @@ int launch_big(GemmArgs g, hipStream_t st, const char* op) {
     }
   } else if (g.K % (2 * kBigK) == 0) {
     // INT8 never splits: a split's partial would leave the exact int32 accumulator.
-    const int64_t split = MODE == MODE_SCALED ? scaled_split(g.M, g.N, g.K, kBigTile, kBigTile) : 1;
-    g.kps = 0;
+    const int64_t planned = MODE == MODE_SCALED ? xcd_pieces(scaled_split(g.M, g.N, g.K, kBigTile, kBigTile)) : 1;
+    g.kps = planned > 1 ? scaled_kps(g.K, planned) : 0;
+    const int64_t split = planned > 1 ? cdiv(g.K, g.kps) : 1;
     if (split > 1) {
       const size_t need = (size_t)split * (size_t)g.M * (size_t)g.N * sizeof(float);
       if (g.ws == nullptr || g.ws_bytes < need)
         return fail(AYK_EWORKSPACE, "%s: workspace of %zu bytes required, %zu given", op, need, g.ws_bytes);
-      g.kps = scaled_kps(g.K, split);
     }
     if (split == 1 && MODE == MODE_SCALED) return launch_pair_tail<MODE>(g, tiles, st, op);
     note_plan("pair split=%d", (int)split);
     g.items = (int)tiles;
-    hipLaunchKernelGGL((fp8_gemm_pair_kernel<MODE>), dim3(split > 1 ? (unsigned)tiles : pair_grid(tiles), (unsigned)split),
+    g.kpieces = split > 1 ? (int)split : 0;  // piece-major, one item per workgroup
+    hipLaunchKernelGGL((fp8_gemm_pair_kernel<MODE>), dim3(split > 1 ? (unsigned)(tiles * split) : pair_grid(tiles)),
                        dim3(kThreads), 0, st, g);
     if (split > 1) {
       if (int rc = check_launch(op)) return rc;
