@@ -1,0 +1,116 @@
+"""GPU: a seeded sweep of shapes through the drop-in layer API, every recipe.
+
+The config-point and kernel tests pin the shapes the benchmarks use and the edges each
+kernel's plan names. This sweep draws (M, N, K) at random, from 1-row decode up to
+K-split and 256 x 256 prefill launches, with ragged N and K where the recipe allows,
+and checks ``LinearMethod.apply`` (activation quant + kernel choice + epilogue) against
+the CPU oracle's composition of the same recipe under the stated tolerance. The kernel
+routes differ by M, N, K and alignment, so a shape that falls between the planned
+cases is where a dispatch mistake would show.
+"""
+
+import random
+import sys
+
+import pytest
+import torch
+from torch import nn
+
+from oracle import fp8_oracle as ora
+from tests._tol import assert_linear_close, rounding_allowance
+
+pytestmark = pytest.mark.gpu
+FP8 = torch.float8_e4m3fn
+
+CONFIGS = {
+    "w8a8_rowwise": {"fp8_recipe": "w8a8_rowwise"},
+    "w8a8_dynamic_per_tensor": {"quant_method": "fp8", "activation_scheme": "dynamic"},
+    "w8a8_static_per_tensor": {"quant_method": "fp8", "activation_scheme": "static"},
+    "w8a8_block128": {"weight_block_size": [128, 128], "scale_format": "float32"},
+    "mxfp8": {"quant_algo": "mxfp8"},
+    "w8a16": {"quant_algo": "w8a16"},
+}
+K_UNIT = {"w8a8_block128": 128, "mxfp8": 32}  # the dynamic quantizers' group widths; else 16
+
+
+def _cases(per_recipe=24, seed=2024):
+    rng = random.Random(seed)
+    cases = []
+    for recipe in CONFIGS:
+        unit = K_UNIT.get(recipe, 16)
+        for i in range(per_recipe):
+            m = [1, rng.randint(2, 8), rng.randint(9, 64), rng.randint(65, 255), rng.randint(256, 640),
+                 rng.randint(2, 640)][i % 6]
+            n = rng.choice([rng.randint(8, 700), rng.randint(256, 2600), 4 * rng.randint(64, 650)])
+            k = unit * rng.randint(max(1, 128 // unit), 4096 // unit)
+            xdt = rng.choice(["bfloat16", "bfloat16", "float16"])
+            cases.append((recipe, m, n, k, xdt))
+    return cases
+
+
+def _checkpoint(recipe, n, k, g):
+    """Checkpoint tensors of one recipe for an [n, k] weight: (e4m3 weight, scale)."""
+    wf = torch.randn(n, k, generator=g) * 0.02
+    if recipe in ("w8a8_rowwise", "w8a16"):
+        s = wf.abs().amax(dim=1).clamp_min(1e-6) / 448
+        return (wf / s[:, None]).to(FP8), s
+    if recipe in ("w8a8_dynamic_per_tensor", "w8a8_static_per_tensor"):
+        s = wf.abs().amax() / 448
+        return (wf / s).to(FP8), s.reshape(())
+    if recipe == "w8a8_block128":
+        nb, kb = -(-n // 128), k // 128
+        pad = torch.zeros(nb * 128, k)
+        pad[:n] = wf
+        s = pad.reshape(nb, 128, kb, 128).abs().amax(dim=(1, 3)).clamp_min(1e-6) / 448
+        w = (pad / s.repeat_interleave(128, 0).repeat_interleave(128, 1))[:n].to(FP8)
+        return w, s
+    if recipe == "mxfp8":
+        return ora.per_token_group_quant_mxfp8(wf, 32)
+    raise AssertionError(recipe)
+
+
+@pytest.mark.parametrize("recipe,m,n,k,xdt", _cases())
+def test_linear_shape_sweep(gpu, recipe, m, n, k, xdt):
+    from ayaka.layers.linear.fp8 import FP8Config
+
+    print(f"shape sweep recipe={recipe} m={m} n={n} k={k} x={xdt}", flush=True)
+    xdt = getattr(torch, xdt)
+    sys.stdout.flush()
+    g = torch.Generator().manual_seed(m * 7919 + n * 31 + k)
+    w, s = _checkpoint(recipe, n, k, g)
+    method = FP8Config.from_config(CONFIGS[recipe]).get_quant_method(None, "model.layers.0.mlp.down_proj")
+    layer = nn.Module()
+    method.create_weights(layer, output_partition_sizes=[n], input_size_per_partition=k, params_dtype=xdt, device=gpu)
+    layer.weight.data.copy_(w.to(gpu))
+    param = getattr(layer, "weight_scale_inv" if recipe == "w8a8_block128" else "weight_scale")
+    param.weight_loader(layer, param, s.to(gpu))
+    input_scale = None
+    if recipe == "w8a8_static_per_tensor":
+        input_scale = torch.tensor(0.05)
+        layer.input_scale.weight_loader(layer, layer.input_scale, input_scale.to(gpu))
+    method.process_weights_after_loading(layer)
+
+    x = torch.randn(m, k, generator=g).to(xdt)
+    bias = torch.randn(n, generator=g).to(xdt)
+    y = method.apply(layer, x.to(gpu), bias.to(gpu))
+    kw = {}
+    if recipe == "w8a16":
+        kw = dict(weight_block=None, scale_dtype="float32")
+        s_ref = s.reshape(n, 1)
+    elif recipe in ("w8a8_dynamic_per_tensor", "w8a8_static_per_tensor"):
+        s_ref = torch.full((n,), float(s))  # the loader broadcasts the scalar into [N]
+    else:
+        s_ref = s
+    # The bias order of the path taken: the W8A8 GEMMs add it in fp32 before their one
+    # rounding; the weight-only paths (W8A16 at every M, the M = 1 GEMV of the W8A8
+    # recipes) round first and add it in bf16, as the reference does. MXFP8 fuses it.
+    # Rounding before the add can move a result that cancels against the bias by one
+    # ulp of the product on either side of a rounding boundary: that ulp (and one
+    # of the sum) is allowed on top of the tolerance there, as in the lifecycle test.
+    fused_bias = recipe != "w8a16" and m > 1
+    ref = ora.fp8_linear(recipe, x, w, s_ref, bias, input_scale=input_scale, bias_in_fp32=fused_bias, **kw)
+    extra = None
+    if not fused_bias:
+        gemm = ora.fp8_linear(recipe, x, w, s_ref, None, input_scale=input_scale, **kw)
+        extra = rounding_allowance(gemm, ref, xdt).reshape(m, n)
+    assert_linear_close(y.reshape(m, n), ref, f"{recipe} m={m} n={n} k={k}", extra=extra)
