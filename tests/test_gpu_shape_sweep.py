@@ -114,3 +114,50 @@ def test_linear_shape_sweep(gpu, recipe, m, n, k, xdt):
         gemm = ora.fp8_linear(recipe, x, w, s_ref, None, input_scale=input_scale, **kw)
         extra = rounding_allowance(gemm, ref, xdt).reshape(m, n)
     assert_linear_close(y.reshape(m, n), ref, f"{recipe} m={m} n={n} k={k}", extra=extra)
+
+
+def _quant_cases(n=48, seed=99):
+    rng = random.Random(seed)
+    kinds = ["per_token", "group128", "group_col", "mx32", "static"]
+    cases = []
+    for i in range(n):
+        kind = kinds[i % len(kinds)]
+        m = rng.choice([1, rng.randint(2, 16), rng.randint(17, 700)])
+        unit = {"group128": 128, "group_col": 128, "mx32": 32}.get(kind, 1)
+        k = unit * rng.randint(1, 20000 // unit) if rng.random() < 0.7 else unit * rng.randint(1, 256 // unit + 1)
+        cases.append((kind, m, k, rng.choice(["bfloat16", "float16", "float32"])))
+    return cases
+
+
+def _bits(t):
+    t = t.cpu().contiguous()
+    return t.view(torch.uint8) if t.dtype == FP8 else (t.view(torch.int32) if t.dtype == torch.float32 else t)
+
+
+@pytest.mark.parametrize("kind,m,k,xdt", _quant_cases())
+def test_quant_shape_sweep(gpu, kind, m, k, xdt):
+    """The activation quantizers on random shapes: e4m3 bytes and scales bit-exact."""
+    from ayaka.kernel.hip import (per_token_group_quant_fp8, per_token_group_quant_mxfp8, per_token_quant_fp8,
+                                  static_quant_fp8)
+    from ayaka.kernel.hip.quant.fp8_quant import per_token_group_quant_fp8_colmajor
+
+    print(f"quant sweep {kind} m={m} k={k} x={xdt}", flush=True)
+    g = torch.Generator().manual_seed(m * 131 + k)
+    x = (torch.randn(m, k, generator=g) * torch.exp(torch.randn(m, 1, generator=g) * 3)).to(getattr(torch, xdt))
+    xg = x.to(gpu)
+    if kind == "per_token":
+        (q, s), (rq, rs) = per_token_quant_fp8(xg), ora.per_token_quant(x)
+    elif kind == "group128":
+        (q, s), (rq, rs) = per_token_group_quant_fp8(xg, 128), ora.per_token_group_quant(x, 128)
+    elif kind == "group_col":
+        (q, s_t), (rq, rs) = per_token_group_quant_fp8_colmajor(xg, 128), ora.per_token_group_quant(x, 128)
+        s = s_t.t()  # [K / 128, M] column-major scales
+    elif kind == "mx32":
+        (q, s), (rq, rs) = per_token_group_quant_mxfp8(xg, 32), ora.per_token_group_quant_mxfp8(x, 32)
+    else:
+        scale = torch.tensor(0.03)
+        q, s = static_quant_fp8(xg, scale.to(gpu)), scale
+        rq, rs = ora.static_quant(x, scale), scale
+    torch.cuda.synchronize()
+    assert torch.equal(_bits(s.reshape(rs.shape)), _bits(rs)), "scales differ"
+    assert torch.equal(_bits(q), _bits(rq)), "codes differ"
