@@ -193,3 +193,39 @@ def test_grouped_mm_transposed_scales_match(gpu, monkeypatch, partial):
         out, _ = _run(gpu, a, b, sa, sb, ps, off, torch.bfloat16)
         outs.append(out.cpu())
     assert torch.equal(outs[0].view(torch.int16), outs[1].view(torch.int16))
+
+
+def _random_cases(n_cases=12, seed=5):
+    import random
+
+    rng = random.Random(seed)
+    cases = []
+    for i in range(n_cases):
+        e = rng.randint(1, 40)
+        hi = rng.choice([4, 140, 300])
+        counts = [0 if rng.random() < 0.15 else rng.randint(1, hi) for _ in range(e)]
+        if i == n_cases - 1:  # enough rows for the column-major scale path
+            counts = [rng.randint(90, 130) for _ in range(40)]
+        cases.append((counts, 128 * rng.randint(1, 8), 128 * rng.randint(1, 16), rng.choice([0, 0, 1, 3])))
+    return cases
+
+
+RANDOM_CASES = _random_cases()
+
+
+@pytest.mark.parametrize("case", range(len(RANDOM_CASES)))
+def test_grouped_mm_random_experts(gpu, case):
+    """Seeded random expert counts (empty experts included), N, K and free rows."""
+    counts, n, k, gap = RANDOM_CASES[case]
+    _say(f"grouped mm random case={case} E={len(counts)} rows={sum(counts)} n={n} k={k} gap={gap}")
+    a, b, sa, sb, ps, off = _problem(counts, n, k, seed=100 + case, gap_every=gap)
+    out, _ = _run(gpu, a, b, sa, sb, ps, off, torch.bfloat16)
+    sentinel = torch.full((a.shape[0], n), 3.0, dtype=torch.bfloat16)
+    ref = ora.grouped_blockwise_mm(a, b, sa, sb, ps, off, sentinel.float())
+    owned = torch.zeros(a.shape[0], dtype=torch.bool)
+    for c, o in zip(counts, off.tolist()):
+        owned[o:o + c] = True
+    got = out.cpu()
+    assert torch.equal(got[~owned], sentinel[~owned]), "rows of no expert were written"
+    if owned.any():
+        assert_linear_close(got[owned], ref[owned], f"random case {case}")
