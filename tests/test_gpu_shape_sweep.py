@@ -161,3 +161,43 @@ def test_quant_shape_sweep(gpu, kind, m, k, xdt):
     torch.cuda.synchronize()
     assert torch.equal(_bits(s.reshape(rs.shape)), _bits(rs)), "scales differ"
     assert torch.equal(_bits(q), _bits(rq)), "codes differ"
+
+
+def _w8a16_cases(n=30, seed=31):
+    rng = random.Random(seed)
+    layouts = [(1, 0, "float32"), (128, 128, "bfloat16"), (128, 128, "float32"), (1, 32, "e8m0"), (64, 64, "float32")]
+    cases = []
+    for i in range(n):
+        by, bx, sdt = layouts[i % len(layouts)]
+        m = rng.choice([1, rng.randint(2, 8), rng.randint(9, 32), rng.randint(33, 300)])
+        nn_ = rng.randint(16, 3000)
+        k = rng.choice([256 * rng.randint(1, 24), 16 * rng.randint(1, 400)])
+        if bx:
+            k = max(bx, k // bx * bx)
+        cases.append((m, nn_, k, by, bx, sdt, rng.choice(["bfloat16", "float16"])))
+    return cases
+
+
+@pytest.mark.parametrize("m,n,k,by,bx,sdt,xdt", _w8a16_cases())
+def test_weight_only_shape_sweep(gpu, m, n, k, by, bx, sdt, xdt):
+    """W8A16 GEMV / GEMM on random shapes and every scale layout (per channel, 128 x 128
+    bf16 / fp32 blocks, per-32 UE8M0, 64 x 64) against the oracle."""
+    from ayaka.kernel.hip import fp8_weight_only_gemm, fp8_weight_only_gemv
+
+    print(f"w8a16 sweep m={m} n={n} k={k} block={by}x{bx} scale={sdt} x={xdt}", flush=True)
+    bx = bx or k  # 0: one scale per row
+    g = torch.Generator().manual_seed(m * 17 + n * 3 + k)
+    w = (torch.randn(n, k, generator=g) * 40).clamp(-448, 448).to(FP8)
+    rows, cols = -(-n // by), -(-k // bx)
+    if sdt == "e8m0":
+        scale = torch.randint(115, 125, (rows, cols), generator=g, dtype=torch.uint8)
+    else:
+        scale = (torch.rand(rows, cols, generator=g) * 0.01 + 1e-3).to(getattr(torch, sdt))
+    x = torch.randn(m, k, generator=g).to(getattr(torch, xdt))
+    if m == 1:
+        y = fp8_weight_only_gemv(x.reshape(k).to(gpu), w.to(gpu), scale.to(gpu), cols, by, bx, sdt).reshape(1, n)
+        ref = ora.fp8_weight_only_gemv(x.reshape(k), w, scale, cols, by, bx, sdt).reshape(1, n)
+    else:
+        y = fp8_weight_only_gemm(x.to(gpu), w.to(gpu), scale.to(gpu), cols, by, bx, sdt)
+        ref = ora.fp8_weight_only_gemm(x, w, scale, cols, by, bx, sdt)
+    assert_linear_close(y, ref, f"w8a16 m={m} n={n} k={k} {by}x{bx} {sdt}")
