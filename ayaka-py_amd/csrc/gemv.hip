@@ -500,10 +500,12 @@ constexpr int64_t kStreamWavesTarget = 2048;
 bool stream_plan(int act, int as, int64_t N, int64_t K, int64_t& ppw, int& lds) {
   const int64_t npairs = cdiv(N, kPair);
   if (npairs < kStreamWavesTarget) return false;
-  // Below twice the target every wavefront takes one pair (up to 4095 wavefronts): the
-  // small projections are ramp-bound, and more wavefronts put more bytes in flight
-  // (Llama-3-8B qkv, 3072 pairs: 7.0 -> 6.85 us against 1536 wavefronts of two pairs).
-  ppw = npairs < 2 * kStreamWavesTarget ? 1 : cdiv(npairs, kStreamWavesTarget);
+  // Short rows below twice the target: every wavefront takes one pair (up to 4095
+  // wavefronts). Such a projection is ramp-bound, and more wavefronts put more bytes in
+  // flight (Llama-3-8B qkv, 3072 pairs of K = 4096: 7.0 -> 6.85 us against 1536
+  // wavefronts of two pairs). Long rows keep two pairs per wavefront (DSv3 down,
+  // 3584 pairs of K = 18432: 23.5 us, against 25.4 with one).
+  ppw = npairs < 2 * kStreamWavesTarget && K <= 4096 ? 1 : cdiv(npairs, kStreamWavesTarget);
   (void)as;
   lds = stream_lds(act, K).total();
   return lds <= kStreamLdsMax && ppw * kPair <= kStreamRowsMax && N < INT32_MAX && K < INT32_MAX;
