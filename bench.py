@@ -100,11 +100,14 @@ def _capture(fn):
     return graph
 
 
-def _graph_per_launch(launch, count, replays=5):
+def _graph_per_launch(launch, count, replays=20, warmup_replays=2):
     """(mean, median) ms per launch of a graph of ``count`` back-to-back launches, timed
-    with events on the replay stream."""
+    with events on the replay stream, one replay at a time, after untimed replays."""
     graph = _capture(lambda: [launch(i) for i in range(count)])
     stream = torch.cuda.current_stream()
+    for _ in range(warmup_replays):
+        graph.replay()
+    torch.cuda.synchronize()
     times = []
     for _ in range(replays):
         start, end = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
