@@ -135,6 +135,38 @@ def _time_dominant(layers, launches_per_graph=24):
     return n, k, mean, med
 
 
+def _decode_batches(layers, device, batches=(4, 16, 32), steps=10):
+    """The Cfg2 decode step at M > 1 (W8A16 GEMM per projection, every layer's own
+    weights): one graph per step over the 32 layers, GB/s of algorithmic bytes."""
+    from ayaka.kernel.hip import fp8_weight_only_gemm
+
+    rows = {}
+    for m in batches:
+        xs = [wl.outlier_activations(m, k, device) for _, _, k, _, _ in layers]
+        outs = [torch.empty(m, n, dtype=torch.bfloat16, device=device) for _, n, _, _, _ in layers]
+
+        def step(m=m, xs=xs, outs=outs):
+            for layer in range(LAYERS):
+                for (name, n, k, copies, _), x, out in zip(layers, xs, outs):
+                    w, s = copies[layer % len(copies)]
+                    fp8_weight_only_gemm(x, w, s, 1, 1, k, "float32", out=out)
+
+        graph = _capture(step)
+        for _ in range(2):
+            graph.replay()
+        torch.cuda.synchronize()
+        t0 = time.perf_counter()
+        for _ in range(steps):
+            graph.replay()
+        torch.cuda.synchronize()
+        ms = (time.perf_counter() - t0) * 1e3 / steps
+        nbytes = LAYERS * sum(_gemv_bytes(n, k, m) for _, n, k, _, _ in layers)
+        rows[f"M{m}"] = {"ms_per_step": round(ms, 4), "GB/s": round(nbytes / (ms * 1e-3) / 1e9, 1),
+                         "frac": round(nbytes / (ms * 1e-3) / 1e9 / HBM_PEAK_GBS, 4)}
+        del graph
+    return rows
+
+
 def _cfg2_projections(layers, launches_per_graph=24):
     """Per-projection M = 1 launch time and GB/s of the Cfg2 step."""
     from ayaka.kernel.hip import fp8_weight_only_gemv
@@ -739,6 +771,7 @@ def main() -> int:
                      "avg_launch_us": round(avg_ms * 1e3, 2), "median_launch_us": round(med_ms * 1e3, 2),
                      "bytes_per_launch": _gemv_bytes(n, k), "traffic": _measured_traffic()},
         "cfg2_m1_projections": _cfg2_projections(layers),
+        "cfg2_decode_batches": _decode_batches(layers, device),
     }
     del layers, outs
     torch.cuda.empty_cache()
