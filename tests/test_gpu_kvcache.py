@@ -255,3 +255,47 @@ def test_gather_fp8_to_16bit_rows_of_16(gpu, cache_dtype, dest_dtype, n, heads, 
         ref = ora.kv_gather(cache, torch.where(valid, slots, 0), dest_dtype, scale, deq).reshape(n, heads, dim)
         ref[~valid] = 0  # the kernel's contract for slots outside the cache: a zero row
         assert _same(dest, ref), f"dequantize={deq}"
+
+
+def _kv_sweep_cases(n=24, seed=77):
+    import random
+
+    rng = random.Random(seed)
+    cases = []
+    for _ in range(n):
+        heads, dim = rng.choice([(1, 8), (2, 24), (8, 64), (4, 128), (3, 40), (1, 576)])
+        cases.append((rng.randint(1, 300), heads, dim, rng.choice([1, 8, 16, 32]),
+                      rng.choice(["bfloat16", "float16", "float32"]),
+                      rng.choice(["float8_e4m3fn", "float8_e5m2", "bfloat16", "float16"])))
+    return cases
+
+
+@pytest.mark.parametrize("n,heads,dim,page_size,src,cache", _kv_sweep_cases())
+def test_kv_cache_shape_sweep(gpu, n, heads, dim, page_size, src, cache):
+    """Seeded random token counts, head layouts, page sizes and dtype pairs: the write
+    (masked slots included) and the dequantizing gather, bit-exact against the oracle."""
+    from ayaka.kernel.hip import gather_cache, write_kv
+
+    _say(f"kv sweep n={n} heads={heads} dim={dim} page={page_size} src={src} cache={cache}")
+    src_dt, cache_dt = getattr(torch, src), getattr(torch, cache)
+    g = torch.Generator().manual_seed(n * 31 + heads * 7 + dim)
+    pages = -(-(n + 5) // page_size)
+    key, value = _source(n, heads, dim, src_dt, n + 1), _source(n, heads, dim, src_dt, n + 2)
+    slots = torch.randperm(pages * page_size, generator=g)[:n]
+    slots[3::7] = -1
+    k_cache = torch.full((pages, page_size, heads, dim), 0.25).to(cache_dt)
+    v_cache = torch.full((pages, page_size, heads, dim), -0.5).to(cache_dt)
+    k_ref, v_ref = k_cache.clone(), v_cache.clone()
+    ora.kv_write(key, k_ref, slots, 0.5)
+    ora.kv_write(value, v_ref, slots, 3.0)
+    kg, vg = k_cache.to(gpu), v_cache.to(gpu)
+    write_kv(key.to(gpu), value.to(gpu), kg, vg, slots.to(gpu), 0.5, 3.0)
+    assert _same(kg, k_ref), "key cache differs"
+    assert _same(vg, v_ref), "value cache differs"
+    read = torch.randint(0, pages * page_size, (n,), generator=g)
+    dest_dt = torch.bfloat16 if cache_dt.itemsize == 1 else cache_dt
+    dequant = cache_dt.itemsize == 1
+    dest = torch.empty(n, heads, dim, dtype=dest_dt, device=gpu)
+    gather_cache(kg, read.to(gpu), dest, 0.75 if dequant else 1.0, dequant)
+    ref = ora.kv_gather(k_ref, read, dest_dt, 0.75 if dequant else 1.0, dequant).reshape(n, heads, dim)
+    assert _same(dest, ref), "gather differs"
